@@ -1,0 +1,212 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized decode GEMV path on one MI355X.
+
+Workload: the decode-step GEMV set of one
+Qwen3.5-0.8B-shaped layer at batch 1 -- Q4_K gate and up (3584x1024),
+Q6_K down (1024x3584), Q5_K 2048x1024, 512x1024 and 1024x2048, Q8_0
+1024x1024 -- random blocks per the BASELINE recipe, activations already
+quantized (Q8_K / Q8_0) and resident in HBM. One step is one fused launch
+(hip_matvec_group) over the seven matrices. Steps rotate through enough
+distinct weight copies (> 512 MB) that every step streams its weights
+from HBM rather than the 256 MB MALL.
+
+metric: GB/s of algorithmic bytes (weights + quantized activations + fp32
+outputs, 11,560,856 B per step) over the timed steps.
+
+Also reported under "extra": config 0 (single Q4_K GEMV), config 2 (LM
+head with fused argmax / top-40), config 3 (prefill GEMM) when available.
+The CPU baseline times the reference's own tensor_matmul_* (oracle/_ref,
+compiled from its sources) on this host's cores over a bounded sample.
+"""
+import argparse
+import ctypes as C
+import importlib.util
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+CONFIG1 = [(12, 3584, 1024), (12, 3584, 1024), (14, 1024, 3584), (13, 2048, 1024),
+           (13, 512, 1024), (13, 1024, 2048), (8, 1024, 1024)]
+HBM_PEAK_GBS = 8000.0
+MALL_DEFEAT_BYTES = 512 << 20
+
+
+def _load(rel, name):
+    if name in sys.modules:
+        return sys.modules[name]
+    spec = importlib.util.spec_from_file_location(name, os.path.join(ROOT, rel))
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def alg_bytes(wtype, n, k):
+    bb = {8: 34, 12: 144, 13: 176, 14: 210}[wtype]
+    be = 32 if wtype == 8 else 256
+    xq = (k // 32) * 34 if wtype == 8 else (k // 256) * 292
+    return n * (k // be) * bb + xq + 4 * n
+
+
+class Events:
+    """HIP events on the stream the kernels run on."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def time(self, fn, steps, warmup):
+        torch = self.torch
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        s = torch.cuda.current_stream()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for i in range(steps):
+            fn(warmup + i)
+        e1.record(s)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3            # seconds
+
+
+def bench_config1(torch, qk, synth, lib, steps, warmup):
+    per_set = sum(alg_bytes(*s) for s in CONFIG1)
+    wbytes = sum(alg_bytes(*s) - ((s[2] // 32) * 34 if s[0] == 8 else (s[2] // 256) * 292) - 4 * s[1] for s in CONFIG1)
+    copies = max(2, -(-MALL_DEFEAT_BYTES // wbytes))
+    base = []
+    for i, (t, n, k) in enumerate(CONFIG1):
+        w = torch.from_numpy(synth.blocks(t, n, k, seed=0, tag=i)).cuda()
+        x = torch.from_numpy(synth.activations(1, k, seed=0, tag=i)).cuda()
+        xq = lib.quantize_for(t, x)[0]
+        base.append((t, w, n, k, xq))
+    sets = []
+    for c in range(copies):
+        items = []
+        for (t, w, n, k, xq) in base:
+            wc = w if c == 0 else w.clone()
+            items.append((t, wc, n, k, xq, torch.empty(n, dtype=torch.float32, device="cuda")))
+        sets.append(items)
+    descs = []
+    for items in sets:
+        arr = (qk.GemvDesc * len(items))()
+        for i, (t, w, n, k, xq, y) in enumerate(items):
+            arr[i] = qk.GemvDesc(t, 0, n, k, w.data_ptr(), xq.data_ptr(), y.data_ptr())
+        descs.append(arr)
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def step(i):
+        rc = lib.L.hip_matvec_group(descs[i % copies], len(CONFIG1), stream)
+        if rc:
+            raise RuntimeError(lib.last_error())
+
+    secs = Events(torch).time(step, steps, warmup)
+    return per_set, copies, secs
+
+
+def bench_config0(torch, qk, synth, lib, steps, warmup):
+    t, n, k = 12, 3584, 1024
+    per = alg_bytes(t, n, k)
+    copies = -(-MALL_DEFEAT_BYTES // (per - 292 * 4 - 4 * n))
+    w = torch.from_numpy(synth.blocks(t, n, k, seed=0)).cuda()
+    ws = [w] + [w.clone() for _ in range(copies - 1)]
+    xq = lib.quantize_q8k(torch.from_numpy(synth.activations(1, k, seed=0)).cuda())[0]
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    secs = Events(torch).time(lambda i: lib.matvec(t, ws[i % copies], n, k, xq, y), steps, warmup)
+    return per, copies, secs
+
+
+def bench_config2(torch, qk, synth, lib, steps, warmup):
+    n, k, topk = 248320, 1024, 40
+    w = torch.from_numpy(synth.blocks(14, n, k, seed=0)).cuda()
+    copies = 3                                        # 3 x 209 MB > 512 MB
+    ws = [w] + [w.clone() for _ in range(copies - 1)]
+    xq = lib.quantize_q8k(torch.from_numpy(synth.activations(1, k, seed=0)).cuda())[0]
+    logits = torch.empty(n, dtype=torch.float32, device="cuda")
+    per = n * 4 * 210 + 4 * 292 + 4 * n
+    secs = Events(torch).time(lambda i: lib.lmhead(ws[i % copies], n, k, xq, topk=topk, logits=logits),
+                              steps, warmup)
+    return per, copies, secs
+
+
+def cpu_baseline(synth, seconds=10.0):
+    """The reference's tensor_matmul_*_f32 (one core, as shipped) over the
+    config-1 set, repeated for a bounded time."""
+    oracle = _load("oracle/oracle.py", "qk_oracle_py")
+    if oracle.Ref.available():
+        R = oracle.Ref()
+        kind, label = "reference", R.label()
+        run = lambda t, w, n, k, x: R.matmul(t, w, n, k, x)
+    else:
+        R = oracle.Oracle()
+        kind, label = "port", "oracle restatement"
+        run = lambda t, w, n, k, x: R.matmul(t, w, n, k, x, oracle.EPI_FUSED, threads=1)
+    mats = [(t, synth.blocks(t, n, k, seed=0, tag=i), n, k, synth.activations(1, k, seed=0, tag=i))
+            for i, (t, n, k) in enumerate(CONFIG1)]
+    per_set = sum(alg_bytes(t, n, k) for (t, n, k) in CONFIG1)
+    reps = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for (t, w, n, k, x) in mats:
+            run(t, w, n, k, x)
+        reps += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(per_set * reps / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{reps} passes of the config-1 GEMV set (7 matrices, fp32 x quantized per call) "
+                      f"through tensor_matmul_*_f32, {dt:.1f} s, dispatch {label}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU: the quantized GEMV path runs on a single MI355X "
+              f"(--gpus {a.gpus} is not supported)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    qk = _load("qwen.haiku_amd/qk.py", "qk_binding")
+    synth = _load("qwen.haiku_amd/synth.py", "qk_synth")
+    lib = qk.QK().init(0)
+
+    per, copies, secs = bench_config1(torch, qk, synth, lib, a.steps, a.warmup)
+    gbs = per * a.steps / secs / 1e9
+    us = secs / a.steps * 1e6
+    out = {
+        "metric": "k-quant GEMV GB/s (decode-step GEMV set, config 1)",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(us / 1e3, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8xq4/q5/q6/q8 (int32 acc, fp32 epilogue)", "data": "synthetic",
+        "config": {"workload": "config1 decode GEMV set: Q4_K 3584x1024 x2, Q6_K 1024x3584, "
+                               "Q5_K 2048x1024/512x1024/1024x2048, Q8_0 1024x1024, batch 1",
+                   "weight_copies": copies, "bytes_per_step": per, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_gemv<true> (one launch per step)", "us_per_launch": round(us, 3)},
+        "tier": lib.tier_label(),
+    }
+    if not a.no_extra:
+        extra = {}
+        p0, c0, s0 = bench_config0(torch, qk, synth, lib, a.steps, a.warmup)
+        extra["config0_q4k_gemv"] = {"GB/s": round(p0 * a.steps / s0 / 1e9, 2),
+                                     "us_per_launch": round(s0 / a.steps * 1e6, 3), "copies": c0}
+        st2 = max(20, a.steps // 20)
+        p2, c2, s2 = bench_config2(torch, qk, synth, lib, st2, 5)
+        extra["config2_lmhead_q6k_argmax_top40"] = {"GB/s": round(p2 * st2 / s2 / 1e9, 2),
+                                                    "us_per_call": round(s2 / st2 * 1e6, 3), "copies": c2}
+        out["extra"] = extra
+    if not a.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(synth, a.cpu_seconds)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,242 @@
+/*
+ * qk.h -- C ABI of libqk, the MI355X (gfx950) quantized matmul path.
+ *
+ * libqk replaces the CPU SIMD dispatch behind qwen.haiku's quantized
+ * tensor ops: GGUF Q4_K / Q5_K / Q6_K / Q8_0 weight rows multiplied
+ * against activations quantized to Q8_K (Q8_0 for Q8_0 weights).
+ * Every entry point is `extern "C"`, takes plain pointers and sizes, and
+ * returns an int status (QK_OK == 0). On failure hip_qk_last_error()
+ * returns a message for the calling thread.
+ *
+ * Two layers:
+ *
+ *  1. Device layer (hip_quantize_*, hip_matvec_*, hip_matmul_*,
+ *     hip_dequant_*, hip_lmhead_*): every pointer is a device pointer;
+ *     work is enqueued on `stream` (a hipStream_t, NULL = the null
+ *     stream) and the call returns without synchronizing.
+ *  2. Host seam (hip_qk_register_weight, hip_qk_matmul_host,
+ *     hip_qk_lmhead_host): host pointers, synchronous. This is the body
+ *     of the reference's tensor_matmul_*_f32 (slm/tensor.c:827-1033)
+ *     moved onto the GPU; weights are uploaded once and found again by
+ *     their host address, so the reference's call signatures need no
+ *     change (qwen.haiku_amd/host/qk_tensor_seam.h).
+ *
+ * Results are bit-identical to the reference CPU path of the selected
+ * tier (hip_qk_set_tier): the integer part of every row dot is exact,
+ * and the float epilogue reproduces the rounding sequence of that tier.
+ */
+#ifndef QK_H
+#define QK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Super-block / block sizes, simd/quants.h:30-31. */
+#define QK_K  256
+#define QK8_0 32
+
+/* GGUF tensor type ids, slm/gguf.c:52-59. */
+enum {
+    QK_TYPE_F32  = 0,
+    QK_TYPE_Q8_0 = 8,
+    QK_TYPE_Q4_K = 12,
+    QK_TYPE_Q5_K = 13,
+    QK_TYPE_Q6_K = 14
+};
+
+/* Block layouts, byte-identical to simd/quants.h:95-130. fp16 fields are
+ * carried as raw IEEE binary16 bits. */
+typedef struct {
+    float   d;                 /* 1 / iscale                        */
+    int8_t  qs[QK_K];          /* 256 quants                        */
+    int16_t bsums[QK_K / 16];  /* sums of 16-element groups         */
+} qk_q8k_block;                /* 292 B                             */
+
+typedef struct {
+    uint16_t d, dmin;          /* fp16                              */
+    uint8_t  scales[12];       /* 8 x (6-bit scale, 6-bit min)      */
+    uint8_t  qs[QK_K / 2];     /* 4-bit quants                      */
+} qk_q4k_block;                /* 144 B                             */
+
+typedef struct {
+    uint16_t d, dmin;
+    uint8_t  scales[12];
+    uint8_t  qh[QK_K / 8];     /* 5th bit                           */
+    uint8_t  qs[QK_K / 2];
+} qk_q5k_block;                /* 176 B                             */
+
+typedef struct {
+    uint8_t  ql[QK_K / 2];     /* low 4 bits                        */
+    uint8_t  qh[QK_K / 4];     /* high 2 bits                       */
+    int8_t   scales[QK_K / 16];
+    uint16_t d;                /* fp16                              */
+} qk_q6k_block;                /* 210 B                             */
+
+typedef struct {
+    uint16_t d;                /* fp16                              */
+    int8_t   qs[QK8_0];
+} qk_q8_0_block;               /* 34 B                              */
+
+/* Status codes. */
+enum {
+    QK_OK               = 0,
+    QK_ERR_ARG          = 1,   /* bad shape, null pointer, k % block   */
+    QK_ERR_HIP          = 2,   /* a HIP runtime call failed            */
+    QK_ERR_NOT_INIT     = 3,   /* hip_qk_init not called / failed      */
+    QK_ERR_UNREGISTERED = 4,   /* host weight pointer not registered   */
+    QK_ERR_NOMEM        = 5,
+    QK_ERR_UNSUPPORTED  = 6    /* tensor type not on this path         */
+};
+
+/* CPU dispatch tiers whose float epilogue the kernels reproduce
+ * (simd/simd.c:208-229). SCALAR and AVX1 round every product and
+ * difference separately; AVX2 and AVX-VNNI fuse d*isum - dmin*mins into
+ * one FMA (Q4_K/Q5_K) and reduce Q8_0 over 8 FMA lanes. */
+enum {
+    QK_TIER_AUTO    = -1,      /* pick the tier this host CPU runs     */
+    QK_TIER_SCALAR  = 0,
+    QK_TIER_AVX1    = 1,
+    QK_TIER_AVX2    = 2,
+    QK_TIER_AVXVNNI = 3
+};
+
+/* ---- lifecycle ------------------------------------------------------ */
+
+/* Select `device`, pick the tier (QK_TIER_AUTO) and create the library's
+ * stream. Replaces simd_init() (simd/simd.c:191), called from
+ * slm_model_load (slm/model.c:1134). Idempotent. */
+int         hip_qk_init(int device);
+/* Free every registered weight and the stream. */
+void        hip_qk_shutdown(void);
+/* "gfx950 <name> / tier AVX2-FMA"; replaces simd_dispatch_label()
+ * (simd/simd.c:234). */
+const char *hip_qk_device_label(void);
+/* Message of the last failed call on this thread ("" if none). */
+const char *hip_qk_last_error(void);
+/* Force a tier (QK_TIER_*); QK_TIER_AUTO re-detects from CPUID the way
+ * detect_cpu() does (simd/simd.c:142-170). */
+int         hip_qk_set_tier(int tier);
+int         hip_qk_get_tier(void);
+/* Tier name as the reference labels it: "scalar", "AVX1", "AVX2-FMA",
+ * "AVX-VNNI". */
+const char *hip_qk_tier_label(int tier);
+
+/* ---- device layer: activation quantizers --------------------------- */
+
+/* m rows of k floats -> m * k/256 Q8_K blocks (row t at xq + t*k/256).
+ * Bit-exact quantize_row_q8_K (slm/tensor.c:683-720). k % 256 == 0. */
+int hip_quantize_q8k(const float *x, int64_t m, int64_t k, void *xq,
+                     void *stream);
+/* m rows of k floats -> m * k/32 Q8_0 blocks. Bit-exact
+ * tensor_quantize_row_q8_0 (slm/tensor.c:930-950; roundf, half away
+ * from zero). k % 32 == 0. */
+int hip_quantize_q8_0(const float *x, int64_t m, int64_t k, void *xq,
+                      void *stream);
+
+/* ---- device layer: decode GEMV (one activation row) ----------------- */
+
+/* y[j] = row_dot(W row j, xq) for j < n. W is n rows of k/256 blocks in
+ * native GGUF layout; xq is k/256 Q8_K blocks (k/32 Q8_0 blocks for
+ * hip_matvec_q8_0). Replaces the LLM_PAR_FOR row loop of
+ * tensor_matmul_q{4k,5k,6k}_f32 / _q8_0_f32 at n_tok == 1
+ * (slm/tensor.c:846-850, 912-917, 1026-1031, 974-979) and the
+ * simd_q*_row_dot entry points it calls (simd/simd.c:236-250). */
+int hip_matvec_q4k (const void *w, int64_t n, int64_t k, const void *xq,
+                    float *y, void *stream);
+int hip_matvec_q5k (const void *w, int64_t n, int64_t k, const void *xq,
+                    float *y, void *stream);
+int hip_matvec_q6k (const void *w, int64_t n, int64_t k, const void *xq,
+                    float *y, void *stream);
+int hip_matvec_q8_0(const void *w, int64_t n, int64_t k, const void *xq,
+                    float *y, void *stream);
+
+/* One launch over several GEMVs (a decode layer's projections): entry i
+ * computes y_i = W_i . xq_i as hip_matvec_<type_i> would. Descriptors
+ * live in host memory and are copied into the launch's kernel
+ * arguments; at most QK_GROUP_MAX entries. */
+#define QK_GROUP_MAX 16
+typedef struct {
+    int32_t     type;          /* QK_TYPE_Q4_K / Q5_K / Q6_K / Q8_0   */
+    int32_t     pad_;
+    int64_t     n, k;
+    const void *w;             /* device                              */
+    const void *xq;            /* device                              */
+    float      *y;             /* device                              */
+} qk_gemv_desc;
+int hip_matvec_group(const qk_gemv_desc *desc, int count, void *stream);
+
+/* ---- device layer: chunked-prefill GEMM ----------------------------- */
+
+/* y[t*n + j] = row_dot(W row j, xq row t) for t < m, j < n: the token
+ * loop of tensor_matmul_q{4k,5k,6k}_f32 (slm/tensor.c:838-851) as one
+ * int8-MFMA GEMM. xq holds m rows of k/256 Q8_K blocks. */
+int hip_matmul_q4k(const void *w, int64_t n, int64_t k, const void *xq,
+                   int64_t m, float *y, void *stream);
+int hip_matmul_q5k(const void *w, int64_t n, int64_t k, const void *xq,
+                   int64_t m, float *y, void *stream);
+int hip_matmul_q6k(const void *w, int64_t n, int64_t k, const void *xq,
+                   int64_t m, float *y, void *stream);
+
+/* ---- device layer: dequantization ----------------------------------- */
+
+/* nblocks blocks -> nblocks*256 floats. Bit-exact q{4,5,6}k_dequant_block
+ * (slm/tensor.c:800-820, 867-896, 988-1010). */
+int hip_dequant_q4k(const void *w, int64_t nblocks, float *y, void *stream);
+int hip_dequant_q5k(const void *w, int64_t nblocks, float *y, void *stream);
+int hip_dequant_q6k(const void *w, int64_t nblocks, float *y, void *stream);
+
+/* ---- device layer: LM head ------------------------------------------ */
+
+/* Q6_K GEMV over n vocabulary rows fused with the greedy pick and a
+ * top-k gather:
+ *   logits (optional, may be NULL): n floats, as hip_matvec_q6k;
+ *   *argmax: first index of the maximum logit (sample_argmax,
+ *            slm/model.c:401-412: strict '>', NaN never wins);
+ *   topk_idx/topk_val (optional when topk == 0): the topk largest
+ *            logits, value-descending, ties broken by lower index; the
+ *            set equals topk_collect's (slm/sampler.c:70-93) whenever
+ *            the topk-th value is not tied.
+ * 1 <= topk <= QK_TOPK_MAX. All outputs are device pointers. */
+#define QK_TOPK_MAX 256
+int hip_lmhead_q6k_argmax_topk(const void *w, int64_t n, int64_t k,
+                               const void *xq, int topk, float *logits,
+                               int32_t *argmax, int32_t *topk_idx,
+                               float *topk_val, void *stream);
+
+/* ---- host seam ------------------------------------------------------ */
+
+/* Upload the n x k weight matrix at host address `host_w` (GGUF type
+ * `type`) once; later host-seam calls with the same address use the
+ * device copy. Weights are immutable after load (slm/slm.h:12-13), so
+ * re-registering an address is a no-op. Thread-safe. */
+int hip_qk_register_weight(const void *host_w, int type, int64_t k,
+                           int64_t n);
+int hip_qk_unregister_weight(const void *host_w);
+/* Device address of a registered weight (NULL if unknown). */
+const void *hip_qk_device_weight(const void *host_w);
+
+/* out[t*out_f + j] = row_dot(W row j, quant(x row t)): exactly what
+ * tensor_matmul_q4k_f32 / _q5k_ / _q6k_ / _q8_0_ compute
+ * (slm/tensor.c:827, 898, 1012, 952), for x of n_tok rows of k floats
+ * in host memory and out in host memory. Registers the weight on first
+ * use. Synchronous. */
+int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f,
+                       int64_t k, const float *x, int64_t n_tok,
+                       float *out);
+/* LM head: matmul_dispatch(&W.output, h) (slm/qwen.c:976) followed by
+ * sample_argmax (slm/model.c:401). logits (n floats) may be NULL when
+ * only the token is needed; topk may be 0. Host pointers. */
+int hip_qk_lmhead_host(const void *host_w, int64_t n, int64_t k,
+                       const float *x, int topk, float *logits,
+                       int32_t *argmax, int32_t *topk_idx,
+                       float *topk_val);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QK_H */

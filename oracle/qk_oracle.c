@@ -1,0 +1,503 @@
+/*
+ * qk_oracle.c -- CPU restatement of qwen.haiku's quantized matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see qk_oracle.h). Each function names the
+ * reference lines it restates. The oracle is pinned three ways in
+ * tests/test_oracle.py: against the reference compiled from its own
+ * sources (oracle/_ref, when present), against the committed golden
+ * vectors under tests/golden/, and against closed forms (exhaustive
+ * fp16, brute-force int64 dots, scale-unpack round trips, quantizer
+ * invariants).
+ */
+#include "qk_oracle.h"
+
+#include <math.h>
+#include <stddef.h>
+#include <string.h>
+
+#define QK_K  256
+#define QK8_0 32
+
+/* Block layouts: simd/quants.h:95-130 (fp16 fields as raw bits). */
+typedef struct { float d; int8_t qs[QK_K]; int16_t bsums[QK_K / 16]; } o_q8k;
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[QK_K / 2]; } o_q4k;
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[QK_K / 8]; uint8_t qs[QK_K / 2]; } o_q5k;
+typedef struct { uint8_t ql[QK_K / 2]; uint8_t qh[QK_K / 4]; int8_t scales[QK_K / 16]; uint16_t d; } o_q6k;
+typedef struct { uint16_t d; int8_t qs[QK8_0]; } o_q8_0;
+
+typedef char o_sz_q8k[sizeof(o_q8k) == 292 ? 1 : -1];
+typedef char o_sz_q4k[sizeof(o_q4k) == 144 ? 1 : -1];
+typedef char o_sz_q5k[sizeof(o_q5k) == 176 ? 1 : -1];
+typedef char o_sz_q6k[sizeof(o_q6k) == 210 ? 1 : -1];
+typedef char o_sz_q80[sizeof(o_q8_0) == 34 ? 1 : -1];
+
+static uint32_t fbits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static float    bitsf(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* simd/quants.h:50-53: with clang, q_fp16_to_f32 is a `_Float16` cast,
+ * i.e. exact IEEE binary16 -> binary32 widening (subnormals kept). */
+float qko_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    float r;
+    if (e == 0) {
+        r = (float)m * 0x1p-24f;                       /* exact */
+        r = sign ? -r : r;
+    } else if (e == 31) {
+        r = bitsf(sign | 0x7f800000u | (m << 13));
+    } else {
+        r = bitsf(sign | ((e + 112u) << 23) | (m << 13));
+    }
+    return r;
+}
+
+/* simd/quants.h:53 and slm/tensor.c:940 (`(_Float16)d`): IEEE
+ * binary32 -> binary16, round to nearest even, overflow to inf. */
+uint16_t qko_f32_to_f16(float f) {
+    uint32_t x = fbits(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    uint32_t q;
+    if (ax > 0x7f800000u) {                            /* NaN: quiet  */
+        q = 0x7e00u | ((ax >> 13) & 0x3ffu);
+    } else if (ax >= 0x477ff000u) {                    /* >= 65520    */
+        q = 0x7c00u;
+    } else if (ax >= 0x38800000u) {                    /* fp16 normal */
+        uint32_t rem = ax & 0x1fffu;
+        q = (((ax >> 23) - 112u) << 10) | ((ax >> 13) & 0x3ffu);
+        if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q += 1;
+    } else if (ax <= 0x33000000u) {                    /* <= 2^-25    */
+        q = 0;
+    } else {                                           /* subnormal   */
+        uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        uint32_t shift = 126u - (ax >> 23);            /* 14..24      */
+        uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        q = m >> shift;
+        if (rem > half || (rem == half && (q & 1u))) q += 1;
+    }
+    return (uint16_t)(sign | q);
+}
+
+/* simd/quants.h:137-142, slm/tensor.c:673-678: magic-number rounding,
+ * half to even for |v| < 2^22. The add is a separate rounding. */
+int32_t qko_nearest_int(float v) {
+    volatile float t = v + 12582912.f;
+    int32_t i;
+    float tt = t;
+    memcpy(&i, &tt, 4);
+    return (i & 0x007fffff) - 0x00400000;
+}
+
+/* slm/tensor.c:683-720 (= simd/quants.h:156-186). */
+void qko_quantize_q8k(const float *x, void *xq, int64_t k) {
+    o_q8k *y = (o_q8k *)xq;
+    for (int64_t b = 0; b < k / QK_K; b++) {
+        const float *s = x + b * QK_K;
+        float amax = 0.0f, xmax = 0.0f;
+        for (int i = 0; i < QK_K; i++) {
+            float ax = fabsf(s[i]);
+            if (ax > amax) { amax = ax; xmax = s[i]; }
+        }
+        if (amax == 0.0f) {
+            y[b].d = 0.0f;
+            memset(y[b].qs, 0, sizeof(y[b].qs));
+            memset(y[b].bsums, 0, sizeof(y[b].bsums));
+        } else {
+            float iscale = -127.0f / xmax;
+            y[b].d = 1.0f / iscale;
+            for (int i = 0; i < QK_K; i++) {
+                int32_t v = qko_nearest_int(iscale * s[i]);
+                if (v > 127) v = 127;
+                if (v < -128) v = -128;
+                y[b].qs[i] = (int8_t)v;
+            }
+            for (int j = 0; j < QK_K / 16; j++) {
+                int32_t acc = 0;
+                for (int l = 0; l < 16; l++) acc += y[b].qs[j * 16 + l];
+                y[b].bsums[j] = (int16_t)acc;
+            }
+        }
+    }
+}
+
+/* slm/tensor.c:930-950: amax/127, reciprocal of the unrounded d,
+ * roundf (half away from zero), d stored as fp16 RNE, clamp to int8. */
+void qko_quantize_q8_0(const float *x, void *xq, int64_t k) {
+    o_q8_0 *y = (o_q8_0 *)xq;
+    for (int64_t i = 0; i < k / QK8_0; i++) {
+        float amax = 0.0f;
+        for (int j = 0; j < QK8_0; j++) {
+            float v = fabsf(x[i * QK8_0 + j]);
+            if (v > amax) amax = v;
+        }
+        float d = amax / 127.0f;
+        float id = (d != 0.0f) ? (1.0f / d) : 0.0f;
+        y[i].d = qko_f32_to_f16(d);
+        for (int j = 0; j < QK8_0; j++) {
+            /* (int32_t)roundf() of a value outside int32 is undefined in
+             * C; the reference as compiled (clang -O3) saturates, which
+             * shows when d underflows and id = 1/d is inf. */
+            float r = roundf(x[i * QK8_0 + j] * id);
+            int32_t q = r >= 127.0f ? 127 : (r <= -128.0f ? -128 : (int32_t)r);
+            y[i].qs[j] = (int8_t)q;
+        }
+    }
+}
+
+/* simd/quants.h:215-224. */
+void qko_scale_min(const uint8_t *s, int j, uint8_t *sc, uint8_t *m) {
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *m  = s[j + 4] & 63;
+    } else {
+        *sc = (uint8_t)((s[j + 4] & 0x0f) | ((s[j - 4] >> 6) << 4));
+        *m  = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+    }
+}
+
+/* Integer part of Q4_K . Q8_K for one super-block, simd/quants.h:
+ * 283-304 (isum over 4 chunks of 64: low nibbles of qs[32c..] with
+ * q8[64c..], high nibbles with q8[64c+32..]; isum_mins from bsum
+ * pairs). */
+void qko_q4k_block_ints(const void *wv, const void *xv, int32_t *isum,
+                        int32_t *isum_mins) {
+    const o_q4k *w = (const o_q4k *)wv;
+    const o_q8k *y = (const o_q8k *)xv;
+    uint8_t sc[8], mn[8];
+    for (int j = 0; j < 8; j++) qko_scale_min(w->scales, j, &sc[j], &mn[j]);
+    int32_t mins = 0;
+    for (int j = 0; j < 8; j++)
+        mins += ((int32_t)y->bsums[2 * j] + y->bsums[2 * j + 1]) * mn[j];
+    int32_t acc = 0;
+    for (int c = 0; c < 4; c++) {
+        int32_t s1 = 0, s2 = 0;
+        for (int l = 0; l < 32; l++) {
+            s1 += (w->qs[32 * c + l] & 0x0f) * (int32_t)y->qs[64 * c + l];
+            s2 += (w->qs[32 * c + l] >> 4) * (int32_t)y->qs[64 * c + 32 + l];
+        }
+        acc += s1 * sc[2 * c] + s2 * sc[2 * c + 1];
+    }
+    *isum = acc;
+    *isum_mins = mins;
+}
+
+/* simd/quants.h:324-349: the 5th bit of element l of chunk c is bit 2c
+ * (low half) / 2c+1 (high half) of qh[l]. */
+void qko_q5k_block_ints(const void *wv, const void *xv, int32_t *isum,
+                        int32_t *isum_mins) {
+    const o_q5k *w = (const o_q5k *)wv;
+    const o_q8k *y = (const o_q8k *)xv;
+    uint8_t sc[8], mn[8];
+    for (int j = 0; j < 8; j++) qko_scale_min(w->scales, j, &sc[j], &mn[j]);
+    int32_t mins = 0;
+    for (int j = 0; j < 8; j++)
+        mins += ((int32_t)y->bsums[2 * j] + y->bsums[2 * j + 1]) * mn[j];
+    int32_t acc = 0;
+    for (int c = 0; c < 4; c++) {
+        int32_t s1 = 0, s2 = 0;
+        for (int l = 0; l < 32; l++) {
+            int32_t lo = (w->qs[32 * c + l] & 0x0f) + (((w->qh[l] >> (2 * c)) & 1) << 4);
+            int32_t hi = (w->qs[32 * c + l] >> 4) + (((w->qh[l] >> (2 * c + 1)) & 1) << 4);
+            s1 += lo * (int32_t)y->qs[64 * c + l];
+            s2 += hi * (int32_t)y->qs[64 * c + 32 + l];
+        }
+        acc += s1 * sc[2 * c] + s2 * sc[2 * c + 1];
+    }
+    *isum = acc;
+    *isum_mins = mins;
+}
+
+/* Raw 6-bit weight of element e (0..255) of a Q6_K block, the index map
+ * of simd/quants.h:370-394 / slm/tensor.c:994-1003: half h = e/128,
+ * within it position p = e%128, quarter q = p/32, l = p%32; low nibble
+ * from ql[64h + l + 32*(q&1)] (>>4 when q >= 2), high pair from
+ * qh[32h + l] bits 2q..2q+1. */
+static int32_t q6_raw(const o_q6k *w, int e) {
+    int h = e / 128, p = e % 128, q = p / 32, l = p % 32;
+    uint8_t lb = w->ql[64 * h + l + 32 * (q & 1)];
+    int32_t lo = (q >= 2) ? (lb >> 4) : (lb & 0x0f);
+    int32_t hi = (w->qh[32 * h + l] >> (2 * q)) & 3;
+    return lo | (hi << 4);
+}
+
+/* simd/quants.h:359-399: isum over 16 sub-blocks of 16 with signed
+ * scales, isum_mins = sum bsums[s]*scales[s]. */
+void qko_q6k_block_ints(const void *wv, const void *xv, int32_t *isum,
+                        int32_t *isum_mins) {
+    const o_q6k *w = (const o_q6k *)wv;
+    const o_q8k *y = (const o_q8k *)xv;
+    int32_t mins = 0, acc = 0;
+    for (int s = 0; s < 16; s++) mins += (int32_t)y->bsums[s] * w->scales[s];
+    for (int s = 0; s < 16; s++) {
+        int32_t part = 0;
+        for (int l = 0; l < 16; l++)
+            part += q6_raw(w, 16 * s + l) * (int32_t)y->qs[16 * s + l];
+        acc += part * w->scales[s];
+    }
+    *isum = acc;
+    *isum_mins = mins;
+}
+
+/* Float epilogue of Q4_K/Q5_K per super-block.
+ * separate: simd/quants.h:305 and simd/avx.c:654 (AVX1), no FMA:
+ *           rn(rn(d*isum) - rn(dmin*mins));
+ * fused:    simd/avx.c:229,466,515 (AVX2/VNNI), contracted by clang to
+ *           fma(d, isum, -rn(dmin*mins)).
+ * d = rn(y.d * fp16(x.d)), dmin = rn(y.d * fp16(x.dmin)). */
+static float k_term(float yd, uint16_t xd, uint16_t xdmin, int32_t isum,
+                    int32_t mins, int epi) {
+    float d = yd * qko_f16_to_f32(xd);
+    float dmin = yd * qko_f16_to_f32(xdmin);
+    float fi = (float)isum, fm = (float)mins;
+    float t;
+    if (epi == QKO_EPI_FUSED) {
+        volatile float pm = dmin * fm;
+        t = fmaf(d, fi, -pm);
+    } else {
+        volatile float a = d * fi;
+        volatile float b = dmin * fm;
+        t = a - b;
+    }
+    return t;
+}
+
+/* simd/avx.c:231-240 (and :300,:405,:467,:516,:587): the AVX2/VNNI
+ * kernels accumulate the row sum broadcast in 8 lanes and return
+ * hsum(8 lanes) / 8, i.e. ((s+s)+(s+s))+((s+s)+(s+s)) / 8. That equals s
+ * unless 8s overflows, in which case it is +-inf. */
+static float avx_bcast_sum(float s) {
+    volatile float s2 = s + s;
+    volatile float s4 = s2 + s2;
+    volatile float s8 = s4 + s4;
+    return s8 / 8.0f;
+}
+
+/* simd/quants.h:267-306 (separate) / simd/avx.c:420-468 (fused): the
+ * row sum starts at 0 and adds one term per super-block in order (the
+ * AVX2/VNNI 8-lane broadcast and /8 are exact). */
+float qko_q4k_dot(int nb, const void *wv, const void *xv, int epi) {
+    const o_q4k *w = (const o_q4k *)wv;
+    const o_q8k *y = (const o_q8k *)xv;
+    float sum = 0.0f;
+    for (int i = 0; i < nb; i++) {
+        int32_t is, im;
+        qko_q4k_block_ints(&w[i], &y[i], &is, &im);
+        sum += k_term(y[i].d, w[i].d, w[i].dmin, is, im, epi);
+    }
+    return epi == QKO_EPI_FUSED ? avx_bcast_sum(sum) : sum;
+}
+
+/* simd/quants.h:310-351 / simd/avx.c:470-523. */
+float qko_q5k_dot(int nb, const void *wv, const void *xv, int epi) {
+    const o_q5k *w = (const o_q5k *)wv;
+    const o_q8k *y = (const o_q8k *)xv;
+    float sum = 0.0f;
+    for (int i = 0; i < nb; i++) {
+        int32_t is, im;
+        qko_q5k_block_ints(&w[i], &y[i], &is, &im);
+        sum += k_term(y[i].d, w[i].d, w[i].dmin, is, im, epi);
+    }
+    return epi == QKO_EPI_FUSED ? avx_bcast_sum(sum) : sum;
+}
+
+/* simd/quants.h:399 and simd/avx.c:404,586,827: every tier computes
+ * rn(rn(fp16(x.d) * y.d) * (float)(isum - 32*isum_mins)) per block and
+ * sums in block order; AVX2/VNNI return it through the 8-lane broadcast. */
+float qko_q6k_dot(int nb, const void *wv, const void *xv, int epi) {
+    const o_q6k *w = (const o_q6k *)wv;
+    const o_q8k *y = (const o_q8k *)xv;
+    float sum = 0.0f;
+    for (int i = 0; i < nb; i++) {
+        int32_t is, im;
+        qko_q6k_block_ints(&w[i], &y[i], &is, &im);
+        volatile float s = qko_f16_to_f32(w[i].d) * y[i].d;
+        volatile float t = s * (float)(is - 32 * im);
+        sum += t;
+    }
+    return epi == QKO_EPI_FUSED ? avx_bcast_sum(sum) : sum;
+}
+
+/* separate: simd/quants.h:244-256 and simd/avx.c:136-158:
+ *   sum += (float)sumi * rn(fp16(x.d)*fp16(y.d)) per block.
+ * fused: simd/avx.c:65-123: lane l (l < 8) accumulates
+ *   acc_l = fma((float)p_l, s_b, acc_l), p_l the 4-byte partial dot of
+ *   bytes 4l..4l+3 of block b, then the reduction tree
+ *   ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)). */
+float qko_q8_0_dot(int64_t k, const void *wv, const void *xv, int epi) {
+    const o_q8_0 *x = (const o_q8_0 *)wv;
+    const o_q8_0 *y = (const o_q8_0 *)xv;
+    int64_t nb = k / QK8_0;
+    float r;
+    if (epi == QKO_EPI_FUSED) {
+        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int64_t i = 0; i < nb; i++) {
+            volatile float s = qko_f16_to_f32(x[i].d) * qko_f16_to_f32(y[i].d);
+            for (int l = 0; l < 8; l++) {
+                int32_t p = 0;
+                for (int b = 0; b < 4; b++)
+                    p += (int32_t)x[i].qs[4 * l + b] * y[i].qs[4 * l + b];
+                acc[l] = fmaf((float)p, s, acc[l]);
+            }
+        }
+        volatile float s04 = acc[0] + acc[4], s15 = acc[1] + acc[5];
+        volatile float s26 = acc[2] + acc[6], s37 = acc[3] + acc[7];
+        volatile float lo = s04 + s15, hi = s26 + s37;
+        r = lo + hi;
+    } else {
+        float sum = 0.0f;
+        for (int64_t i = 0; i < nb; i++) {
+            int32_t p = 0;
+            for (int j = 0; j < QK8_0; j++) p += (int32_t)x[i].qs[j] * y[i].qs[j];
+            volatile float s = qko_f16_to_f32(x[i].d) * qko_f16_to_f32(y[i].d);
+            volatile float t = (float)p * s;
+            sum += t;
+        }
+        r = sum;
+    }
+    return r;
+}
+
+/* slm/tensor.c:800-820: y = rn(rn(d1*q) - m1), d1 = rn(d*sc),
+ * m1 = rn(dmin*m). The x86 host build has no FMA to contract into. */
+void qko_dequant_q4k(const void *wv, int64_t nblocks, float *out) {
+    const o_q4k *w = (const o_q4k *)wv;
+    for (int64_t b = 0; b < nblocks; b++) {
+        const float d = qko_f16_to_f32(w[b].d), mn = qko_f16_to_f32(w[b].dmin);
+        float *y = out + b * QK_K;
+        for (int c = 0; c < 4; c++) {
+            uint8_t sc, m;
+            qko_scale_min(w[b].scales, 2 * c, &sc, &m);
+            volatile float d1 = d * (float)sc, m1 = mn * (float)m;
+            qko_scale_min(w[b].scales, 2 * c + 1, &sc, &m);
+            volatile float d2 = d * (float)sc, m2 = mn * (float)m;
+            for (int l = 0; l < 32; l++) {
+                volatile float a = d1 * (float)(w[b].qs[32 * c + l] & 0x0f);
+                volatile float e = d2 * (float)(w[b].qs[32 * c + l] >> 4);
+                y[64 * c + l] = a - m1;
+                y[64 * c + 32 + l] = e - m2;
+            }
+        }
+    }
+}
+
+/* slm/tensor.c:867-896. */
+void qko_dequant_q5k(const void *wv, int64_t nblocks, float *out) {
+    const o_q5k *w = (const o_q5k *)wv;
+    for (int64_t b = 0; b < nblocks; b++) {
+        const float d = qko_f16_to_f32(w[b].d), mn = qko_f16_to_f32(w[b].dmin);
+        float *y = out + b * QK_K;
+        for (int c = 0; c < 4; c++) {
+            uint8_t sc, m;
+            qko_scale_min(w[b].scales, 2 * c, &sc, &m);
+            volatile float d1 = d * (float)sc, m1 = mn * (float)m;
+            qko_scale_min(w[b].scales, 2 * c + 1, &sc, &m);
+            volatile float d2 = d * (float)sc, m2 = mn * (float)m;
+            for (int l = 0; l < 32; l++) {
+                int32_t lo = (w[b].qs[32 * c + l] & 0x0f) + (((w[b].qh[l] >> (2 * c)) & 1) << 4);
+                int32_t hi = (w[b].qs[32 * c + l] >> 4) + (((w[b].qh[l] >> (2 * c + 1)) & 1) << 4);
+                volatile float a = d1 * (float)lo, e = d2 * (float)hi;
+                y[64 * c + l] = a - m1;
+                y[64 * c + 32 + l] = e - m2;
+            }
+        }
+    }
+}
+
+/* slm/tensor.c:988-1010: y = rn(rn(d*sc) * (u6 - 32)). */
+void qko_dequant_q6k(const void *wv, int64_t nblocks, float *out) {
+    const o_q6k *w = (const o_q6k *)wv;
+    for (int64_t b = 0; b < nblocks; b++) {
+        const float d = qko_f16_to_f32(w[b].d);
+        for (int e = 0; e < QK_K; e++) {
+            volatile float ds = d * (float)w[b].scales[e / 16];
+            out[b * QK_K + e] = ds * (float)(q6_raw(&w[b], e) - 32);
+        }
+    }
+}
+
+static int type_block(int type, int64_t *elems, int64_t *bytes) {
+    int ok = 1;
+    switch (type) {
+        case 8:  *elems = QK8_0; *bytes = sizeof(o_q8_0); break;
+        case 12: *elems = QK_K;  *bytes = sizeof(o_q4k);  break;
+        case 13: *elems = QK_K;  *bytes = sizeof(o_q5k);  break;
+        case 14: *elems = QK_K;  *bytes = sizeof(o_q6k);  break;
+        default: ok = 0; break;
+    }
+    return ok;
+}
+
+/* slm/tensor.c:838-851 (and 908-918, 968-980, 1022-1032): per token t,
+ * out[t*n + j] = row_dot(W row j, xq row t). */
+int qko_matmul_xq(int type, const void *w, int64_t n, int64_t k,
+                  const void *xq, int64_t m, float *out, int epi,
+                  int64_t row0, int64_t row1) {
+    int64_t be, bb;
+    if (!type_block(type, &be, &bb) || k % be) return -1;
+    const int64_t nb = k / be;
+    const int64_t xbytes = (type == 8) ? (int64_t)sizeof(o_q8_0) : (int64_t)sizeof(o_q8k);
+    for (int64_t t = 0; t < m; t++) {
+        const char *xr = (const char *)xq + t * nb * xbytes;
+        for (int64_t j = row0; j < row1; j++) {
+            const char *wr = (const char *)w + j * nb * bb;
+            float v;
+            switch (type) {
+                case 8:  v = qko_q8_0_dot(k, wr, xr, epi); break;
+                case 12: v = qko_q4k_dot((int)nb, wr, xr, epi); break;
+                case 13: v = qko_q5k_dot((int)nb, wr, xr, epi); break;
+                default: v = qko_q6k_dot((int)nb, wr, xr, epi); break;
+            }
+            out[t * n + j] = v;
+        }
+    }
+    return 0;
+}
+
+int qko_matmul(int type, const void *w, int64_t n, int64_t k,
+               const float *x, int64_t m, float *out, int epi,
+               int64_t row0, int64_t row1) {
+    int64_t be, bb;
+    if (!type_block(type, &be, &bb) || k % be) return -1;
+    /* One quantized activation row at a time, as the reference does. */
+    static __thread unsigned char buf[(1 << 16) / 256 * 292 + 64];
+    const int64_t xbytes = (type == 8) ? (k / QK8_0) * 34 : (k / QK_K) * 292;
+    if (xbytes > (int64_t)sizeof(buf)) return -2;
+    for (int64_t t = 0; t < m; t++) {
+        if (type == 8) qko_quantize_q8_0(x + t * k, buf, k);
+        else           qko_quantize_q8k(x + t * k, buf, k);
+        int r = qko_matmul_xq(type, w, n, k, buf, 1, out + t * n, epi, row0, row1);
+        if (r) return r;
+    }
+    return 0;
+}
+
+/* slm/model.c:401-412: first index of the maximum, strict '>'. */
+int32_t qko_argmax(const float *v, int64_t n) {
+    int32_t best = 0;
+    float b = v[0];
+    for (int64_t i = 1; i < n; i++) {
+        if (v[i] > b) { b = v[i]; best = (int32_t)i; }
+    }
+    return best;
+}
+
+/* slm/sampler.c:70-93: fill k slots in scan order, then replace the
+ * first minimum slot when strictly greater. */
+int32_t qko_topk_collect(const float *v, int64_t n, int32_t k,
+                         int32_t *idx, float *val) {
+    int32_t filled = 0;
+    if (k <= 0 || k > 256) k = 256;
+    for (int64_t i = 0; i < n; i++) {
+        if (filled < k) {
+            idx[filled] = (int32_t)i;
+            val[filled] = v[i];
+            filled++;
+        } else {
+            int32_t worst = 0;
+            for (int32_t j = 1; j < k; j++)
+                if (val[j] < val[worst]) worst = j;
+            if (v[i] > val[worst]) { idx[worst] = (int32_t)i; val[worst] = v[i]; }
+        }
+    }
+    return filled;
+}

@@ -1,0 +1,224 @@
+/*
+ * ref_shim.c -- exports the reference's own quantized-matmul functions
+ * from a shared library built out of the reference sources where they
+ * lie (REF/slm/qwen.c and everything it includes; nothing is copied).
+ *
+ * TEST INFRASTRUCTURE ONLY: loaded by tests/ (to pin the C oracle) and
+ * by bench.py's cpu_baseline leg (kind "reference"). Built by
+ * oracle/Makefile with the reference's own flags (slm/Makefile:13-17:
+ * clang -O3 -std=c17 -fvectorize -fslp-vectorize, no -march) into
+ * oracle/_ref/libqkref.so.
+ */
+#include "qwen.c"
+#include "sampler.c"   /* guarded by SAMPLER_C; topk_collect */
+
+#include <pthread.h>
+
+void ref_simd_init(void) { simd_init(); }
+const char *ref_dispatch_label(void) { return simd_dispatch_label(); }
+
+/* Which x86 tiers this CPU can run (bit t set = tier t usable;
+ * 0 scalar, 1 AVX1, 2 AVX2-FMA, 3 AVX-VNNI), simd/simd.c:208-229. */
+int ref_tiers_available(void) {
+    simd_init();
+    int m = 1;
+#if defined(SIMD_X86)
+    if (g_cpu.x86_avx) m |= 2;
+    if (g_cpu.x86_avx2 && g_cpu.x86_fma) m |= 4;
+    if (g_cpu.x86_avx_vnni && g_cpu.x86_avx2 && g_cpu.x86_fma) m |= 8;
+#endif
+    return m;
+}
+
+void ref_quantize_q8k(const float *x, void *y, int64_t k) {
+    quantize_row_q8_K(x, (q8k_block *)y, k);
+}
+void ref_quantize_q8k_quants_h(const float *x, void *y, int64_t k) {
+    q_quantize_row_q8_K(x, (q8k_block *)y, k);
+}
+void ref_quantize_q8_0(const float *x, void *y, int64_t k) {
+    tensor_quantize_row_q8_0(x, (q8_0_block *)y, k);
+}
+
+/* tier -1: the dispatched entry point; 0..3: one tier by name. A tier
+ * the CPU cannot run returns NaN instead of executing it. */
+static int tier_ok(int tier) { return tier < 0 || ((ref_tiers_available() >> tier) & 1); }
+
+float ref_q4k_dot(int tier, int nb, const void *w, const void *x) {
+    const q4k_block *a = w; const q8k_block *b = x;
+    float r = NAN;
+    if (!tier_ok(tier)) return r;
+    switch (tier) {
+        case -1: r = simd_q4k_row_dot_q8k(nb, a, b); break;
+        case 0:  r = q_scalar_q4k_row_dot_q8k(nb, a, b); break;
+#if defined(SIMD_X86)
+        case 1:  r = q4k_row_dot_q8k_avx1(nb, a, b); break;
+        case 2:  r = q4k_row_dot_q8k_avx2(nb, a, b); break;
+        case 3:  r = q4k_row_dot_q8k_avxvnni(nb, a, b); break;
+#endif
+        default: break;
+    }
+    return r;
+}
+
+float ref_q5k_dot(int tier, int nb, const void *w, const void *x) {
+    const q5k_block *a = w; const q8k_block *b = x;
+    float r = NAN;
+    if (!tier_ok(tier)) return r;
+    switch (tier) {
+        case -1: r = simd_q5k_row_dot_q8k(nb, a, b); break;
+        case 0:  r = q_scalar_q5k_row_dot_q8k(nb, a, b); break;
+#if defined(SIMD_X86)
+        case 1:  r = q5k_row_dot_q8k_avx1(nb, a, b); break;
+        case 2:  r = q5k_row_dot_q8k_avx2(nb, a, b); break;
+        case 3:  r = q5k_row_dot_q8k_avxvnni(nb, a, b); break;
+#endif
+        default: break;
+    }
+    return r;
+}
+
+float ref_q6k_dot(int tier, int nb, const void *w, const void *x) {
+    const q6k_block *a = w; const q8k_block *b = x;
+    float r = NAN;
+    if (!tier_ok(tier)) return r;
+    switch (tier) {
+        case -1: r = simd_q6k_row_dot_q8k(nb, a, b); break;
+        case 0:  r = q_scalar_q6k_row_dot_q8k(nb, a, b); break;
+#if defined(SIMD_X86)
+        case 1:  r = q6k_row_dot_q8k_avx1(nb, a, b); break;
+        case 2:  r = q6k_row_dot_q8k_avx2(nb, a, b); break;
+        case 3:  r = q6k_row_dot_q8k_avxvnni(nb, a, b); break;
+#endif
+        default: break;
+    }
+    return r;
+}
+
+float ref_q8_0_dot(int tier, int64_t k, const void *w, const void *x) {
+    const q8_0_block *a = w; const q8_0_block *b = x;
+    float r = NAN;
+    if (!tier_ok(tier)) return r;
+    switch (tier) {
+        case -1: r = simd_q8_0_dot_q8_0(a, b, k); break;
+        case 0:  r = q_scalar_q8_0_dot_q8_0(a, b, k); break;
+#if defined(SIMD_X86)
+        case 1:  r = q8_0_dot_q8_0_avx1(a, b, k); break;
+        case 2:  r = q8_0_dot_q8_0_avx2(a, b, k); break;
+        case 3:  r = q8_0_dot_q8_0_avxvnni(a, b, k); break;
+#endif
+        default: break;
+    }
+    return r;
+}
+
+void ref_dequant_q4k(const void *w, int64_t nb, float *y) {
+    for (int64_t i = 0; i < nb; i++) q4k_dequant_block((const q4k_block *)w + i, y + i * QK_K);
+}
+void ref_dequant_q5k(const void *w, int64_t nb, float *y) {
+    for (int64_t i = 0; i < nb; i++) q5k_dequant_block((const q5k_block *)w + i, y + i * QK_K);
+}
+void ref_dequant_q6k(const void *w, int64_t nb, float *y) {
+    for (int64_t i = 0; i < nb; i++) q6k_dequant_block((const q6k_block *)w + i, y + i * QK_K);
+}
+void ref_scale_min(const uint8_t *s, int j, uint8_t *sc, uint8_t *m) {
+    q4k_get_scale_min(s, j, sc, m);
+}
+
+/* tensor_matmul_*_f32 (slm/tensor.c:827-1033) called as the model
+ * calls it through matmul_dispatch (slm/model.c:220-264): x is m rows
+ * of k floats, out receives the (n, m) result tensor's data. */
+int ref_matmul(int type, const void *w, int64_t n, int64_t k,
+               const float *x, int64_t m, float *out) {
+    simd_init();
+    struct arena *a = arena_new((size_t)(m * k + m * n) * sizeof(float) + (1u << 20));
+    struct tensor *xt = tensor_new_2d(a, k, m);
+    memcpy(xt->data, x, (size_t)(m * k) * sizeof(float));
+    struct tensor *r = NULL;
+    switch (type) {
+        case GGUF_TT_Q4_K: r = tensor_matmul_q4k_f32((const q4k_block *)w, n, k, xt); break;
+        case GGUF_TT_Q5_K: r = tensor_matmul_q5k_f32((const q5k_block *)w, n, k, xt); break;
+        case GGUF_TT_Q6_K: r = tensor_matmul_q6k_f32((const q6k_block *)w, n, k, xt); break;
+        case GGUF_TT_Q8_0: r = tensor_matmul_q8_0_f32((const q8_0_block *)w, n, k, xt); break;
+        default: break;
+    }
+    if (r) memcpy(out, r->data, (size_t)(m * n) * sizeof(float));
+    arena_free(a);
+    return r ? 0 : -1;
+}
+
+/* Harness-side row split for the N-core CPU baseline: quantize each
+ * token once with the reference quantizer, then hand row ranges to
+ * threads that call the unmodified dispatched simd_q*_row_dot. Rows
+ * are independent (slm/tensor.c:846), so the output is bit-identical
+ * to ref_matmul. */
+struct rows_job {
+    int type; const void *w; int64_t n, k, nb; const void *xq; float *out;
+    int64_t r0, r1;
+};
+
+static void *rows_worker(void *p) {
+    struct rows_job *j = p;
+    for (int64_t r = j->r0; r < j->r1; r++) {
+        float v = 0.0f;
+        switch (j->type) {
+            case GGUF_TT_Q4_K: v = simd_q4k_row_dot_q8k((int)j->nb, (const q4k_block *)j->w + r * j->nb, j->xq); break;
+            case GGUF_TT_Q5_K: v = simd_q5k_row_dot_q8k((int)j->nb, (const q5k_block *)j->w + r * j->nb, j->xq); break;
+            case GGUF_TT_Q6_K: v = simd_q6k_row_dot_q8k((int)j->nb, (const q6k_block *)j->w + r * j->nb, j->xq); break;
+            default:           v = simd_q8_0_dot_q8_0((const q8_0_block *)j->w + r * j->nb, j->xq, j->k); break;
+        }
+        j->out[r] = v;
+    }
+    return NULL;
+}
+
+int ref_matmul_threads(int type, const void *w, int64_t n, int64_t k,
+                       const float *x, int64_t m, float *out, int nthreads) {
+    simd_init();
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    int q8_0 = (type == GGUF_TT_Q8_0);
+    int64_t nb = q8_0 ? k / QK8_0 : k / QK_K;
+    size_t xbytes = q8_0 ? (size_t)nb * sizeof(q8_0_block) : (size_t)nb * sizeof(q8k_block);
+    void *xq = malloc(xbytes);
+    pthread_t th[256];
+    struct rows_job jobs[256];
+    if (!xq) return -1;
+    for (int64_t t = 0; t < m; t++) {
+        if (q8_0) tensor_quantize_row_q8_0(x + t * k, xq, k);
+        else      quantize_row_q8_K(x + t * k, xq, k);
+        for (int i = 0; i < nthreads; i++) {
+            jobs[i] = (struct rows_job){type, w, n, k, nb, xq, out + t * n,
+                                        n * i / nthreads, n * (i + 1) / nthreads};
+            if (nthreads == 1) rows_worker(&jobs[i]);
+            else pthread_create(&th[i], NULL, rows_worker, &jobs[i]);
+        }
+        if (nthreads > 1)
+            for (int i = 0; i < nthreads; i++) pthread_join(th[i], NULL);
+    }
+    free(xq);
+    return 0;
+}
+
+/* sample_argmax (slm/model.c:401) and topk_collect (slm/sampler.c:70)
+ * on a 1-D view of v. */
+static struct tensor view1d(const float *v, int64_t n) {
+    struct tensor t;
+    memset(&t, 0, sizeof(t));
+    t.ndim = 1;
+    t.ne[0] = n;
+    for (int i = 1; i < TENSOR_MAX_DIMS; i++) t.ne[i] = 1;
+    t.nb[0] = sizeof(float);
+    t.data = (float *)v;
+    return t;
+}
+
+int32_t ref_argmax(const float *v, int64_t n) {
+    struct tensor t = view1d(v, n);
+    return sample_argmax(&t);
+}
+
+int32_t ref_topk_collect(const float *v, int64_t n, int32_t k, int32_t *idx, float *val) {
+    struct tensor t = view1d(v, n);
+    return topk_collect(&t, k, idx, val);
+}

@@ -1,0 +1,194 @@
+// qk_dev.h -- device-side helpers shared by the libqk kernels (gfx950).
+//
+// Everything here is exact integer work or a single IEEE operation with
+// an explicit rounding: the translation units are compiled with
+// -ffp-contract=off and each place where the reference's AVX2/VNNI tier
+// contracts to an FMA calls __builtin_fmaf by name.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define QK_K 256
+#define QK8_0 32
+
+// Block byte sizes and field offsets (simd/quants.h:95-130).
+#define Q8K_BYTES 292   // f32 d | i8 qs[256] @4 | i16 bsums[16] @260
+#define Q4K_BYTES 144   // f16 d | f16 dmin @2 | u8 scales[12] @4 | u8 qs[128] @16
+#define Q5K_BYTES 176   // ... scales @4 | u8 qh[32] @16 | u8 qs[128] @48
+#define Q6K_BYTES 210   // u8 ql[128] | u8 qh[64] @128 | i8 scales[16] @192 | f16 d @208
+#define Q80_BYTES 34    // f16 d | i8 qs[32] @2
+
+// Upper bound on blocks per activation row staged in LDS: K <= 16384.
+#define QK_MAX_K 16384
+#define QK_NB_MAX (QK_MAX_K / QK_K)
+
+namespace qk {
+
+// ---- fp16 <-> fp32 as exact integer work (the reference's `_Float16`
+// casts on x86: exact widening, round-to-nearest-even narrowing). The
+// bit formulation does not depend on the MODE register's fp16 denormal
+// setting.
+__device__ __forceinline__ float h2f(uint32_t h) {
+    uint32_t sign = (h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    float r;
+    if (e == 0) {
+        r = __int_as_float(__float_as_int((float)m * 0x1p-24f) | (int)sign);
+    } else if (e == 31) {
+        r = __uint_as_float(sign | 0x7f800000u | (m << 13));
+    } else {
+        r = __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
+    }
+    return r;
+}
+
+__device__ __forceinline__ uint32_t f2h(float f) {
+    uint32_t x = __float_as_uint(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    uint32_t q;
+    if (ax > 0x7f800000u) {
+        q = 0x7e00u | ((ax >> 13) & 0x3ffu);
+    } else if (ax >= 0x477ff000u) {
+        q = 0x7c00u;
+    } else if (ax >= 0x38800000u) {
+        uint32_t rem = ax & 0x1fffu;
+        q = (((ax >> 23) - 112u) << 10) | ((ax >> 13) & 0x3ffu);
+        if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q += 1;
+    } else if (ax <= 0x33000000u) {
+        q = 0;
+    } else {
+        uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        uint32_t shift = 126u - (ax >> 23);
+        uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        q = m >> shift;
+        if (rem > half || (rem == half && (q & 1u))) q += 1;
+    }
+    return sign | q;
+}
+
+// q_nearest_int (simd/quants.h:137-142): magic-number rounding with a
+// separately rounded add.
+__device__ __forceinline__ int32_t nearest_int(float v) {
+    float t = __fadd_rn(v, 12582912.f);
+    return (__float_as_int(t) & 0x007fffff) - 0x00400000;
+}
+
+// ---- 4-wide int8 dot (v_dot4_i32_i8): exact int32 accumulate.
+__device__ __forceinline__ int32_t dot4(uint32_t a, uint32_t b, int32_t c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// ---- cross-lane helpers within aligned groups of 8 lanes -------------
+__device__ __forceinline__ int32_t dpp_xor1(int32_t v) {
+    return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);   // quad_perm [1,0,3,2]
+}
+__device__ __forceinline__ int32_t dpp_xor2(int32_t v) {
+    return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);   // quad_perm [2,3,0,1]
+}
+__device__ __forceinline__ int32_t dpp_hmirror(int32_t v) {
+    return __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true);  // row_half_mirror
+}
+// Sum over the 8-lane group; every lane of the group gets the total.
+__device__ __forceinline__ int32_t sum8(int32_t v) {
+    v += dpp_xor1(v);
+    v += dpp_xor2(v);
+    v += dpp_hmirror(v);
+    return v;
+}
+// Lane l <- lane l^4 (ds_swizzle bit mode, xor_mask 4, within 32 lanes).
+__device__ __forceinline__ float swz_xor4(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x101F));
+}
+__device__ __forceinline__ float swz_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x041F));
+}
+__device__ __forceinline__ float swz_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x081F));
+}
+
+// ---- loads -------------------------------------------------------------
+struct __attribute__((aligned(4))) u32x4a4 { uint32_t x, y, z, w; };
+
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) {       // 16-B aligned
+    return *reinterpret_cast<const uint4 *>(p);
+}
+
+// 16 bytes starting at a 2-byte aligned address, read as an aligned
+// 20-byte window [floor4(p), floor4(p)+20) and funnel-shifted. Callers
+// guarantee that the whole window lies inside the buffer.
+__device__ __forceinline__ uint4 ld16_a2(const uint8_t *p) {
+    uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(a & ~(uintptr_t)3);
+    uint32_t sh = (uint32_t)(a & 3);
+    u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(q);
+    uint4 r;
+    if (sh == 0) {
+        r = make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+        uint32_t e = q[4];
+        r.x = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+        r.y = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+        r.z = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
+        r.w = __builtin_amdgcn_alignbyte(e, v.w, sh);
+    }
+    return r;
+}
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) {  // 2-B aligned
+    return *reinterpret_cast<const uint16_t *>(p);
+}
+
+// ---- Q4_K / Q5_K 6-bit scale and min of sub-block s (0..7) from the
+// 12 packed bytes held in three dwords (q4k_get_scale_min,
+// simd/quants.h:215-224).
+__device__ __forceinline__ uint32_t sbyte(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
+    uint32_t d = (i < 4) ? s0 : ((i < 8) ? s1 : s2);
+    return (d >> (8 * (i & 3))) & 0xffu;
+}
+__device__ __forceinline__ void scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int s,
+                                          int32_t &sc, int32_t &m) {
+    if (s < 4) {
+        sc = (int32_t)(sbyte(s0, s1, s2, s) & 63u);
+        m  = (int32_t)(sbyte(s0, s1, s2, s + 4) & 63u);
+    } else {
+        sc = (int32_t)((sbyte(s0, s1, s2, s + 4) & 15u) | ((sbyte(s0, s1, s2, s - 4) >> 6) << 4));
+        m  = (int32_t)((sbyte(s0, s1, s2, s + 4) >> 4) | ((sbyte(s0, s1, s2, s) >> 6) << 4));
+    }
+}
+
+// ---- float epilogues (bit-exact per tier) --------------------------------
+// Q4_K/Q5_K super-block term. separate (scalar/AVX1, simd/quants.h:305,
+// simd/avx.c:654): rn(rn(d*isum) - rn(dmin*mins)); fused (AVX2/VNNI,
+// simd/avx.c:229,466,515): fma(d, isum, -rn(dmin*mins)).
+template <bool FUSED>
+__device__ __forceinline__ float kterm(float yd, uint32_t xd, uint32_t xdmin, int32_t isum,
+                                       int32_t mins) {
+    float d = __fmul_rn(yd, h2f(xd));
+    float dmin = __fmul_rn(yd, h2f(xdmin));
+    float pm = __fmul_rn(dmin, (float)mins);
+    float t;
+    if (FUSED) {
+        t = __builtin_fmaf(d, (float)isum, -pm);
+    } else {
+        t = __fsub_rn(__fmul_rn(d, (float)isum), pm);
+    }
+    return t;
+}
+
+// AVX2/VNNI return the row sum through an 8-lane broadcast:
+// hsum(8 x s) / 8 (simd/avx.c:231-240), which is s unless 8s overflows.
+__device__ __forceinline__ float bcast8(float s) {
+    const float s2 = __fadd_rn(s, s);
+    const float s4 = __fadd_rn(s2, s2);
+    const float s8 = __fadd_rn(s4, s4);
+    return __fdiv_rn(s8, 8.0f);
+}
+
+// Q6_K term (all tiers, simd/quants.h:399): rn(rn(fp16(x.d)*y.d) * (float)v).
+__device__ __forceinline__ float q6term(float yd, uint32_t xd, int32_t v) {
+    return __fmul_rn(__fmul_rn(h2f(xd), yd), (float)v);
+}
+
+}  // namespace qk

@@ -1,0 +1,211 @@
+"""ctypes binding of libqk (include/qk.h) for tests and the benchmark.
+
+PyTorch is used only to own device memory and streams: every tensor
+passed to the device layer must already live on the GPU, and the call is
+enqueued on torch's current stream. The library itself is plain C ABI
+(libqk.so next to this file); when it is missing this module raises
+instead of falling back to anything else.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "libqk.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "qk.h")
+
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
+BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+BLOCK_ELEMS = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+Q8K_BYTES = 292
+TIER_SCALAR, TIER_AVX1, TIER_AVX2, TIER_AVXVNNI, TIER_AUTO = 0, 1, 2, 3, -1
+GROUP_MAX = 16
+TOPK_MAX = 256
+
+_vp, _i64, _i32 = C.c_void_p, C.c_int64, C.c_int32
+
+
+class QKError(RuntimeError):
+    def __init__(self, rc, msg):
+        super().__init__(f"libqk error {rc}: {msg}")
+        self.rc = rc
+
+
+class GemvDesc(C.Structure):
+    _fields_ = [("type", C.c_int32), ("pad_", C.c_int32), ("n", C.c_int64), ("k", C.c_int64),
+                ("w", C.c_void_p), ("xq", C.c_void_p), ("y", C.c_void_p)]
+
+
+def header_functions(path=HEADER):
+    """Names of the functions include/qk.h declares."""
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(hip_[a-z0-9_]+)\s*\(", text)))
+
+
+def act_bytes(wtype, k):
+    return (k // 32) * 34 if wtype == Q8_0 else (k // 256) * Q8K_BYTES
+
+
+def _dp(t):
+    return C.c_void_p(0 if t is None else t.data_ptr())
+
+
+class QK:
+    """libqk.so. Device-layer methods take torch CUDA tensors."""
+
+    def __init__(self, path=LIB):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is not built (run __graft_entry__.build())")
+        L = C.CDLL(path)
+        self.L = L
+        L.hip_qk_init.argtypes = [C.c_int]
+        L.hip_qk_shutdown.restype = None
+        for f in ("hip_qk_device_label", "hip_qk_last_error"):
+            getattr(L, f).restype = C.c_char_p
+        L.hip_qk_tier_label.restype = C.c_char_p
+        L.hip_qk_tier_label.argtypes = [C.c_int]
+        L.hip_qk_set_tier.argtypes = [C.c_int]
+        for f in ("hip_quantize_q8k", "hip_quantize_q8_0"):
+            getattr(L, f).argtypes = [_vp, _i64, _i64, _vp, _vp]
+        for f in ("hip_matvec_q4k", "hip_matvec_q5k", "hip_matvec_q6k", "hip_matvec_q8_0"):
+            getattr(L, f).argtypes = [_vp, _i64, _i64, _vp, _vp, _vp]
+        L.hip_matvec_group.argtypes = [C.POINTER(GemvDesc), C.c_int, _vp]
+        for f in ("hip_matmul_q4k", "hip_matmul_q5k", "hip_matmul_q6k"):
+            getattr(L, f).argtypes = [_vp, _i64, _i64, _vp, _i64, _vp, _vp]
+        for f in ("hip_dequant_q4k", "hip_dequant_q5k", "hip_dequant_q6k"):
+            getattr(L, f).argtypes = [_vp, _i64, _vp, _vp]
+        L.hip_lmhead_q6k_argmax_topk.argtypes = [_vp, _i64, _i64, _vp, C.c_int, _vp, _vp, _vp, _vp, _vp]
+        L.hip_qk_register_weight.argtypes = [_vp, C.c_int, _i64, _i64]
+        L.hip_qk_unregister_weight.argtypes = [_vp]
+        L.hip_qk_device_weight.argtypes = [_vp]
+        L.hip_qk_device_weight.restype = C.c_void_p
+        L.hip_qk_matmul_host.argtypes = [_vp, C.c_int, _i64, _i64, _vp, _i64, _vp]
+        L.hip_qk_lmhead_host.argtypes = [_vp, _i64, _i64, _vp, C.c_int, _vp, _vp, _vp, _vp]
+
+    # -- plumbing ---------------------------------------------------------
+    def _ck(self, rc):
+        if rc != 0:
+            raise QKError(rc, self.L.hip_qk_last_error().decode())
+        return rc
+
+    def last_error(self):
+        return self.L.hip_qk_last_error().decode()
+
+    @staticmethod
+    def _stream():
+        import torch
+        return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def init(self, device=0):
+        self._ck(self.L.hip_qk_init(device))
+        return self
+
+    def shutdown(self):
+        self.L.hip_qk_shutdown()
+
+    def label(self):
+        return self.L.hip_qk_device_label().decode()
+
+    def set_tier(self, tier):
+        self._ck(self.L.hip_qk_set_tier(tier))
+
+    def tier(self):
+        return self.L.hip_qk_get_tier()
+
+    def tier_label(self, tier=None):
+        return self.L.hip_qk_tier_label(self.tier() if tier is None else tier).decode()
+
+    # -- device layer ---------------------------------------------------------
+    def quantize_q8k(self, x, out=None):
+        import torch
+        m, k = x.shape
+        if out is None:
+            out = torch.empty((m, (k // 256) * Q8K_BYTES), dtype=torch.uint8, device=x.device)
+        self._ck(self.L.hip_quantize_q8k(_dp(x), m, k, _dp(out), self._stream()))
+        return out
+
+    def quantize_q8_0(self, x, out=None):
+        import torch
+        m, k = x.shape
+        if out is None:
+            out = torch.empty((m, (k // 32) * 34), dtype=torch.uint8, device=x.device)
+        self._ck(self.L.hip_quantize_q8_0(_dp(x), m, k, _dp(out), self._stream()))
+        return out
+
+    def quantize_for(self, wtype, x, out=None):
+        return self.quantize_q8_0(x, out) if wtype == Q8_0 else self.quantize_q8k(x, out)
+
+    def matvec(self, wtype, w, n, k, xq, y=None):
+        import torch
+        if y is None:
+            y = torch.empty(n, dtype=torch.float32, device=w.device)
+        f = {Q4_K: self.L.hip_matvec_q4k, Q5_K: self.L.hip_matvec_q5k,
+             Q6_K: self.L.hip_matvec_q6k, Q8_0: self.L.hip_matvec_q8_0}[wtype]
+        self._ck(f(_dp(w), n, k, _dp(xq), _dp(y), self._stream()))
+        return y
+
+    def matvec_group(self, items):
+        """items: list of (wtype, w, n, k, xq, y) with device tensors."""
+        arr = (GemvDesc * len(items))()
+        for i, (t, w, n, k, xq, y) in enumerate(items):
+            arr[i] = GemvDesc(t, 0, n, k, w.data_ptr(), xq.data_ptr(), y.data_ptr())
+        self._ck(self.L.hip_matvec_group(arr, len(items), self._stream()))
+
+    def matmul(self, wtype, w, n, k, xq, m, y=None):
+        import torch
+        if y is None:
+            y = torch.empty((m, n), dtype=torch.float32, device=w.device)
+        f = {Q4_K: self.L.hip_matmul_q4k, Q5_K: self.L.hip_matmul_q5k, Q6_K: self.L.hip_matmul_q6k}[wtype]
+        self._ck(f(_dp(w), n, k, _dp(xq), m, _dp(y), self._stream()))
+        return y
+
+    def dequant(self, wtype, w, nblocks, y=None):
+        import torch
+        if y is None:
+            y = torch.empty(nblocks * 256, dtype=torch.float32, device=w.device)
+        f = {Q4_K: self.L.hip_dequant_q4k, Q5_K: self.L.hip_dequant_q5k, Q6_K: self.L.hip_dequant_q6k}[wtype]
+        self._ck(f(_dp(w), nblocks, _dp(y), self._stream()))
+        return y
+
+    def lmhead(self, w, n, k, xq, topk=0, logits=None, want_logits=True):
+        import torch
+        dev = w.device
+        if logits is None and want_logits:
+            logits = torch.empty(n, dtype=torch.float32, device=dev)
+        am = torch.empty(1, dtype=torch.int32, device=dev)
+        ti = torch.empty(max(topk, 1), dtype=torch.int32, device=dev)
+        tv = torch.empty(max(topk, 1), dtype=torch.float32, device=dev)
+        self._ck(self.L.hip_lmhead_q6k_argmax_topk(_dp(w), n, k, _dp(xq), topk, _dp(logits), _dp(am),
+                                                    _dp(ti) if topk else None, _dp(tv) if topk else None,
+                                                    self._stream()))
+        return logits, am, ti[:topk], tv[:topk]
+
+    # -- host seam --------------------------------------------------------------
+    def matmul_host(self, wtype, w_np, out_f, k, x_np):
+        x = np.ascontiguousarray(x_np, np.float32).reshape(-1, k)
+        out = np.empty((x.shape[0], out_f), np.float32)
+        self._ck(self.L.hip_qk_matmul_host(w_np.ctypes.data_as(_vp), wtype, out_f, k,
+                                           x.ctypes.data_as(_vp), x.shape[0], out.ctypes.data_as(_vp)))
+        return out
+
+    def lmhead_host(self, w_np, n, k, x_np, topk=0):
+        x = np.ascontiguousarray(x_np, np.float32).reshape(k)
+        logits = np.empty(n, np.float32)
+        am = np.zeros(1, np.int32)
+        ti = np.zeros(max(topk, 1), np.int32)
+        tv = np.zeros(max(topk, 1), np.float32)
+        self._ck(self.L.hip_qk_lmhead_host(w_np.ctypes.data_as(_vp), n, k, x.ctypes.data_as(_vp), topk,
+                                           logits.ctypes.data_as(_vp), am.ctypes.data_as(_vp),
+                                           ti.ctypes.data_as(_vp), tv.ctypes.data_as(_vp)))
+        return logits, int(am[0]), ti[:topk], tv[:topk]
+
+    def register_weight(self, w_np, wtype, k, n):
+        self._ck(self.L.hip_qk_register_weight(w_np.ctypes.data_as(_vp), wtype, k, n))
+
+    def unregister_weight(self, w_np):
+        self._ck(self.L.hip_qk_unregister_weight(w_np.ctypes.data_as(_vp)))

@@ -1,0 +1,204 @@
+"""GPU parity: libqk (through its C ABI) against the CPU oracle on the same
+inputs. Bar: bit-exact for quantizers, dequant and every row dot (both
+float-epilogue families), identical argmax token; top-k as a set.
+
+Sizes: the BASELINE configurations at full size where the oracle is fast
+(config 0-2), plus ragged and edge shapes."""
+import numpy as np
+import pytest
+
+from cases import edge_rows
+from conftest import assert_bits_equal, oracle, qk, synth
+
+pytestmark = pytest.mark.gpu
+
+EPI_TIERS = [(oracle.EPI_SEPARATE, qk.TIER_SCALAR), (oracle.EPI_FUSED, qk.TIER_AVX2)]
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def step(msg):
+    print(f"[gpu] {msg}", flush=True)
+
+
+# ---- quantizers ---------------------------------------------------------------
+
+@pytest.mark.parametrize("k", [256, 1024, 3584, 16384])
+def test_quantize_q8k_bit_exact(lib, orc, k):
+    step(f"quantize_q8k k={k}")
+    x = np.concatenate([edge_rows(k), synth.activations(37, k, seed=k)])
+    got = host(lib.quantize_q8k(dev(x)))
+    np.testing.assert_array_equal(got, orc.quantize_q8k(x))
+
+
+@pytest.mark.parametrize("k", [32, 1024, 2080])
+def test_quantize_q8_0_bit_exact(lib, orc, k):
+    step(f"quantize_q8_0 k={k}")
+    x = np.concatenate([edge_rows(k), synth.activations(21, k, seed=k)])
+    got = host(lib.quantize_q8_0(dev(x)))
+    np.testing.assert_array_equal(got, orc.quantize_q8_0(x))
+
+
+def test_quantize_prefill_rows(lib, orc):
+    step("quantize_q8k m=512 k=1024")
+    x = synth.activations(512, 1024, seed=0)
+    np.testing.assert_array_equal(host(lib.quantize_q8k(dev(x))), orc.quantize_q8k(x))
+
+
+# ---- dequant ---------------------------------------------------------------------
+
+@pytest.mark.parametrize("wtype", [12, 13, 14])
+def test_dequant_bit_exact(lib, orc, wtype):
+    step(f"dequant type={wtype}")
+    w = synth.blocks(wtype, 33, 1024, seed=2, tag=wtype)
+    nb = w.size // qk.BLOCK_BYTES[wtype]
+    got = host(lib.dequant(wtype, dev(w.ravel()), nb))
+    assert_bits_equal(got, orc.dequant(wtype, w, nb), f"dequant {wtype}")
+
+
+# ---- decode GEMV -------------------------------------------------------------------
+
+SHAPES = [
+    (12, 3584, 1024), (13, 2048, 1024), (13, 512, 1024), (13, 1024, 2048),
+    (14, 1024, 3584), (8, 1024, 1024),                     # config 1
+    (12, 7, 256), (12, 33, 768), (12, 65, 1280), (13, 19, 512), (14, 17, 768),
+    (14, 100, 2560), (12, 40, 16384), (14, 9, 16384), (8, 45, 96), (8, 3, 16384),
+]
+
+
+@pytest.mark.parametrize("wtype,n,k", SHAPES)
+@pytest.mark.parametrize("epi,t", EPI_TIERS)
+def test_matvec(tier, orc, wtype, n, k, epi, t):
+    lib = tier
+    step(f"matvec type={wtype} n={n} k={k} tier={t}")
+    lib.set_tier(t)
+    w = synth.blocks(wtype, n, k, seed=n, tag=wtype)
+    x = np.concatenate([synth.activations(2, k, seed=k), edge_rows(k)[[0, 6, 7]]])
+    xq = orc.quantize_for(wtype, x)
+    wd = dev(w)
+    xqd = dev(xq)
+    for r in range(x.shape[0]):
+        got = host(lib.matvec(wtype, wd, n, k, xqd[r]))
+        want = orc.matmul_xq(wtype, w, n, k, xq[r:r + 1], 1, epi)[0]
+        assert_bits_equal(got, want, f"row {r}")
+
+
+def test_matvec_group_matches_single(lib, orc):
+    step("matvec_group config 1")
+    import torch
+    specs = [(12, 3584, 1024), (12, 3584, 1024), (14, 1024, 3584), (13, 2048, 1024),
+             (13, 512, 1024), (13, 1024, 2048), (8, 1024, 1024)]
+    items, wants = [], []
+    for i, (t, n, k) in enumerate(specs):
+        w = synth.blocks(t, n, k, seed=1, tag=i)
+        x = synth.activations(1, k, seed=1, tag=i)
+        xq = orc.quantize_for(t, x)
+        y = torch.empty(n, dtype=torch.float32, device="cuda")
+        items.append((t, dev(w), n, k, dev(xq[0]), y))
+        wants.append(orc.matmul_xq(t, w, n, k, xq, 1, oracle.TIER_EPI[lib.tier()])[0])
+    lib.matvec_group(items)
+    for (t, _, n, k, _, y), want in zip(items, wants):
+        assert_bits_equal(host(y), want, f"group type {t} {n}x{k}")
+
+
+def test_quantize_then_matvec_on_device(lib, orc):
+    step("quantize + matvec chain")
+    k, n = 1024, 3584
+    w = synth.blocks(12, n, k, seed=0)
+    x = synth.activations(1, k, seed=0)
+    xq = lib.quantize_q8k(dev(x))
+    got = host(lib.matvec(12, dev(w), n, k, xq))
+    want = orc.matmul(12, w, n, k, x, oracle.TIER_EPI[lib.tier()])[0]
+    assert_bits_equal(got, want, "config 0")
+
+
+# ---- LM head ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,k,topk", [(248320, 1024, 40), (31040, 1024, 40), (5000, 512, 256), (77, 256, 1)])
+def test_lmhead_argmax_topk(lib, orc, n, k, topk):
+    step(f"lmhead n={n} k={k} topk={topk}")
+    w = synth.blocks(14, n, k, seed=2)
+    x = synth.activations(1, k, seed=2)
+    xq = orc.quantize_q8k(x)
+    epi = oracle.TIER_EPI[lib.tier()]
+    want = orc.matmul_xq(14, w, n, k, xq, 1, epi)[0]
+    logits, am, ti, tv = lib.lmhead(dev(w), n, k, dev(xq[0]), topk=topk)
+    assert_bits_equal(host(logits), want, "logits")
+    assert int(host(am)[0]) == orc.argmax(want)
+    ti, tv = host(ti), host(tv)
+    ri, rv = orc.topk_collect(want, topk)
+    kth = np.sort(rv)[0]
+    if (want == kth).sum() == 1:                   # no tie at the k-th value
+        assert set(ti.tolist()) == set(ri.tolist())
+    assert_bits_equal(tv, want[ti], "topk values")
+    assert (np.diff(tv) <= 0).all()
+
+
+def test_lmhead_argmax_ties_and_nan(lib, orc):
+    step("lmhead argmax rules")
+    # duplicate rows give tied logits: the first index must win
+    k, n = 256, 4096
+    w = synth.blocks(14, n, k, seed=5)
+    w[3000] = w[17]
+    w[2000] = w[17]
+    xq = orc.quantize_q8k(synth.activations(1, k, seed=5))
+    epi = oracle.TIER_EPI[lib.tier()]
+    want = orc.matmul_xq(14, w, n, k, xq, 1, epi)[0]
+    top = orc.argmax(want)
+    w[[3000, 2000]] = w[top]                       # tie the maximum at later rows
+    want = orc.matmul_xq(14, w, n, k, xq, 1, epi)[0]
+    logits, am, _, _ = lib.lmhead(dev(w), n, k, dev(xq[0]), topk=0)
+    assert int(host(am)[0]) == orc.argmax(want) == top
+
+
+# ---- host seam ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("wtype,n,k,m", [(12, 3584, 1024, 1), (13, 512, 1024, 1), (14, 1024, 3584, 1),
+                                          (8, 1024, 1024, 1), (8, 64, 1024, 21)])
+def test_matmul_host_seam(lib, orc, wtype, n, k, m):
+    step(f"host seam type={wtype} n={n} k={k} m={m}")
+    w = synth.blocks(wtype, n, k, seed=3, tag=wtype)
+    x = synth.activations(m, k, seed=3)
+    got = lib.matmul_host(wtype, w, n, k, x)
+    want = orc.matmul(wtype, w, n, k, x, oracle.TIER_EPI[lib.tier()])
+    assert_bits_equal(got, want, "tensor_matmul seam")
+    lib.unregister_weight(w)
+
+
+def test_lmhead_host_seam(lib, orc):
+    step("lmhead host seam")
+    n, k = 20000, 1024
+    w = synth.blocks(14, n, k, seed=4)
+    x = synth.activations(1, k, seed=4)
+    logits, am, ti, tv = lib.lmhead_host(w, n, k, x[0], topk=40)
+    want = orc.matmul(14, w, n, k, x, oracle.TIER_EPI[lib.tier()])[0]
+    assert_bits_equal(logits, want, "logits")
+    assert am == orc.argmax(want)
+    lib.unregister_weight(w)
+
+
+# ---- argument checks ---------------------------------------------------------------------
+
+def test_rejects_bad_shapes(lib):
+    import torch
+    w = torch.zeros(144 * 4, dtype=torch.uint8, device="cuda")
+    xq = torch.zeros(292 * 4, dtype=torch.uint8, device="cuda")
+    y = torch.zeros(4, dtype=torch.float32, device="cuda")
+    with pytest.raises(qk.QKError) as e:
+        lib.matvec(12, w, 4, 1000, xq, y)              # k % 256
+    assert e.value.rc == 1
+    with pytest.raises(qk.QKError):
+        lib.matvec(12, w[1:], 1, 256, xq, y)           # misaligned weights
+    with pytest.raises(qk.QKError):
+        lib.matvec(12, w, 1, 32768, xq, y)             # k above the LDS stage
+    with pytest.raises(qk.QKError):
+        lib.lmhead(w, 4, 256, xq, topk=5)              # topk > n
