@@ -7,6 +7,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
 #include <stdint.h>
 
 #define QK_K 256
@@ -25,22 +26,13 @@
 
 namespace qk {
 
-// ---- fp16 <-> fp32 as exact integer work (the reference's `_Float16`
-// casts on x86: exact widening, round-to-nearest-even narrowing). The
-// bit formulation does not depend on the MODE register's fp16 denormal
-// setting.
+// ---- fp16 <-> fp32 (the reference's `_Float16` casts on x86: exact
+// widening, round-to-nearest-even narrowing; narrowing is integer work so
+// it does not depend on the MODE register).
 __device__ __forceinline__ float h2f(uint32_t h) {
-    uint32_t sign = (h & 0x8000u) << 16;
-    uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
-    float r;
-    if (e == 0) {
-        r = __int_as_float(__float_as_int((float)m * 0x1p-24f) | (int)sign);
-    } else if (e == 31) {
-        r = __uint_as_float(sign | 0x7f800000u | (m << 13));
-    } else {
-        r = __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
-    }
-    return r;
+    // v_cvt_f32_f16: exact widening; fp16 denormals are kept (the kernels
+    // run with denorm mode 3 for f16/f64).
+    return __half2float(__ushort_as_half((unsigned short)(h & 0xffffu)));
 }
 
 __device__ __forceinline__ uint32_t f2h(float f) {
@@ -109,35 +101,42 @@ __device__ __forceinline__ float swz_xor2(float v) {
 }
 
 // ---- loads -------------------------------------------------------------
+// Weight and activation pointers reach the kernels inside argument structs,
+// where the compiler only sees generic pointers; the casts below make
+// every such load a global_load (not flat_load).
+#if defined(__HIP_DEVICE_COMPILE__)
+#define QK_GLOBAL __attribute__((address_space(1)))
+#define QK_LDS __attribute__((address_space(3)))
+#else
+#define QK_GLOBAL   /* host pass: device bodies are parsed, never run */
+#define QK_LDS
+#endif
 struct __attribute__((aligned(4))) u32x4a4 { uint32_t x, y, z, w; };
 
 __device__ __forceinline__ uint4 ld16(const uint8_t *p) {       // 16-B aligned
-    return *reinterpret_cast<const uint4 *>(p);
+    return *(const QK_GLOBAL uint4 *)(p);
 }
 
-// 16 bytes starting at a 2-byte aligned address, read as an aligned
-// 20-byte window [floor4(p), floor4(p)+20) and funnel-shifted. Callers
-// guarantee that the whole window lies inside the buffer.
-__device__ __forceinline__ uint4 ld16_a2(const uint8_t *p) {
-    uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t *q = reinterpret_cast<const uint32_t *>(a & ~(uintptr_t)3);
-    uint32_t sh = (uint32_t)(a & 3);
-    u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(q);
-    uint4 r;
-    if (sh == 0) {
-        r = make_uint4(v.x, v.y, v.z, v.w);
-    } else {
-        uint32_t e = q[4];
-        r.x = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
-        r.y = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
-        r.z = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
-        r.w = __builtin_amdgcn_alignbyte(e, v.w, sh);
-    }
+__device__ __forceinline__ uint32_t ld32(const uint8_t *p) {    // 4-B aligned
+    return *(const QK_GLOBAL uint32_t *)(p);
+}
+
+__device__ __forceinline__ u32x4a4 ld16_a4(const uint8_t *p) {  // 4-B aligned
+    const QK_GLOBAL uint32_t *q = (const QK_GLOBAL uint32_t *)(p);
+    u32x4a4 r;
+    r.x = q[0];
+    r.y = q[1];
+    r.z = q[2];
+    r.w = q[3];
     return r;
 }
 
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) {  // 2-B aligned
-    return *reinterpret_cast<const uint16_t *>(p);
+    return *(const QK_GLOBAL uint16_t *)(p);
+}
+
+__device__ __forceinline__ uint32_t ld_u8(const uint8_t *p) {
+    return *(const QK_GLOBAL uint8_t *)(p);
 }
 
 // ---- Q4_K / Q5_K 6-bit scale and min of sub-block s (0..7) from the

@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #define QK_GROUP_MAX_DEV 16
+#define QK_TOPK_MAX_DEV 256
 
 namespace qk {
 
@@ -18,33 +19,38 @@ struct GemvDesc {
     const uint8_t *xq;
     float *y;
     int32_t nb;            // blocks per row (k/256, or k/32 for Q8_0)
-    int32_t rows_per_tile; // rows one 256-thread workgroup computes
-    int32_t tile0;         // first tile index of this descriptor
+    int32_t rows_per_tile; // rows per tile (== tr)
+    int32_t tr;            // rows per tile
+    int32_t tile_cap;      // LDS bytes of one tile buffer
     int32_t ntiles;
+    int32_t wg0;           // first workgroup of the launch serving this descriptor
+    int32_t nwg;           // workgroups serving it (grid-stride over tiles)
+    int32_t lds_act;       // bytes of the staged activation row
 };
 
 struct GemvArgs {
     GemvDesc d[QK_GROUP_MAX_DEV];
     int32_t count;
-    int32_t tiles_total;
     int32_t lds_bytes;
     int32_t fused;         // float epilogue family: 1 = AVX2/VNNI
 };
 
 // Fill p / rows_per_tile / nb for a descriptor.
 void gemv_plan(GemvDesc &d);
-hipError_t launch_gemv(GemvArgs &a, int max_grid, hipStream_t s);
+int64_t gemv_max_row_bytes();
+// max_wg: workgroups per descriptor at most (the rest grid-stride).
+hipError_t launch_gemv(GemvArgs &a, int max_wg, hipStream_t s);
 
 hipError_t launch_quantize_q8k(const float *x, int64_t nblocks, uint8_t *xq, hipStream_t s);
 hipError_t launch_quantize_q8_0(const float *x, int64_t nblocks, uint8_t *xq, hipStream_t s);
 hipError_t launch_dequant(int type, const uint8_t *w, int64_t nblocks, float *y, hipStream_t s);
 
 // LM head: Q6_K GEMV -> logits, then exact argmax / top-k selection.
-// cand must hold lmhead_cand_bytes(n, topk) bytes.
+// scratch must hold lmhead_cand_bytes(n, topk) bytes.
 size_t lmhead_cand_bytes(int64_t n, int topk);
 hipError_t launch_lmhead(const uint8_t *w, int64_t n, int64_t k, const uint8_t *xq, int topk,
                          float *logits, int32_t *argmax, int32_t *topk_idx, float *topk_val,
-                         void *cand, int fused, hipStream_t s);
+                         void *scratch, int fused, hipStream_t s);
 
 // Prefill GEMM (int8 MFMA); y[t*n + j].
 hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, const uint8_t *xq,

@@ -55,6 +55,21 @@ def _dp(t):
     return C.c_void_p(0 if t is None else t.data_ptr())
 
 
+def _nbytes(t):
+    return t.numel() * t.element_size()
+
+
+def _need(t, nbytes, what):
+    """Refuse a launch whose buffer is smaller than the shape implies (the
+    C ABI takes raw pointers and cannot check this itself)."""
+    if t is not None and _nbytes(t) < nbytes:
+        raise ValueError(f"{what}: buffer of {_nbytes(t)} bytes, shape needs {nbytes}")
+
+
+def row_bytes(wtype, k):
+    return (k // BLOCK_ELEMS[wtype]) * BLOCK_BYTES[wtype] if k % BLOCK_ELEMS[wtype] == 0 else 0
+
+
 class QK:
     """libqk.so. Device-layer methods take torch CUDA tensors."""
 
@@ -126,6 +141,7 @@ class QK:
         m, k = x.shape
         if out is None:
             out = torch.empty((m, (k // 256) * Q8K_BYTES), dtype=torch.uint8, device=x.device)
+        _need(out, m * (k // 256) * Q8K_BYTES, "xq")
         self._ck(self.L.hip_quantize_q8k(_dp(x), m, k, _dp(out), self._stream()))
         return out
 
@@ -134,6 +150,7 @@ class QK:
         m, k = x.shape
         if out is None:
             out = torch.empty((m, (k // 32) * 34), dtype=torch.uint8, device=x.device)
+        _need(out, m * (k // 32) * 34, "xq")
         self._ck(self.L.hip_quantize_q8_0(_dp(x), m, k, _dp(out), self._stream()))
         return out
 
@@ -146,6 +163,9 @@ class QK:
             y = torch.empty(n, dtype=torch.float32, device=w.device)
         f = {Q4_K: self.L.hip_matvec_q4k, Q5_K: self.L.hip_matvec_q5k,
              Q6_K: self.L.hip_matvec_q6k, Q8_0: self.L.hip_matvec_q8_0}[wtype]
+        _need(w, n * row_bytes(wtype, k), "w")
+        _need(xq, act_bytes(wtype, k), "xq")
+        _need(y, 4 * n, "y")
         self._ck(f(_dp(w), n, k, _dp(xq), _dp(y), self._stream()))
         return y
 
@@ -153,6 +173,9 @@ class QK:
         """items: list of (wtype, w, n, k, xq, y) with device tensors."""
         arr = (GemvDesc * len(items))()
         for i, (t, w, n, k, xq, y) in enumerate(items):
+            _need(w, n * row_bytes(t, k), "w")
+            _need(xq, act_bytes(t, k), "xq")
+            _need(y, 4 * n, "y")
             arr[i] = GemvDesc(t, 0, n, k, w.data_ptr(), xq.data_ptr(), y.data_ptr())
         self._ck(self.L.hip_matvec_group(arr, len(items), self._stream()))
 
@@ -161,6 +184,9 @@ class QK:
         if y is None:
             y = torch.empty((m, n), dtype=torch.float32, device=w.device)
         f = {Q4_K: self.L.hip_matmul_q4k, Q5_K: self.L.hip_matmul_q5k, Q6_K: self.L.hip_matmul_q6k}[wtype]
+        _need(w, n * row_bytes(wtype, k), "w")
+        _need(xq, m * act_bytes(wtype, k), "xq")
+        _need(y, 4 * m * n, "y")
         self._ck(f(_dp(w), n, k, _dp(xq), m, _dp(y), self._stream()))
         return y
 
@@ -169,6 +195,8 @@ class QK:
         if y is None:
             y = torch.empty(nblocks * 256, dtype=torch.float32, device=w.device)
         f = {Q4_K: self.L.hip_dequant_q4k, Q5_K: self.L.hip_dequant_q5k, Q6_K: self.L.hip_dequant_q6k}[wtype]
+        _need(w, nblocks * BLOCK_BYTES[wtype], "w")
+        _need(y, 4 * 256 * nblocks, "y")
         self._ck(f(_dp(w), nblocks, _dp(y), self._stream()))
         return y
 
@@ -177,6 +205,9 @@ class QK:
         dev = w.device
         if logits is None and want_logits:
             logits = torch.empty(n, dtype=torch.float32, device=dev)
+        _need(w, n * row_bytes(Q6_K, k), "w")
+        _need(xq, act_bytes(Q6_K, k), "xq")
+        _need(logits, 4 * n, "logits")
         am = torch.empty(1, dtype=torch.int32, device=dev)
         ti = torch.empty(max(topk, 1), dtype=torch.int32, device=dev)
         tv = torch.empty(max(topk, 1), dtype=torch.float32, device=dev)

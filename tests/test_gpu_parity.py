@@ -123,7 +123,7 @@ def test_quantize_then_matvec_on_device(lib, orc):
 
 # ---- LM head ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("n,k,topk", [(248320, 1024, 40), (31040, 1024, 40), (5000, 512, 256), (77, 256, 1)])
+@pytest.mark.parametrize("n,k,topk", [(248320, 1024, 40), (31040, 1024, 40), (5000, 512, 256), (77, 256, 1), (300, 256, 200), (9000, 256, 64)])
 def test_lmhead_argmax_topk(lib, orc, n, k, topk):
     step(f"lmhead n={n} k={k} topk={topk}")
     w = synth.blocks(14, n, k, seed=2)
@@ -189,16 +189,41 @@ def test_lmhead_host_seam(lib, orc):
 # ---- argument checks ---------------------------------------------------------------------
 
 def test_rejects_bad_shapes(lib):
+    # the C ABI's own checks, called directly: every call is rejected on the
+    # host before any launch
+    import ctypes as C
     import torch
     w = torch.zeros(144 * 4, dtype=torch.uint8, device="cuda")
     xq = torch.zeros(292 * 4, dtype=torch.uint8, device="cuda")
     y = torch.zeros(4, dtype=torch.float32, device="cuda")
-    with pytest.raises(qk.QKError) as e:
-        lib.matvec(12, w, 4, 1000, xq, y)              # k % 256
-    assert e.value.rc == 1
-    with pytest.raises(qk.QKError):
-        lib.matvec(12, w[1:], 1, 256, xq, y)           # misaligned weights
-    with pytest.raises(qk.QKError):
-        lib.matvec(12, w, 1, 32768, xq, y)             # k above the LDS stage
-    with pytest.raises(qk.QKError):
-        lib.lmhead(w, 4, 256, xq, topk=5)              # topk > n
+    wp, xp, yp = C.c_void_p(w.data_ptr()), C.c_void_p(xq.data_ptr()), C.c_void_p(y.data_ptr())
+    L = lib.L
+    assert L.hip_matvec_q4k(wp, 4, 1000, xp, yp, None) == 1          # k % 256
+    assert L.hip_matvec_q4k(C.c_void_p(w.data_ptr() + 1), 1, 256, xp, yp, None) == 1   # misaligned
+    assert L.hip_matvec_q4k(wp, 1, 32768, xp, yp, None) == 1         # k above the LDS stage
+    assert L.hip_matvec_q8_0(wp, 1, 32768, xp, yp, None) == 1
+    assert L.hip_matvec_q4k(wp, 0, 256, xp, yp, None) == 1           # empty
+    assert L.hip_matvec_q4k(None, 1, 256, xp, yp, None) == 1         # null
+    am = torch.zeros(1, dtype=torch.int32, device="cuda")
+    assert L.hip_lmhead_q6k_argmax_topk(wp, 4, 256, xp, 5, yp, C.c_void_p(am.data_ptr()), None, None, None) == 1
+    assert L.hip_matmul_q4k(wp, 4, 256, xp, 0, yp, None) == 1        # m = 0
+    assert "k=" in lib.last_error() or "m=" in lib.last_error()
+    with pytest.raises(ValueError):                                   # binding's size guard
+        lib.matvec(12, w, 8, 256, xq, y)
+
+
+def test_lmhead_topk_flat_logits_fallback(lib, orc):
+    # identical rows: every logit ties, far more than the candidate buffer
+    # passes the filter and the exact fallback runs; ties go to low rows
+    step("lmhead top-k fallback")
+    n, k, topk = 20000, 256, 10
+    row = synth.blocks(14, 1, k, seed=6)
+    w = np.repeat(row, n, axis=0)
+    xq = orc.quantize_q8k(synth.activations(1, k, seed=6))
+    logits, am, ti, tv = lib.lmhead(dev(w), n, k, dev(xq[0]), topk=topk)
+    want = orc.matmul_xq(14, w, n, k, xq, 1, oracle.TIER_EPI[lib.tier()])[0]
+    assert_bits_equal(host(logits), want, "logits")
+    assert int(host(am)[0]) == 0
+    np.testing.assert_array_equal(host(ti), np.arange(topk))
+    ri, _ = orc.topk_collect(want, topk)
+    assert set(ri.tolist()) == set(range(topk))
