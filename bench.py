@@ -32,6 +32,12 @@ CONFIG1 = [(12, 3584, 1024), (12, 3584, 1024), (14, 1024, 3584), (13, 2048, 1024
            (13, 512, 1024), (13, 1024, 2048), (8, 1024, 1024)]
 HBM_PEAK_GBS = 8000.0
 MALL_DEFEAT_BYTES = 512 << 20
+# HBM bytes per config-1 launch of the current k_gemv, from rocprofv3 --pmc
+# FETCH_SIZE and WRITE_SIZE runs of this script (--copy-probe 256), each
+# scaled by its reading for a known-size copy / fill (FETCH x2.000,
+# WRITE x1.000); the runs are recorded in profiles/k_gemv_decode_set_lmhead.md.
+# None when the kernel has changed since the last counter run.
+CONFIG1_TRAFFIC_BYTES = 11_796_224 + 350_208
 
 
 def _load(rel, name):
@@ -97,10 +103,10 @@ def bench_config1(torch, qk, synth, lib, steps, warmup):
             arr[i] = qk.GemvDesc(t, 0, n, k, w.data_ptr(), xq.data_ptr(), y.data_ptr())
         descs.append(arr)
     stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    fn = lib.L.hip_matvec_group
 
     def step(i):
-        rc = lib.L.hip_matvec_group(descs[i % copies], len(CONFIG1), stream)
-        if rc:
+        if fn(descs[i % copies], len(CONFIG1), stream):
             raise RuntimeError(lib.last_error())
 
     secs = Events(torch).time(step, steps, warmup)
@@ -115,7 +121,18 @@ def bench_config0(torch, qk, synth, lib, steps, warmup):
     ws = [w] + [w.clone() for _ in range(copies - 1)]
     xq = lib.quantize_q8k(torch.from_numpy(synth.activations(1, k, seed=0)).cuda())[0]
     y = torch.empty(n, dtype=torch.float32, device="cuda")
-    secs = Events(torch).time(lambda i: lib.matvec(t, ws[i % copies], n, k, xq, y), steps, warmup)
+    # direct C calls with prebuilt pointers: a 2 MB GEMV is shorter than
+    # the binding's Python-side checks
+    wp = [C.c_void_p(x.data_ptr()) for x in ws]
+    xp, yp = C.c_void_p(xq.data_ptr()), C.c_void_p(y.data_ptr())
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    fn = lib.L.hip_matvec_q4k
+
+    def step(i):
+        if fn(wp[i % copies], n, k, xp, yp, stream):
+            raise RuntimeError(lib.last_error())
+
+    secs = Events(torch).time(step, steps, warmup)
     return per, copies, secs
 
 
@@ -167,6 +184,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first run 8 plain device copies of MIB MiB each: the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: the quantized GEMV path runs on a single MI355X "
@@ -176,20 +196,27 @@ def main():
     qk = _load("qwen.haiku_amd/qk.py", "qk_binding")
     synth = _load("qwen.haiku_amd/synth.py", "qk_synth")
     lib = qk.QK().init(0)
+    if a.copy_probe > 0:
+        src = torch.ones(a.copy_probe << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(8):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     per, copies, secs = bench_config1(torch, qk, synth, lib, a.steps, a.warmup)
     gbs = per * a.steps / secs / 1e9
     us = secs / a.steps * 1e6
     out = {
-        "metric": "k-quant GEMV GB/s (decode-step GEMV set, config 1)",
+        "metric": "k-quant GEMV GB/s (% of 8 TB/s); prefill int8 TOPS; decode tok/s",
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(us / 1e3, 6), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "int8xq4/q5/q6/q8 (int32 acc, fp32 epilogue)", "data": "synthetic",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": "config1 decode GEMV set: Q4_K 3584x1024 x2, Q6_K 1024x3584, "
                                "Q5_K 2048x1024/512x1024/1024x2048, Q8_0 1024x1024, batch 1",
                    "weight_copies": copies, "bytes_per_step": per, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": CONFIG1_TRAFFIC_BYTES,
                      "kernel": "k_gemv<true> (one launch per step)", "us_per_launch": round(us, 3)},
         "tier": lib.tier_label(),
     }
