@@ -149,6 +149,38 @@ def bench_config2(torch, qk, synth, lib, steps, warmup):
     return per, copies, secs
 
 
+def bench_config3(torch, qk, synth, lib, steps, warmup, wtype=12, n=3584, k=1024, m=512):
+    """Chunked-prefill GEMM (int8 MFMA): xq resident, y fp32. Weight and
+    output buffers rotate through > 512 MB so each step reads its weights
+    from HBM and writes its outputs to fresh lines. Returns (seconds for
+    the GEMM alone, seconds for quantize + GEMM from fp32 x)."""
+    per = n * (k // 256) * qk.BLOCK_BYTES[wtype] + 4 * m * n
+    copies = max(2, -(-MALL_DEFEAT_BYTES // per))
+    w = torch.from_numpy(synth.blocks(wtype, n, k, seed=0)).cuda()
+    ws = [w] + [w.clone() for _ in range(copies - 1)]
+    ys = [torch.empty((m, n), dtype=torch.float32, device="cuda") for _ in range(copies)]
+    x = torch.from_numpy(synth.activations(m, k, seed=0)).cuda()
+    xq = lib.quantize_q8k(x)
+    fn = {12: lib.L.hip_matmul_q4k, 13: lib.L.hip_matmul_q5k, 14: lib.L.hip_matmul_q6k}[wtype]
+    wp = [C.c_void_p(t.data_ptr()) for t in ws]
+    yp = [C.c_void_p(t.data_ptr()) for t in ys]
+    xp, xqp = C.c_void_p(x.data_ptr()), C.c_void_p(xq.data_ptr())
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    quant = lib.L.hip_quantize_q8k
+
+    def gemm(i):
+        if fn(wp[i % copies], n, k, xqp, m, yp[i % copies], stream):
+            raise RuntimeError(lib.last_error())
+
+    def both(i):
+        if quant(xp, m, k, xqp, stream):
+            raise RuntimeError(lib.last_error())
+        gemm(i)
+
+    ev = Events(torch)
+    return copies, ev.time(gemm, steps, warmup), ev.time(both, steps, warmup)
+
+
 def cpu_baseline(synth, seconds=10.0):
     """The reference's tensor_matmul_*_f32 (one core, as shipped) over the
     config-1 set, repeated for a bounded time."""
@@ -229,6 +261,20 @@ def main():
         p2, c2, s2 = bench_config2(torch, qk, synth, lib, st2, 5)
         extra["config2_lmhead_q6k_argmax_top40"] = {"GB/s": round(p2 * st2 / s2 / 1e9, 2),
                                                     "us_per_call": round(s2 / st2 * 1e6, 3), "copies": c2}
+        for (t, n3, k3, m3) in ((12, 3584, 1024, 512), (12, 3584, 1024, 128), (12, 3584, 1024, 2048),
+                                (14, 1024, 3584, 512)):
+            st3 = max(20, a.steps // 10)
+            c3, sg, sb = bench_config3(torch, qk, synth, lib, st3, 10, t, n3, k3, m3)
+            ops = 2.0 * m3 * n3 * k3
+            xbytes = 4 * m3 * k3
+            alg = xbytes + n3 * (k3 // 256) * qk.BLOCK_BYTES[t] + 4 * m3 * n3
+            name = {12: "q4k", 14: "q6k"}[t]
+            extra[f"config3_gemm_{name}_m{m3}_n{n3}_k{k3}"] = {
+                "TOPS_gemm": round(ops * st3 / sg / 1e12, 2), "us_gemm": round(sg / st3 * 1e6, 3),
+                "TOPS_with_quantize": round(ops * st3 / sb / 1e12, 2), "us_with_quantize": round(sb / st3 * 1e6, 3),
+                "frac_of_5POPS": round(ops * st3 / sb / 5.0e15, 4),
+                "frac_of_bw_x_ai": round((ops * st3 / sb) / (HBM_PEAK_GBS * 1e9 * ops / alg), 4),
+                "copies": c3}
         out["extra"] = extra
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(synth, a.cpu_seconds)

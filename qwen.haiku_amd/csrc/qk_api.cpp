@@ -171,7 +171,7 @@ int matmul(int type, const void *w, int64_t n, int64_t k, const void *xq, int64_
     int rc = require_init();
     if (rc) return rc;
     if ((rc = check_mat(type, w, n, k, xq, y))) return rc;
-    if (m < 1) return fail(QK_ERR_ARG, "m=%lld tokens", (long long)m);
+    if (m < 1 || m > 65535LL * 64) return fail(QK_ERR_ARG, "m=%lld tokens (1..%lld)", (long long)m, 65535LL * 64);
     if (type == QK_TYPE_Q8_0) return fail(QK_ERR_UNSUPPORTED, "no Q8_0 GEMM; use hip_matvec_q8_0 per token");
     HIP_OK(qk::launch_gemm(type, static_cast<const uint8_t *>(w), n, k,
                            static_cast<const uint8_t *>(xq), m, y, fused_of(st().tier), stream_of(s)),

@@ -121,6 +121,45 @@ def test_quantize_then_matvec_on_device(lib, orc):
     assert_bits_equal(got, want, "config 0")
 
 
+# ---- chunked-prefill GEMM ------------------------------------------------------------
+
+GEMM_SHAPES = [
+    (12, 3584, 1024, 512), (12, 3584, 1024, 128), (14, 1024, 3584, 512),    # config 3
+    (13, 2048, 1024, 96), (13, 1024, 2048, 33),
+    (12, 100, 768, 37), (13, 65, 256, 1), (14, 63, 512, 65), (14, 129, 1280, 7),
+    (12, 64, 256, 64), (12, 1, 512, 3),
+]
+
+
+@pytest.mark.parametrize("wtype,n,k,m", GEMM_SHAPES)
+@pytest.mark.parametrize("epi,t", EPI_TIERS)
+def test_matmul_gemm(tier, orc, wtype, n, k, m, epi, t):
+    lib = tier
+    step(f"matmul type={wtype} n={n} k={k} m={m} tier={t}")
+    lib.set_tier(t)
+    w = synth.blocks(wtype, n, k, seed=m, tag=wtype)
+    x = synth.activations(m, k, seed=m + 1)
+    if m >= 4:
+        x[1:4] = edge_rows(k)[[0, 6, 7]]               # zero / huge / subnormal rows
+    xq = orc.quantize_q8k(x)
+    got = host(lib.matmul(wtype, dev(w), n, k, dev(xq), m))
+    want = orc.matmul_xq(wtype, w, n, k, xq, m, epi)
+    assert_bits_equal(got, want, f"gemm {wtype} {m}x{n}x{k}")
+
+
+def test_matmul_gemm_m2048(lib, orc):
+    step("matmul config 3 M=2048")
+    n, k, m = 3584, 1024, 2048
+    w = synth.blocks(12, n, k, seed=0)
+    x = synth.activations(m, k, seed=0)
+    xq = lib.quantize_q8k(dev(x))
+    got = host(lib.matmul(12, dev(w), n, k, xq, m))
+    # every 7th token row against the oracle (row dots are independent)
+    sel = np.arange(0, m, 7)
+    want = orc.matmul(12, w, n, k, x[sel], oracle.TIER_EPI[lib.tier()])
+    assert_bits_equal(got[sel], want, "gemm M=2048")
+
+
 # ---- LM head ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("n,k,topk", [(248320, 1024, 40), (31040, 1024, 40), (5000, 512, 256), (77, 256, 1), (300, 256, 200), (9000, 256, 64)])
@@ -163,7 +202,8 @@ def test_lmhead_argmax_ties_and_nan(lib, orc):
 # ---- host seam ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("wtype,n,k,m", [(12, 3584, 1024, 1), (13, 512, 1024, 1), (14, 1024, 3584, 1),
-                                          (8, 1024, 1024, 1), (8, 64, 1024, 21)])
+                                          (8, 1024, 1024, 1), (8, 64, 1024, 21), (12, 3584, 1024, 64),
+                                          (13, 512, 1024, 21), (14, 1024, 3584, 9)])
 def test_matmul_host_seam(lib, orc, wtype, n, k, m):
     step(f"host seam type={wtype} n={n} k={k} m={m}")
     w = synth.blocks(wtype, n, k, seed=3, tag=wtype)
@@ -207,6 +247,7 @@ def test_rejects_bad_shapes(lib):
     am = torch.zeros(1, dtype=torch.int32, device="cuda")
     assert L.hip_lmhead_q6k_argmax_topk(wp, 4, 256, xp, 5, yp, C.c_void_p(am.data_ptr()), None, None, None) == 1
     assert L.hip_matmul_q4k(wp, 4, 256, xp, 0, yp, None) == 1        # m = 0
+    assert L.hip_matmul_q4k(wp, 4, 1000, xp, 2, yp, None) == 1       # k % 256
     assert "k=" in lib.last_error() or "m=" in lib.last_error()
     with pytest.raises(ValueError):                                   # binding's size guard
         lib.matvec(12, w, 8, 256, xq, y)
