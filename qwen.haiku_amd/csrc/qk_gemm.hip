@@ -18,7 +18,9 @@
 // output tile and walks the super-blocks of K in order. For each one it
 // stages the 64 activation rows (int8 Q8_K quants, scale, bsum pairs)
 // and the 64 weight rows, dequantised to int8 with their sub-block
-// scales, into LDS; each of the 4 waves then computes a 32x32 sub-tile:
+// scales, into LDS (the next super-block's raw bytes are loaded into
+// registers meanwhile); each of the 4 waves then computes a 32x32
+// sub-tile:
 //
 //  * Q4_K / Q5_K: one v_mfma_i32_32x32x32_i8 per 32-element sub-block
 //    (weights 0..15 / 0..31), times the 6-bit scale; mins from the Q8_K
@@ -46,8 +48,8 @@ typedef int32_t v16i __attribute__((ext_vector_type(16)));
 struct __attribute__((aligned(16))) GemmLds {
     int8_t a[GM_BM][GM_LD];           // activation quants of the super-block
     int8_t b[GM_BN][GM_LD];           // dequantised int8 weights
+    int8_t am[GM_BM][16];             // bsum pairs p = 128*hi + lo: lo[8] (0..127) | hi[8] (-64..63)
     float yd[GM_BM];                  // Q8_K d per token
-    int16_t bp[GM_BM][8];             // bsum pairs (bsums[2j] + bsums[2j+1])
     int8_t sc[GM_BN][16];             // sub-block scales per weight row
     uint8_t mn[GM_BN][8];             // 6-bit mins (Q4_K / Q5_K)
     float wd[GM_BN];                  // fp16 d, widened
@@ -58,101 +60,122 @@ __device__ __forceinline__ void lds_st16(void *p, uint32_t a, uint32_t b, uint32
     *(QK_LDS uint4 *)p = make_uint4(a, b, c, d);
 }
 
-// ---- activation stage: tokens [t0, t0+64) of super-block i ---------------
-__device__ __forceinline__ void stage_act(GemmLds &s, const uint8_t *__restrict__ xq, int64_t m, int nb,
-                                          int64_t t0, int i) {
-    for (int idx = threadIdx.x; idx < GM_BM * 73; idx += 256) {
-        const int t = idx / 73, r = idx - t * 73;
-        uint32_t v = 0;
-        if (t0 + t < m) v = ld32(xq + ((t0 + t) * nb + i) * Q8K_BYTES + 4 * r);
-        if (r == 0) {
-            s.yd[t] = __uint_as_float(v);
-        } else if (r <= 64) {
-            *(QK_LDS uint32_t *)&s.a[t][4 * (r - 1)] = v;
-        } else {
-            s.bp[t][r - 65] = (int16_t)((int32_t)(int16_t)(v & 0xffffu) + (int32_t)(int16_t)(v >> 16));
-        }
-    }
-}
+// ---- staging ---------------------------------------------------------------
+// Each super-block step moves its raw bytes in two halves: load_*() issues
+// every global load of the step into registers, and store_*() unpacks
+// those registers into LDS; the kernel loads step i+1 while it computes
+// step i. Thread tid works on token / weight row tid/4 and quarter
+// q = tid%4 of it, so all of a thread's loads in a step are immediate
+// offsets from one row pointer computed once per kernel.
 
-// ---- weight stage: rows [r0, r0+64) of super-block i, dequantised ---------
-// Q4_K (144 B = 9 x 16 B): piece 0 is d | dmin | scales, pieces 1..8 are
-// qs; qs[32c + l] low nibble -> element 64c + l, high -> 64c + 32 + l.
-__device__ __forceinline__ void stage_w_q4k(GemmLds &s, const uint8_t *__restrict__ w, int64_t n, int nb,
-                                            int64_t r0, int i) {
-    for (int idx = threadIdx.x; idx < GM_BN * 9; idx += 256) {
-        const int r = idx / 9, p = idx - r * 9;
-        const bool ok = r0 + r < n;
-        const uint8_t *blk = w + ((r0 + r) * nb + i) * Q4K_BYTES;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (ok) v = ld16(blk + 16 * p);
-        if (p == 0) {
-            int32_t sc, mm;
+// Activations: the thread holds dwords q, q+4, ..., q+72 (those < 73) of
+// its token's 292-byte Q8_K block (d | 64 dwords of qs | 8 dwords of
+// bsums).
+struct ActRaw { uint32_t v[19]; };
+
+__device__ __forceinline__ void load_act(ActRaw &a, const uint8_t *row, int q, int i) {
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                scale_min(v.y, v.z, v.w, j, sc, mm);
-                s.sc[r][j] = (int8_t)sc;
-                s.mn[r][j] = (uint8_t)mm;
-            }
-            s.wd[r] = h2f(v.x & 0xffffu);
-            s.wdm[r] = h2f(v.x >> 16);
-        } else {
-            const int c = (p - 1) >> 1, l0 = 16 * ((p - 1) & 1);
-            const uint32_t M = 0x0F0F0F0Fu;
-            lds_st16(&s.b[r][64 * c + l0], v.x & M, v.y & M, v.z & M, v.w & M);
-            lds_st16(&s.b[r][64 * c + 32 + l0], (v.x >> 4) & M, (v.y >> 4) & M, (v.z >> 4) & M, (v.w >> 4) & M);
-        }
-    }
-}
-
-// Q5_K (176 B = 11 x 16 B): piece 0 header, pieces 1-2 qh[32], pieces
-// 3..10 qs. Element 64c + l gets bit 2c of qh[l] as its 5th bit, element
-// 64c + 32 + l bit 2c+1.
-__device__ __forceinline__ void stage_w_q5k(GemmLds &s, const uint8_t *__restrict__ w, int64_t n, int nb,
-                                            int64_t r0, int i) {
-    for (int idx = threadIdx.x; idx < GM_BN * 9; idx += 256) {
-        const int r = idx / 9, p = idx - r * 9;
-        const bool ok = r0 + r < n;
-        const uint8_t *blk = w + ((r0 + r) * nb + i) * Q5K_BYTES;
-        if (p == 0) {
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (ok) v = ld16(blk);
-            int32_t sc, mm;
+    for (int j = 0; j < 19; j++) a.v[j] = 0;
+    if (!row) return;
+    const uint8_t *p = row + (int64_t)i * Q8K_BYTES;
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                scale_min(v.y, v.z, v.w, j, sc, mm);
-                s.sc[r][j] = (int8_t)sc;
-                s.mn[r][j] = (uint8_t)mm;
-            }
-            s.wd[r] = h2f(v.x & 0xffffu);
-            s.wdm[r] = h2f(v.x >> 16);
-        } else {
-            const int c = (p - 1) >> 1, half = (p - 1) & 1, l0 = 16 * half;
-            uint4 q = make_uint4(0, 0, 0, 0), h = make_uint4(0, 0, 0, 0);
-            if (ok) {
-                q = ld16(blk + 48 + 16 * (p - 1));
-                h = ld16(blk + 16 + 16 * half);
-            }
-            const uint32_t M = 0x0F0F0F0Fu, B1 = 0x01010101u;
-            const uint32_t s0 = 2 * c, s1 = 2 * c + 1;
-            lds_st16(&s.b[r][64 * c + l0], (q.x & M) | (((h.x >> s0) & B1) << 4), (q.y & M) | (((h.y >> s0) & B1) << 4),
-                     (q.z & M) | (((h.z >> s0) & B1) << 4), (q.w & M) | (((h.w >> s0) & B1) << 4));
-            lds_st16(&s.b[r][64 * c + 32 + l0], ((q.x >> 4) & M) | (((h.x >> s1) & B1) << 4),
-                     ((q.y >> 4) & M) | (((h.y >> s1) & B1) << 4), ((q.z >> 4) & M) | (((h.z >> s1) & B1) << 4),
-                     ((q.w >> 4) & M) | (((h.w >> s1) & B1) << 4));
-        }
+    for (int j = 0; j < 18; j++) a.v[j] = ld32(p + 16 * j);
+    if (q == 0) a.v[18] = ld32(p + 288);
+}
+
+// bsum pair j (bsums[2j] + bsums[2j+1], one dword of the block) as two
+// int8 digits of the mins operand.
+__device__ __forceinline__ void store_pair(GemmLds &s, int t, int j, uint32_t v) {
+    const int32_t p = (int32_t)(int16_t)(v & 0xffffu) + (int32_t)(int16_t)(v >> 16);
+    s.am[t][j] = (int8_t)(p & 127);
+    s.am[t][8 + j] = (int8_t)(p >> 7);
+}
+
+__device__ __forceinline__ void store_act(GemmLds &s, const ActRaw &a, int t, int q) {
+    // dword r = q + 4j: r = 0 is d, 1..64 the quants, 65..72 the bsums
+    if (q == 0) s.yd[t] = __uint_as_float(a.v[0]);
+    else *(QK_LDS uint32_t *)&s.a[t][4 * q - 4] = a.v[0];
+#pragma unroll
+    for (int j = 1; j < 16; j++) *(QK_LDS uint32_t *)&s.a[t][4 * q + 16 * j - 4] = a.v[j];
+    if (q == 0) {
+        *(QK_LDS uint32_t *)&s.a[t][252] = a.v[16];
+        store_pair(s, t, 3, a.v[17]);
+        store_pair(s, t, 7, a.v[18]);
+    } else {
+        store_pair(s, t, q - 1, a.v[16]);
+        store_pair(s, t, 3 + q, a.v[17]);
     }
 }
 
-// 16 bytes at a 2-byte aligned address inside a block, read as five
-// aligned dwords and funnel-shifted (the last dword read ends at most 4
-// bytes past the 16, which callers keep inside the block).
-__device__ __forceinline__ uint4 ld16_a2(const uint8_t *p) {
-    const uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(p) & 3u;
-    const uint8_t *a = p - sh;
-    const uint32_t d0 = ld32(a), d1 = ld32(a + 4), d2 = ld32(a + 8), d3 = ld32(a + 12), d4 = ld32(a + 16);
-    return make_uint4(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
-                      __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh));
+// Scales and mins of a Q4_K / Q5_K header (d | dmin | scales[12]).
+__device__ __forceinline__ void store_kq_header(GemmLds &s, int r, const uint4 v) {
+    int32_t sc, mm;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        scale_min(v.y, v.z, v.w, j, sc, mm);
+        s.sc[r][j] = (int8_t)sc;
+        s.mn[r][j] = (uint8_t)mm;
+    }
+    s.wd[r] = h2f(v.x & 0xffffu);
+    s.wdm[r] = h2f(v.x >> 16);
+}
+
+// Q4_K (144 B): header | qs[128]; qs[32c + l] low nibble is element
+// 64c + l, high nibble 64c + 32 + l. Quarter q takes the 16-byte qs
+// pieces q and q+4 (chunk c = q/2 and 2 + q/2, positions 16(q&1)..+16);
+// quarter 0 also the header.
+struct WRaw12 { uint4 hdr, p0, p1; };
+
+__device__ __forceinline__ void load_w(WRaw12 &a, const uint8_t *row, int q, int i) {
+    a.hdr = a.p0 = a.p1 = make_uint4(0, 0, 0, 0);
+    if (!row) return;
+    const uint8_t *p = row + (int64_t)i * Q4K_BYTES;
+    if (q == 0) a.hdr = ld16(p);
+    a.p0 = ld16(p + 16 + 16 * q);
+    a.p1 = ld16(p + 80 + 16 * q);
+}
+
+__device__ __forceinline__ void store_nibbles(GemmLds &s, int r, int c, int l0, const uint4 v) {
+    const uint32_t M = 0x0F0F0F0Fu;
+    lds_st16(&s.b[r][64 * c + l0], v.x & M, v.y & M, v.z & M, v.w & M);
+    lds_st16(&s.b[r][64 * c + 32 + l0], (v.x >> 4) & M, (v.y >> 4) & M, (v.z >> 4) & M, (v.w >> 4) & M);
+}
+
+__device__ __forceinline__ void store_w(GemmLds &s, const WRaw12 &a, int r, int q) {
+    if (q == 0) store_kq_header(s, r, a.hdr);
+    store_nibbles(s, r, q >> 1, 16 * (q & 1), a.p0);
+    store_nibbles(s, r, 2 + (q >> 1), 16 * (q & 1), a.p1);
+}
+
+// Q5_K (176 B): header | qh[32] | qs[128]. Element 64c + l gets bit 2c of
+// qh[l] as its 5th bit, element 64c + 32 + l bit 2c+1; quarter q needs the
+// qh bytes of its positions 16(q&1)..+16.
+struct WRaw13 { uint4 hdr, p0, p1, qh; };
+
+__device__ __forceinline__ void load_w(WRaw13 &a, const uint8_t *row, int q, int i) {
+    a.hdr = a.p0 = a.p1 = a.qh = make_uint4(0, 0, 0, 0);
+    if (!row) return;
+    const uint8_t *p = row + (int64_t)i * Q5K_BYTES;
+    if (q == 0) a.hdr = ld16(p);
+    a.qh = ld16(p + 16 + 16 * (q & 1));
+    a.p0 = ld16(p + 48 + 16 * q);
+    a.p1 = ld16(p + 112 + 16 * q);
+}
+
+__device__ __forceinline__ void store_nibbles5(GemmLds &s, int r, int c, int l0, const uint4 q, const uint4 h) {
+    const uint32_t M = 0x0F0F0F0Fu, B1 = 0x01010101u;
+    const uint32_t s0 = 2 * c, s1 = 2 * c + 1;
+    lds_st16(&s.b[r][64 * c + l0], (q.x & M) | (((h.x >> s0) & B1) << 4), (q.y & M) | (((h.y >> s0) & B1) << 4),
+             (q.z & M) | (((h.z >> s0) & B1) << 4), (q.w & M) | (((h.w >> s0) & B1) << 4));
+    lds_st16(&s.b[r][64 * c + 32 + l0], ((q.x >> 4) & M) | (((h.x >> s1) & B1) << 4),
+             ((q.y >> 4) & M) | (((h.y >> s1) & B1) << 4), ((q.z >> 4) & M) | (((h.z >> s1) & B1) << 4),
+             ((q.w >> 4) & M) | (((h.w >> s1) & B1) << 4));
+}
+
+__device__ __forceinline__ void store_w(GemmLds &s, const WRaw13 &a, int r, int q) {
+    if (q == 0) store_kq_header(s, r, a.hdr);
+    store_nibbles5(s, r, q >> 1, 16 * (q & 1), a.p0, a.qh);
+    store_nibbles5(s, r, 2 + (q >> 1), 16 * (q & 1), a.p1, a.qh);
 }
 
 // Four bytes u6 in [0, 63] -> four int8 bytes u6 - 32. u6 ^ 0x20 is
@@ -164,53 +187,77 @@ __device__ __forceinline__ uint32_t u6_minus_32(uint32_t x) {
     return v | (sg << 1) | (sg << 2);
 }
 
-// Q6_K (210 B, 2-byte aligned): element 128h + 32q + l (l < 32) is
-// ql[64h + l + 32(q&1)] (low nibble for q < 2, high for q >= 2) | the
-// 2 bits of qh[32h + l] at 2q, minus 32. A unit (h, l0) covers l0..l0+15 of
-// all four quarters of half h.
-__device__ __forceinline__ void stage_w_q6k(GemmLds &s, const uint8_t *__restrict__ w, int64_t n, int nb,
-                                            int64_t r0, int i) {
-    for (int idx = threadIdx.x; idx < GM_BN * 5; idx += 256) {
-        const int r = idx / 5, u = idx - r * 5;
-        const bool ok = r0 + r < n;
-        const uint8_t *blk = w + ((r0 + r) * nb + i) * Q6K_BYTES;
-        if (u == 4) {
-            uint32_t sw[8], d = 0;
+// Q6_K (210 B, 2-byte aligned): element 128h + 32qq + l (l < 32) is
+// ql[64h + l + 32(qq&1)] (low nibble for qq < 2, high for qq >= 2) | the
+// 2 bits of qh[32h + l] at 2qq, minus 32. Quarter q covers positions
+// l0..l0+15 (l0 = 16(q&1)) of all four quarters of half h = q/2, read as
+// three 16-byte runs, each through the five aligned dwords that contain
+// it (the last ends at most at byte 196 of the block); quarter 0 also
+// reads the scales (eight 2-byte words) and d.
+struct WRaw14 { uint32_t v[15]; uint32_t sc[8]; uint32_t d, sh; };
+
+__device__ __forceinline__ void load_w(WRaw14 &a, const uint8_t *row, int q, int i) {
 #pragma unroll
-            for (int j = 0; j < 8; j++) sw[j] = ok ? ld_u16(blk + 192 + 2 * j) : 0u;
-            if (ok) d = ld_u16(blk + 208);
+    for (int j = 0; j < 15; j++) a.v[j] = 0;
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                s.sc[r][2 * j] = (int8_t)(sw[j] & 0xffu);
-                s.sc[r][2 * j + 1] = (int8_t)(sw[j] >> 8);
-            }
-            s.wd[r] = h2f(d);
-        } else {
-            const int h = u >> 1, l0 = 16 * (u & 1);
-            uint4 qa = make_uint4(0, 0, 0, 0), qb = qa, qh = qa;
-            if (ok) {
-                qa = ld16_a2(blk + 64 * h + l0);         // quarters 0 (low) and 2 (high)
-                qb = ld16_a2(blk + 64 * h + 32 + l0);    // quarters 1 and 3
-                qh = ld16_a2(blk + 128 + 32 * h + l0);
-            }
-            const uint32_t M = 0x0F0F0F0Fu, T = 0x30303030u;
-            const uint32_t a[4] = {qa.x, qa.y, qa.z, qa.w}, b[4] = {qb.x, qb.y, qb.z, qb.w},
-                           hh[4] = {qh.x, qh.y, qh.z, qh.w};
-            uint32_t o0[4], o1[4], o2[4], o3[4];
+    for (int j = 0; j < 8; j++) a.sc[j] = 0;
+    a.d = a.sh = 0;
+    if (!row) return;
+    const uint8_t *blk = row + (int64_t)i * Q6K_BYTES;
+    const int h = q >> 1, l0 = 16 * (q & 1);
+    const uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(blk) & 3u;
+    a.sh = sh;
+    const uint8_t *p0 = blk - sh + 64 * h + l0, *p2 = blk - sh + 128 + 32 * h + l0;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                o0[k] = u6_minus_32((a[k] & M) | ((hh[k] << 4) & T));
-                o1[k] = u6_minus_32((b[k] & M) | ((hh[k] << 2) & T));
-                o2[k] = u6_minus_32(((a[k] >> 4) & M) | (hh[k] & T));
-                o3[k] = u6_minus_32(((b[k] >> 4) & M) | ((hh[k] >> 2) & T));
-            }
-            lds_st16(&s.b[r][128 * h + l0], o0[0], o0[1], o0[2], o0[3]);
-            lds_st16(&s.b[r][128 * h + 32 + l0], o1[0], o1[1], o1[2], o1[3]);
-            lds_st16(&s.b[r][128 * h + 64 + l0], o2[0], o2[1], o2[2], o2[3]);
-            lds_st16(&s.b[r][128 * h + 96 + l0], o3[0], o3[1], o3[2], o3[3]);
-        }
+    for (int j = 0; j < 5; j++) {
+        a.v[j] = ld32(p0 + 4 * j);
+        a.v[5 + j] = ld32(p0 + 32 + 4 * j);
+        a.v[10 + j] = ld32(p2 + 4 * j);
+    }
+    if (q == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) a.sc[j] = ld_u16(blk + 192 + 2 * j);
+        a.d = ld_u16(blk + 208);
     }
 }
+
+__device__ __forceinline__ void store_w(GemmLds &s, const WRaw14 &a, int r, int q) {
+    if (q == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            s.sc[r][2 * j] = (int8_t)(a.sc[j] & 0xffu);
+            s.sc[r][2 * j + 1] = (int8_t)(a.sc[j] >> 8);
+        }
+        s.wd[r] = h2f(a.d);
+    }
+    const int h = q >> 1, l0 = 16 * (q & 1);
+    const uint32_t sh = a.sh;
+    uint32_t qa[4], qb[4], hh[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        qa[k] = __builtin_amdgcn_alignbyte(a.v[k + 1], a.v[k], sh);       // quarters 0 / 2
+        qb[k] = __builtin_amdgcn_alignbyte(a.v[k + 6], a.v[k + 5], sh);   // quarters 1 / 3
+        hh[k] = __builtin_amdgcn_alignbyte(a.v[k + 11], a.v[k + 10], sh);
+    }
+    const uint32_t M = 0x0F0F0F0Fu, T = 0x30303030u;
+    uint32_t o0[4], o1[4], o2[4], o3[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        o0[k] = u6_minus_32((qa[k] & M) | ((hh[k] << 4) & T));
+        o1[k] = u6_minus_32((qb[k] & M) | ((hh[k] << 2) & T));
+        o2[k] = u6_minus_32(((qa[k] >> 4) & M) | (hh[k] & T));
+        o3[k] = u6_minus_32(((qb[k] >> 4) & M) | ((hh[k] >> 2) & T));
+    }
+    lds_st16(&s.b[r][128 * h + l0], o0[0], o0[1], o0[2], o0[3]);
+    lds_st16(&s.b[r][128 * h + 32 + l0], o1[0], o1[1], o1[2], o1[3]);
+    lds_st16(&s.b[r][128 * h + 64 + l0], o2[0], o2[1], o2[2], o2[3]);
+    lds_st16(&s.b[r][128 * h + 96 + l0], o3[0], o3[1], o3[2], o3[3]);
+}
+
+template <int TYPE> struct WRawOf;
+template <> struct WRawOf<12> { typedef WRaw12 T; };
+template <> struct WRawOf<13> { typedef WRaw13 T; };
+template <> struct WRawOf<14> { typedef WRaw14 T; };
 
 // Output element v (0..15) of a lane in a 32x32 MFMA tile: column (weight
 // row) = lane % 32, row (token) = 8*(v/4) + 4*(lane/32) + v%4.
@@ -219,46 +266,62 @@ __device__ __forceinline__ int tok_of(int v, int h) { return 8 * (v >> 2) + 4 * 
 template <int TYPE, bool FUSED>
 __global__ __launch_bounds__(256) void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb,
                                               const uint8_t *__restrict__ xq, int64_t m, float *__restrict__ y) {
+    constexpr int BB = TYPE == 12 ? Q4K_BYTES : (TYPE == 13 ? Q5K_BYTES : Q6K_BYTES);
     __shared__ GemmLds s;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 31, h = lane >> 5;
     const int tm = 32 * (wave >> 1), tn = 32 * (wave & 1);   // wave sub-tile in the workgroup tile
     const int64_t r0 = (int64_t)blockIdx.x * GM_BN, t0 = (int64_t)blockIdx.y * GM_BM;
+    // staging roles: token / weight row st of the tile, quarter sq
+    const int st = threadIdx.x >> 2, sq = threadIdx.x & 3;
+    const uint8_t *xrow = (t0 + st < m) ? xq + (t0 + st) * nb * Q8K_BYTES + 4 * sq : nullptr;
+    const uint8_t *wrow = (r0 + st < n) ? w + (r0 + st) * nb * BB : nullptr;
+
     float sum[16];
 #pragma unroll
     for (int v = 0; v < 16; v++) sum[v] = 0.0f;
+    ActRaw ar;
+    typename WRawOf<TYPE>::T wr;
+    load_act(ar, xrow, sq, 0);
+    load_w(wr, wrow, sq, 0);
+    const int8_t *arow = &s.a[tm + col][0];
+    const int8_t *brow = &s.b[tn + col][0];
+    const v16i zero = {0};
 
     for (int i = 0; i < nb; i++) {
         __syncthreads();                                     // previous super-block's reads done
-        stage_act(s, xq, m, nb, t0, i);
-        if (TYPE == 12) stage_w_q4k(s, w, n, nb, r0, i);
-        else if (TYPE == 13) stage_w_q5k(s, w, n, nb, r0, i);
-        else stage_w_q6k(s, w, n, nb, r0, i);
+        store_act(s, ar, st, sq);
+        store_w(s, wr, st, sq);
+        if (i + 1 < nb) {                                    // next super-block in flight during compute
+            load_act(ar, xrow, sq, i + 1);
+            load_w(wr, wrow, sq, i + 1);
+        }
         __syncthreads();
 
+        // isum = sum over sub-blocks of scale * (exact int8 dot of the sub-block)
         int32_t isum[16];
 #pragma unroll
         for (int v = 0; v < 16; v++) isum[v] = 0;
-        const int8_t *arow = &s.a[tm + col][0];
-        const int8_t *brow = &s.b[tn + col][0];
-        const v16i zero = {0};
         if (TYPE == 14) {
+            const uint4 scp = *(const QK_LDS uint4 *)&s.sc[tn + col][0];
+            const uint32_t scw[4] = {scp.x, scp.y, scp.z, scp.w};
 #pragma unroll
             for (int sb = 0; sb < 16; sb++) {
                 const long av = *(const QK_LDS long *)(arow + 16 * sb + 8 * h);
                 const long bv = *(const QK_LDS long *)(brow + 16 * sb + 8 * h);
                 const v16i d = __builtin_amdgcn_mfma_i32_32x32x16_i8(av, bv, zero, 0, 0, 0);
-                const int32_t scv = s.sc[tn + col][sb];
+                const int32_t scv = (int32_t)(int8_t)(scw[sb >> 2] >> (8 * (sb & 3)));
 #pragma unroll
                 for (int v = 0; v < 16; v++) isum[v] += __mul24(scv, d[v]);
             }
         } else {
+            const uint2 scp = *(const QK_LDS uint2 *)&s.sc[tn + col][0];
 #pragma unroll
             for (int sb = 0; sb < 8; sb++) {
                 const v4i av = *(const QK_LDS v4i *)(arow + 32 * sb + 16 * h);
                 const v4i bv = *(const QK_LDS v4i *)(brow + 32 * sb + 16 * h);
                 const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
-                const int32_t scv = s.sc[tn + col][sb];
+                const int32_t scv = (int32_t)(((sb < 4 ? scp.x : scp.y) >> (8 * (sb & 3))) & 0xffu);
 #pragma unroll
                 for (int v = 0; v < 16; v++) isum[v] += __mul24(scv, d[v]);
             }
@@ -272,21 +335,19 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t *__restrict__ w, int
                 sum[v] = __fadd_rn(sum[v], __fmul_rn(__fmul_rn(wd, yd), (float)isum[v]));
             }
         } else {
+            // isum_mins = sum_j m_j * (bsums[2j] + bsums[2j+1]) as two small
+            // MFMAs: the bsum pairs enter as int8 digits (lo | hi), the mins
+            // sit against the lo half for one product and the hi half for
+            // the other, so mins = lo_product + 128 * hi_product exactly.
+            const long amv = *(const QK_LDS long *)&s.am[tm + col][8 * h];
+            const long mnv = *(const QK_LDS long *)&s.mn[tn + col][0];
+            const v16i dl = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 0 ? mnv : 0L, zero, 0, 0, 0);
+            const v16i dh = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 1 ? mnv : 0L, zero, 0, 0, 0);
             const float wdm = s.wdm[tn + col];
-            int32_t mm[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) mm[j] = s.mn[tn + col][j];
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const int t = tm + tok_of(v, h);
-                const v4i bp = *(const QK_LDS v4i *)&s.bp[t][0];
-                int32_t mins = 0;
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    mins += __mul24(mm[2 * q], (int32_t)(int16_t)(bp[q] & 0xffff));
-                    mins += __mul24(mm[2 * q + 1], (int32_t)(int16_t)((uint32_t)bp[q] >> 16));
-                }
-                const float yd = s.yd[t];
+                const int32_t mins = dl[v] + dh[v] * 128;
+                const float yd = s.yd[tm + tok_of(v, h)];
                 const float d = __fmul_rn(yd, wd);
                 const float dmin = __fmul_rn(yd, wdm);
                 const float pm = __fmul_rn(dmin, (float)mins);
