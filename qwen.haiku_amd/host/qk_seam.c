@@ -1,0 +1,123 @@
+/*
+ * qk_seam.c -- MI355X bodies for qwen.haiku's quantized tensor ops.
+ *
+ * The reference is one C translation unit (slm/slm.c includes model.c,
+ * which includes tensor.c behind the TENSOR_C guard). Including this
+ * file ahead of those includes makes the model's quantized matmuls run on
+ * the GPU with no edit to any reference file:
+ *
+ *   1. the four reference definitions of tensor_matmul_q4k_f32 /
+ *      _q5k_ / _q6k_ / _q8_0_ (slm/tensor.c:827, 898, 1012, 952) are
+ *      compiled under other names by renaming them around
+ *      `#include "tensor.c"`;
+ *   2. the originals' names are then defined here with the same
+ *      signatures, ownership and layout: the result tensor (out_f, n)
+ *      comes from x->arena, out[t*out_f + j] is the row dot of weight
+ *      row j with token t (slm/tensor.c:833-851). The body hands the
+ *      rows to libqk (hip_qk_matmul_host, include/qk.h), which uploads
+ *      each weight matrix once, keyed by its host address (weights are
+ *      borrowed from the GGUF mmap and immutable, slm/model.c:200-205),
+ *      quantizes the activations to Q8_K / Q8_0 on the GPU, runs the
+ *      GEMV (one token) or the int8-MFMA GEMM (a prefill batch) and
+ *      copies the outputs back into the arena tensor.
+ *
+ * The model's later `#include "tensor.c"` is then a no-op, so every
+ * caller of matmul_dispatch (slm/model.c:220-264) reaches these bodies.
+ * The results are bit-identical to the CPU tier this host dispatches to
+ * (simd_init, simd/simd.c:191-229): libqk picks the same tier by CPUID.
+ *
+ * There is no CPU fallback. Like the reference, which abort()s on an
+ * unsupported weight type (slm/model.c:259-261) and assert()s on bad
+ * shapes (slm/tensor.c:831-832), a GPU failure prints libqk's message
+ * and aborts.
+ *
+ * Needs on the include path: the reference's slm/ (for tensor.c) and
+ * this repository's include/ (for qk.h); links against libqk.so.
+ */
+#ifndef QK_SEAM_C
+#define QK_SEAM_C
+
+/* This file opens the translation unit, so it sets the feature-test
+ * macros the reference's TU roots set before any system header
+ * (slm/slm.c:41-50, slm/qwen.c:29-43). */
+#if !defined(__APPLE__)
+#ifndef _POSIX_C_SOURCE
+#define _POSIX_C_SOURCE 200809L
+#endif
+#ifndef _GNU_SOURCE
+#define _GNU_SOURCE
+#endif
+#endif
+
+#define tensor_matmul_q4k_f32  qk_seam_cpu_matmul_q4k_f32
+#define tensor_matmul_q5k_f32  qk_seam_cpu_matmul_q5k_f32
+#define tensor_matmul_q6k_f32  qk_seam_cpu_matmul_q6k_f32
+#define tensor_matmul_q8_0_f32 qk_seam_cpu_matmul_q8_0_f32
+#include "tensor.c"
+#undef tensor_matmul_q4k_f32
+#undef tensor_matmul_q5k_f32
+#undef tensor_matmul_q6k_f32
+#undef tensor_matmul_q8_0_f32
+
+#include "qk.h"
+
+/* Device used by the seam (QK_DEVICE in the environment, default 0);
+ * initialised on the first matmul. */
+static void qk_seam_init(void) {
+    static int done = 0;
+    if (!done) {
+        const char *dev = getenv("QK_DEVICE");
+        int rc = hip_qk_init(dev != NULL ? atoi(dev) : 0);
+        if (rc != QK_OK) {
+            fprintf(stderr, "qk_seam: hip_qk_init failed (%d): %s\n", rc, hip_qk_last_error());
+            abort();
+        }
+        done = 1;
+    }
+}
+
+static struct tensor *qk_seam_matmul(int type, const void *w, int64_t out_f, int64_t k,
+                                     struct tensor *x) {
+    assert(x->ndim == 2 && x->ne[0] == k);
+    assert(k % (type == QK_TYPE_Q8_0 ? QK8_0 : QK_K) == 0);
+    qk_seam_init();
+    int64_t n = x->ne[1];
+    struct tensor *out = tensor_new_2d(x->arena, out_f, n);
+    int rc = hip_qk_matmul_host(w, type, out_f, k, x->data, n, out->data);
+    if (rc != QK_OK) {
+        fprintf(stderr, "qk_seam: matmul type %d (%lld x %lld, %lld tokens) failed (%d): %s\n", type,
+                (long long)out_f, (long long)k, (long long)n, rc, hip_qk_last_error());
+        abort();
+    }
+    return out;
+}
+
+struct tensor *tensor_matmul_q4k_f32(const q4k_block *w, int64_t out_f, int64_t k, struct tensor *x) {
+    return qk_seam_matmul(QK_TYPE_Q4_K, w, out_f, k, x);
+}
+
+struct tensor *tensor_matmul_q5k_f32(const q5k_block *w, int64_t out_f, int64_t k, struct tensor *x) {
+    return qk_seam_matmul(QK_TYPE_Q5_K, w, out_f, k, x);
+}
+
+struct tensor *tensor_matmul_q6k_f32(const q6k_block *w, int64_t out_f, int64_t k, struct tensor *x) {
+    return qk_seam_matmul(QK_TYPE_Q6_K, w, out_f, k, x);
+}
+
+struct tensor *tensor_matmul_q8_0_f32(const q8_0_block *w, int64_t out_f, int64_t k, struct tensor *x) {
+    return qk_seam_matmul(QK_TYPE_Q8_0, w, out_f, k, x);
+}
+
+/* Upload a weight matrix before the first forward pass (what
+ * slm_model_load would do once per quantized tensor, slm/model.c:1130).
+ * Optional: the first matmul with an unseen weight uploads it too. */
+static void qk_seam_register(const void *w, int type, int64_t k, int64_t out_f) {
+    qk_seam_init();
+    int rc = hip_qk_register_weight(w, type, k, out_f);
+    if (rc != QK_OK) {
+        fprintf(stderr, "qk_seam: register weight failed (%d): %s\n", rc, hip_qk_last_error());
+        abort();
+    }
+}
+
+#endif /* QK_SEAM_C */
