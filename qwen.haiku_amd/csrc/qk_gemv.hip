@@ -432,8 +432,10 @@ void gemv_plan(GemvDesc &d) {
         d.lds_act = (d.nb * 36 + 15) & ~15;
     } else {
         d.nb = (int32_t)(d.k / QK_K);
+        // groups per row: enough to cover the row in one step up to 16
+        // super-blocks (k <= 4096), so a row costs one memory latency
         int p = 1;
-        while (p < 16 && 2 * p <= d.nb) p *= 2;
+        while (p < 16 && p < d.nb) p *= 2;
         d.p = p;
         d.rows_per_tile = 4 * (16 / p);
         d.lds_act = (d.nb * 292 + 15) & ~15;
@@ -496,6 +498,8 @@ hipError_t launch_gemv(GemvArgs &a, int max_grid, hipStream_t s) {
 // logits.
 #define TOPK_CAND 4096
 #define LMHEAD_MAX_WG 4096                             // argmax partials (one per workgroup)
+#define LMHEAD_WG 1024                                 // workgroups of the LM-head GEMV (grid-stride
+                                                       // over tiles): fewer maxima for the top-k bound
 
 __device__ __forceinline__ uint32_t valkey(float v) {
     uint32_t b = __float_as_uint(v);
@@ -701,7 +705,7 @@ hipError_t launch_lmhead(const uint8_t *w, int64_t n, int64_t k, const uint8_t *
     uint64_t *cand = partial + LMHEAD_MAX_WG;
     uint32_t *ctr = reinterpret_cast<uint32_t *>(cand + TOPK_CAND);
     int grid = 0;
-    hipError_t e = launch_gemv_impl(a, LMHEAD_MAX_WG, partial, ctr, &grid, s);
+    hipError_t e = launch_gemv_impl(a, LMHEAD_WG, partial, ctr, &grid, s);
     if (e != hipSuccess) return e;
     if (grid > LMHEAD_MAX_WG) return hipErrorInvalidValue;
     if (topk > 0) {
