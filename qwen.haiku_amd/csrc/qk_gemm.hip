@@ -22,9 +22,11 @@
 // registers meanwhile); each of the 4 waves then computes a 32x32
 // sub-tile:
 //
-//  * Q4_K / Q5_K: one v_mfma_i32_32x32x32_i8 per 32-element sub-block
-//    (weights 0..15 / 0..31), times the 6-bit scale; mins from the Q8_K
-//    bsums (simd/quants.h:283-304, 324-349);
+//  * Q4_K / Q5_K: the 6-bit sub-block scales are split into two 3-bit
+//    digits and baked into int8 weight planes (plus a 5th-bit plane for
+//    Q5_K), so one chain of v_mfma_i32_32x32x32_i8 per plane accumulates
+//    the whole super-block and isum = acc0 + 8*acc1 (+ 16*acc2); mins
+//    from the Q8_K bsums (simd/quants.h:283-304, 324-349);
 //  * Q6_K: one v_mfma_i32_32x32x16_i8 per 16-element sub-block, weights
 //    staged as u6 - 32 in [-32, 31] so the reference's
 //    isum - 32*isum_mins (simd/quants.h:359-399) is one exact int32 sum.
@@ -45,12 +47,24 @@ typedef int32_t v16i __attribute__((ext_vector_type(16)));
 #define GM_BN 64                      // weight rows per workgroup tile
 #define GM_LD 272                     // LDS row stride of the int8 tiles (256 + 16)
 
+// Dequantised weight planes per super-block. Q4_K / Q5_K: the 6-bit
+// sub-block scale sc = 8*hi + lo is split into two 3-bit digits and baked
+// into the weights, plane 0 = q4 * lo, plane 1 = q4 * hi (<= 105, int8);
+// Q5_K adds plane 2 = (5th bit) * sc (<= 63). One MFMA chain per plane
+// then accumulates a whole super-block, and
+//   isum = acc0 + 8*acc1 (+ 16*acc2)
+// exactly (every int8 product and every int32 sum is exact). Q6_K: one
+// plane, u6 - 32 in [-32, 31], scaled per 16-element sub-block after each
+// MFMA.
+template <int TYPE> struct Planes { static constexpr int n = TYPE == 12 ? 2 : (TYPE == 13 ? 3 : 1); };
+
+template <int NP>
 struct __attribute__((aligned(16))) GemmLds {
     int8_t a[GM_BM][GM_LD];           // activation quants of the super-block
-    int8_t b[GM_BN][GM_LD];           // dequantised int8 weights
+    int8_t b[NP][GM_BN][GM_LD];       // dequantised int8 weight planes
     int8_t am[GM_BM][16];             // bsum pairs p = 128*hi + lo: lo[8] (0..127) | hi[8] (-64..63)
     float yd[GM_BM];                  // Q8_K d per token
-    int8_t sc[GM_BN][16];             // sub-block scales per weight row
+    int8_t sc[GM_BN][16];             // Q6_K sub-block scales per weight row
     uint8_t mn[GM_BN][8];             // 6-bit mins (Q4_K / Q5_K)
     float wd[GM_BN];                  // fp16 d, widened
     float wdm[GM_BN];                 // fp16 dmin, widened
@@ -85,13 +99,15 @@ __device__ __forceinline__ void load_act(ActRaw &a, const uint8_t *row, int q, i
 
 // bsum pair j (bsums[2j] + bsums[2j+1], one dword of the block) as two
 // int8 digits of the mins operand.
-__device__ __forceinline__ void store_pair(GemmLds &s, int t, int j, uint32_t v) {
+template <typename GL>
+__device__ __forceinline__ void store_pair(GL &s, int t, int j, uint32_t v) {
     const int32_t p = (int32_t)(int16_t)(v & 0xffffu) + (int32_t)(int16_t)(v >> 16);
     s.am[t][j] = (int8_t)(p & 127);
     s.am[t][8 + j] = (int8_t)(p >> 7);
 }
 
-__device__ __forceinline__ void store_act(GemmLds &s, const ActRaw &a, int t, int q) {
+template <typename GL>
+__device__ __forceinline__ void store_act(GL &s, const ActRaw &a, int t, int q) {
     // dword r = q + 4j: r = 0 is d, 1..64 the quants, 65..72 the bsums
     if (q == 0) s.yd[t] = __uint_as_float(a.v[0]);
     else *(QK_LDS uint32_t *)&s.a[t][4 * q - 4] = a.v[0];
@@ -107,75 +123,127 @@ __device__ __forceinline__ void store_act(GemmLds &s, const ActRaw &a, int t, in
     }
 }
 
-// Scales and mins of a Q4_K / Q5_K header (d | dmin | scales[12]).
-__device__ __forceinline__ void store_kq_header(GemmLds &s, int r, const uint4 v) {
+// Mins, d and dmin of a Q4_K / Q5_K header (d | dmin | scales[12]).
+template <typename GL>
+__device__ __forceinline__ void store_kq_header(GL &s, int r, const uint4 v) {
     int32_t sc, mm;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         scale_min(v.y, v.z, v.w, j, sc, mm);
-        s.sc[r][j] = (int8_t)sc;
         s.mn[r][j] = (uint8_t)mm;
     }
     s.wd[r] = h2f(v.x & 0xffffu);
     s.wdm[r] = h2f(v.x >> 16);
 }
 
+// Bytes of x times d, byte by byte, for products below 256: two packed
+// 16-bit multiplies (each 16-bit lane holds two bytes b0 + 256*b1; with
+// b*d < 256 the low byte's product never carries into the high byte's).
+__device__ __forceinline__ uint32_t bmul(uint32_t x, uint32_t d) {
+    typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+    const us2 a = __builtin_bit_cast(us2, x);
+    const us2 b = {(unsigned short)d, (unsigned short)d};
+    return __builtin_bit_cast(uint32_t, a * b);
+}
+
+__device__ __forceinline__ void st16(int8_t *p, const uint32_t (&v)[4]) {
+    *(QK_LDS uint4 *)p = make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// 16 four-bit weights (one 16-byte run of nibble bytes, values 0..15) of
+// sub-block `sb` at element offset e, times the two digits of its scale.
+template <typename GL>
+__device__ __forceinline__ void store_q4_digits(GL &s, int r, int e, const uint32_t (&q)[4], int32_t sc) {
+    const uint32_t lo = (uint32_t)sc & 7u, hi = (uint32_t)sc >> 3;
+    uint32_t a[4], b[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        a[k] = bmul(q[k], lo);
+        b[k] = bmul(q[k], hi);
+    }
+    st16(&s.b[0][r][e], a);
+    st16(&s.b[1][r][e], b);
+}
+
 // Q4_K (144 B): header | qs[128]; qs[32c + l] low nibble is element
-// 64c + l, high nibble 64c + 32 + l. Quarter q takes the 16-byte qs
-// pieces q and q+4 (chunk c = q/2 and 2 + q/2, positions 16(q&1)..+16);
-// quarter 0 also the header.
+// 64c + l (sub-block 2c), high nibble 64c + 32 + l (sub-block 2c+1).
+// Quarter q takes the 16-byte qs pieces q and q+4 (chunk c = q/2 and
+// 2 + q/2, positions 16(q&1)..+16) and needs the header for their scales.
 struct WRaw12 { uint4 hdr, p0, p1; };
 
 __device__ __forceinline__ void load_w(WRaw12 &a, const uint8_t *row, int q, int i) {
     a.hdr = a.p0 = a.p1 = make_uint4(0, 0, 0, 0);
     if (!row) return;
     const uint8_t *p = row + (int64_t)i * Q4K_BYTES;
-    if (q == 0) a.hdr = ld16(p);
+    a.hdr = ld16(p);
     a.p0 = ld16(p + 16 + 16 * q);
     a.p1 = ld16(p + 80 + 16 * q);
 }
 
-__device__ __forceinline__ void store_nibbles(GemmLds &s, int r, int c, int l0, const uint4 v) {
+template <typename GL>
+__device__ __forceinline__ void store_piece4(GL &s, int r, int c, int l0, const uint4 v, const uint4 hdr) {
     const uint32_t M = 0x0F0F0F0Fu;
-    lds_st16(&s.b[r][64 * c + l0], v.x & M, v.y & M, v.z & M, v.w & M);
-    lds_st16(&s.b[r][64 * c + 32 + l0], (v.x >> 4) & M, (v.y >> 4) & M, (v.z >> 4) & M, (v.w >> 4) & M);
+    const uint32_t lo[4] = {v.x & M, v.y & M, v.z & M, v.w & M};
+    const uint32_t hi[4] = {(v.x >> 4) & M, (v.y >> 4) & M, (v.z >> 4) & M, (v.w >> 4) & M};
+    int32_t sc0, m0, sc1, m1;
+    scale_min(hdr.y, hdr.z, hdr.w, 2 * c, sc0, m0);
+    scale_min(hdr.y, hdr.z, hdr.w, 2 * c + 1, sc1, m1);
+    store_q4_digits(s, r, 64 * c + l0, lo, sc0);
+    store_q4_digits(s, r, 64 * c + 32 + l0, hi, sc1);
 }
 
-__device__ __forceinline__ void store_w(GemmLds &s, const WRaw12 &a, int r, int q) {
+template <typename GL>
+__device__ __forceinline__ void store_w(GL &s, const WRaw12 &a, int r, int q) {
     if (q == 0) store_kq_header(s, r, a.hdr);
-    store_nibbles(s, r, q >> 1, 16 * (q & 1), a.p0);
-    store_nibbles(s, r, 2 + (q >> 1), 16 * (q & 1), a.p1);
+    store_piece4(s, r, q >> 1, 16 * (q & 1), a.p0, a.hdr);
+    store_piece4(s, r, 2 + (q >> 1), 16 * (q & 1), a.p1, a.hdr);
 }
 
 // Q5_K (176 B): header | qh[32] | qs[128]. Element 64c + l gets bit 2c of
 // qh[l] as its 5th bit, element 64c + 32 + l bit 2c+1; quarter q needs the
-// qh bytes of its positions 16(q&1)..+16.
+// qh bytes of its positions 16(q&1)..+16. Planes 0/1 carry the low four
+// bits times the scale digits, plane 2 the 5th bit times the scale.
 struct WRaw13 { uint4 hdr, p0, p1, qh; };
 
 __device__ __forceinline__ void load_w(WRaw13 &a, const uint8_t *row, int q, int i) {
     a.hdr = a.p0 = a.p1 = a.qh = make_uint4(0, 0, 0, 0);
     if (!row) return;
     const uint8_t *p = row + (int64_t)i * Q5K_BYTES;
-    if (q == 0) a.hdr = ld16(p);
+    a.hdr = ld16(p);
     a.qh = ld16(p + 16 + 16 * (q & 1));
     a.p0 = ld16(p + 48 + 16 * q);
     a.p1 = ld16(p + 112 + 16 * q);
 }
 
-__device__ __forceinline__ void store_nibbles5(GemmLds &s, int r, int c, int l0, const uint4 q, const uint4 h) {
+template <typename GL>
+__device__ __forceinline__ void store_piece5(GL &s, int r, int c, int l0, const uint4 v, const uint4 h,
+                                             const uint4 hdr) {
     const uint32_t M = 0x0F0F0F0Fu, B1 = 0x01010101u;
     const uint32_t s0 = 2 * c, s1 = 2 * c + 1;
-    lds_st16(&s.b[r][64 * c + l0], (q.x & M) | (((h.x >> s0) & B1) << 4), (q.y & M) | (((h.y >> s0) & B1) << 4),
-             (q.z & M) | (((h.z >> s0) & B1) << 4), (q.w & M) | (((h.w >> s0) & B1) << 4));
-    lds_st16(&s.b[r][64 * c + 32 + l0], ((q.x >> 4) & M) | (((h.x >> s1) & B1) << 4),
-             ((q.y >> 4) & M) | (((h.y >> s1) & B1) << 4), ((q.z >> 4) & M) | (((h.z >> s1) & B1) << 4),
-             ((q.w >> 4) & M) | (((h.w >> s1) & B1) << 4));
+    const uint32_t lo[4] = {v.x & M, v.y & M, v.z & M, v.w & M};
+    const uint32_t hi[4] = {(v.x >> 4) & M, (v.y >> 4) & M, (v.z >> 4) & M, (v.w >> 4) & M};
+    const uint32_t hl[4] = {(h.x >> s0) & B1, (h.y >> s0) & B1, (h.z >> s0) & B1, (h.w >> s0) & B1};
+    const uint32_t hh[4] = {(h.x >> s1) & B1, (h.y >> s1) & B1, (h.z >> s1) & B1, (h.w >> s1) & B1};
+    int32_t sc0, m0, sc1, m1;
+    scale_min(hdr.y, hdr.z, hdr.w, 2 * c, sc0, m0);
+    scale_min(hdr.y, hdr.z, hdr.w, 2 * c + 1, sc1, m1);
+    store_q4_digits(s, r, 64 * c + l0, lo, sc0);
+    store_q4_digits(s, r, 64 * c + 32 + l0, hi, sc1);
+    uint32_t a[4], b[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        a[k] = bmul(hl[k], (uint32_t)sc0);
+        b[k] = bmul(hh[k], (uint32_t)sc1);
+    }
+    st16(&s.b[2][r][64 * c + l0], a);
+    st16(&s.b[2][r][64 * c + 32 + l0], b);
 }
 
-__device__ __forceinline__ void store_w(GemmLds &s, const WRaw13 &a, int r, int q) {
+template <typename GL>
+__device__ __forceinline__ void store_w(GL &s, const WRaw13 &a, int r, int q) {
     if (q == 0) store_kq_header(s, r, a.hdr);
-    store_nibbles5(s, r, q >> 1, 16 * (q & 1), a.p0, a.qh);
-    store_nibbles5(s, r, 2 + (q >> 1), 16 * (q & 1), a.p1, a.qh);
+    store_piece5(s, r, q >> 1, 16 * (q & 1), a.p0, a.qh, a.hdr);
+    store_piece5(s, r, 2 + (q >> 1), 16 * (q & 1), a.p1, a.qh, a.hdr);
 }
 
 // Four bytes u6 in [0, 63] -> four int8 bytes u6 - 32. u6 ^ 0x20 is
@@ -221,7 +289,8 @@ __device__ __forceinline__ void load_w(WRaw14 &a, const uint8_t *row, int q, int
     }
 }
 
-__device__ __forceinline__ void store_w(GemmLds &s, const WRaw14 &a, int r, int q) {
+template <typename GL>
+__device__ __forceinline__ void store_w(GL &s, const WRaw14 &a, int r, int q) {
     if (q == 0) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -248,10 +317,10 @@ __device__ __forceinline__ void store_w(GemmLds &s, const WRaw14 &a, int r, int 
         o2[k] = u6_minus_32(((qa[k] >> 4) & M) | (hh[k] & T));
         o3[k] = u6_minus_32(((qb[k] >> 4) & M) | ((hh[k] >> 2) & T));
     }
-    lds_st16(&s.b[r][128 * h + l0], o0[0], o0[1], o0[2], o0[3]);
-    lds_st16(&s.b[r][128 * h + 32 + l0], o1[0], o1[1], o1[2], o1[3]);
-    lds_st16(&s.b[r][128 * h + 64 + l0], o2[0], o2[1], o2[2], o2[3]);
-    lds_st16(&s.b[r][128 * h + 96 + l0], o3[0], o3[1], o3[2], o3[3]);
+    lds_st16(&s.b[0][r][128 * h + l0], o0[0], o0[1], o0[2], o0[3]);
+    lds_st16(&s.b[0][r][128 * h + 32 + l0], o1[0], o1[1], o1[2], o1[3]);
+    lds_st16(&s.b[0][r][128 * h + 64 + l0], o2[0], o2[1], o2[2], o2[3]);
+    lds_st16(&s.b[0][r][128 * h + 96 + l0], o3[0], o3[1], o3[2], o3[3]);
 }
 
 template <int TYPE> struct WRawOf;
@@ -267,7 +336,7 @@ template <int TYPE, bool FUSED>
 __global__ __launch_bounds__(256) void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb,
                                               const uint8_t *__restrict__ xq, int64_t m, float *__restrict__ y) {
     constexpr int BB = TYPE == 12 ? Q4K_BYTES : (TYPE == 13 ? Q5K_BYTES : Q6K_BYTES);
-    __shared__ GemmLds s;
+    __shared__ GemmLds<Planes<TYPE>::n> s;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 31, h = lane >> 5;
     const int tm = 32 * (wave >> 1), tn = 32 * (wave & 1);   // wave sub-tile in the workgroup tile
@@ -285,7 +354,6 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t *__restrict__ w, int
     load_act(ar, xrow, sq, 0);
     load_w(wr, wrow, sq, 0);
     const int8_t *arow = &s.a[tm + col][0];
-    const int8_t *brow = &s.b[tn + col][0];
     const v16i zero = {0};
 
     for (int i = 0; i < nb; i++) {
@@ -298,11 +366,12 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t *__restrict__ w, int
         }
         __syncthreads();
 
-        // isum = sum over sub-blocks of scale * (exact int8 dot of the sub-block)
         int32_t isum[16];
-#pragma unroll
-        for (int v = 0; v < 16; v++) isum[v] = 0;
         if (TYPE == 14) {
+            // per 16-element sub-block: MFMA, then times its int8 scale
+            const int8_t *brow = &s.b[0][tn + col][0];
+#pragma unroll
+            for (int v = 0; v < 16; v++) isum[v] = 0;
             const uint4 scp = *(const QK_LDS uint4 *)&s.sc[tn + col][0];
             const uint32_t scw[4] = {scp.x, scp.y, scp.z, scp.w};
 #pragma unroll
@@ -315,15 +384,25 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t *__restrict__ w, int
                 for (int v = 0; v < 16; v++) isum[v] += __mul24(scv, d[v]);
             }
         } else {
-            const uint2 scp = *(const QK_LDS uint2 *)&s.sc[tn + col][0];
+            // one accumulation chain per digit plane over the whole super-block
+            constexpr int NP = Planes<TYPE>::n;
+            v16i acc[NP];
 #pragma unroll
-            for (int sb = 0; sb < 8; sb++) {
-                const v4i av = *(const QK_LDS v4i *)(arow + 32 * sb + 16 * h);
-                const v4i bv = *(const QK_LDS v4i *)(brow + 32 * sb + 16 * h);
-                const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
-                const int32_t scv = (int32_t)(((sb < 4 ? scp.x : scp.y) >> (8 * (sb & 3))) & 0xffu);
+            for (int pl = 0; pl < NP; pl++) acc[pl] = zero;
 #pragma unroll
-                for (int v = 0; v < 16; v++) isum[v] += __mul24(scv, d[v]);
+            for (int c = 0; c < 8; c++) {
+                const v4i av = *(const QK_LDS v4i *)(arow + 32 * c + 16 * h);
+#pragma unroll
+                for (int pl = 0; pl < NP; pl++) {
+                    const v4i bv = *(const QK_LDS v4i *)(&s.b[pl][tn + col][32 * c + 16 * h]);
+                    acc[pl] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, acc[pl], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                int32_t t = acc[0][v] + 8 * acc[1][v];
+                if constexpr (NP == 3) t += 16 * acc[2][v];
+                isum[v] = t;
             }
         }
 
