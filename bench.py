@@ -37,7 +37,7 @@ MALL_DEFEAT_BYTES = 512 << 20
 # scaled by its reading for a known-size copy / fill (FETCH x2.000,
 # WRITE x1.000); the runs are recorded in profiles/k_gemv_decode_set_lmhead.md.
 # None when the kernel has changed since the last counter run.
-CONFIG1_TRAFFIC_BYTES = 11_796_224 + 350_208
+CONFIG1_TRAFFIC_BYTES = 11_811_840 + 354_304
 
 
 def _load(rel, name):
@@ -208,6 +208,25 @@ def cpu_baseline(synth, seconds=10.0):
                       f"through tensor_matmul_*_f32, {dt:.1f} s, dispatch {label}"}
 
 
+def config3_extras(torch, qk, synth, lib, steps):
+    """Config 3 at M = 512 / 128 / 2048 (Q4_K) and the Q6_K down projection."""
+    extra = {}
+    for (t, n3, k3, m3) in ((12, 3584, 1024, 512), (12, 3584, 1024, 128), (12, 3584, 1024, 2048),
+                            (14, 1024, 3584, 512)):
+        c3, sg, sb = bench_config3(torch, qk, synth, lib, steps, 10, t, n3, k3, m3)
+        ops = 2.0 * m3 * n3 * k3
+        xbytes = 4 * m3 * k3
+        alg = xbytes + n3 * (k3 // 256) * qk.BLOCK_BYTES[t] + 4 * m3 * n3
+        name = {12: "q4k", 14: "q6k"}[t]
+        extra[f"config3_gemm_{name}_m{m3}_n{n3}_k{k3}"] = {
+            "TOPS_gemm": round(ops * steps / sg / 1e12, 2), "us_gemm": round(sg / steps * 1e6, 3),
+            "TOPS_with_quantize": round(ops * steps / sb / 1e12, 2), "us_with_quantize": round(sb / steps * 1e6, 3),
+            "frac_of_5POPS": round(ops * steps / sb / 5.0e15, 4),
+            "frac_of_bw_x_ai": round((ops * steps / sb) / (HBM_PEAK_GBS * 1e9 * ops / alg), 4),
+            "copies": c3}
+    return extra
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -216,6 +235,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["all", "config3"], default="all",
+                    help="config3: time only the prefill GEMM cases (a profiling aid)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run 8 plain device copies of MIB MiB each: the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -235,6 +256,11 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+
+    if a.only == "config3":
+        print(json.dumps({"metric": "prefill int8 TOPS (config 3)", "unit": "TOPS", "dtype": "int8",
+                          "extra": config3_extras(torch, qk, synth, lib, a.steps)}))
+        return
 
     per, copies, secs = bench_config1(torch, qk, synth, lib, a.steps, a.warmup)
     gbs = per * a.steps / secs / 1e9
@@ -261,20 +287,7 @@ def main():
         p2, c2, s2 = bench_config2(torch, qk, synth, lib, st2, 5)
         extra["config2_lmhead_q6k_argmax_top40"] = {"GB/s": round(p2 * st2 / s2 / 1e9, 2),
                                                     "us_per_call": round(s2 / st2 * 1e6, 3), "copies": c2}
-        for (t, n3, k3, m3) in ((12, 3584, 1024, 512), (12, 3584, 1024, 128), (12, 3584, 1024, 2048),
-                                (14, 1024, 3584, 512)):
-            st3 = max(20, a.steps // 10)
-            c3, sg, sb = bench_config3(torch, qk, synth, lib, st3, 10, t, n3, k3, m3)
-            ops = 2.0 * m3 * n3 * k3
-            xbytes = 4 * m3 * k3
-            alg = xbytes + n3 * (k3 // 256) * qk.BLOCK_BYTES[t] + 4 * m3 * n3
-            name = {12: "q4k", 14: "q6k"}[t]
-            extra[f"config3_gemm_{name}_m{m3}_n{n3}_k{k3}"] = {
-                "TOPS_gemm": round(ops * st3 / sg / 1e12, 2), "us_gemm": round(sg / st3 * 1e6, 3),
-                "TOPS_with_quantize": round(ops * st3 / sb / 1e12, 2), "us_with_quantize": round(sb / st3 * 1e6, 3),
-                "frac_of_5POPS": round(ops * st3 / sb / 5.0e15, 4),
-                "frac_of_bw_x_ai": round((ops * st3 / sb) / (HBM_PEAK_GBS * 1e9 * ops / alg), 4),
-                "copies": c3}
+        extra.update(config3_extras(torch, qk, synth, lib, max(20, a.steps // 10)))
         out["extra"] = extra
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(synth, a.cpu_seconds)
