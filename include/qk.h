@@ -19,7 +19,7 @@
  *     of the reference's tensor_matmul_*_f32 (slm/tensor.c:827-1033)
  *     moved onto the GPU; weights are uploaded once and found again by
  *     their host address, so the reference's call signatures need no
- *     change (qwen.haiku_amd/host/qk_tensor_seam.h).
+ *     change (qwen.haiku_amd/host/qk_seam.c).
  *
  * Results are bit-identical to the reference CPU path of the selected
  * tier (hip_qk_set_tier): the integer part of every row dot is exact,
