@@ -146,7 +146,7 @@ int hip_quantize_q8_0(const float *x, int64_t m, int64_t k, void *xq,
  * (slm/tensor.c:846-850, 912-917, 1026-1031, 974-979) and the
  * simd_q*_row_dot entry points it calls (simd/simd.c:236-250).
  * Limits: w 16-byte aligned; k <= 16384 (the activation row is staged
- * in LDS). */
+ * in LDS); the matrix (n rows x row bytes) below 4 GB (32-bit offsets). */
 int hip_matvec_q4k (const void *w, int64_t n, int64_t k, const void *xq,
                     float *y, void *stream);
 int hip_matvec_q5k (const void *w, int64_t n, int64_t k, const void *xq,

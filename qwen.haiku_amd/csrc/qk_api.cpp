@@ -126,13 +126,13 @@ int check_mat(int type, const void *w, int64_t n, int64_t k, const void *xq, con
     if (k % block_elems(type)) return fail(QK_ERR_ARG, "k=%lld is not a multiple of %lld", (long long)k, (long long)block_elems(type));
     if (k > 16384) return fail(QK_ERR_ARG, "k=%lld exceeds the 16384 limit of the LDS activation stage", (long long)k);
     if (n > 0x7fffffffLL) return fail(QK_ERR_ARG, "n=%lld exceeds 2^31-1 rows", (long long)n);
-    // The GEMV streams the matrix with 16-byte loads from its base, one
-    // tile of whole rows at a time.
+    // The GEMV streams the matrix with 16-byte loads from its base and
+    // addresses it with 32-bit byte offsets (buffer loads).
     if (!aligned(w, 16)) return fail(QK_ERR_ARG, "weights must be 16-byte aligned");
     const int64_t row_bytes = (k / block_elems(type)) * block_bytes(type);
-    if (row_bytes > qk::gemv_max_row_bytes())
-        return fail(QK_ERR_ARG, "row of %lld bytes exceeds the %lld-byte tile (k too large for this type)",
-                    (long long)row_bytes, (long long)qk::gemv_max_row_bytes());
+    if (n * row_bytes > qk::gemv_max_matrix_bytes())
+        return fail(QK_ERR_ARG, "matrix of %lld bytes exceeds the %lld-byte limit",
+                    (long long)(n * row_bytes), (long long)qk::gemv_max_matrix_bytes());
     if (!aligned(xq, type == QK_TYPE_Q8_0 ? 2 : 4)) return fail(QK_ERR_ARG, "activations misaligned");
     if (!aligned(y, 4)) return fail(QK_ERR_ARG, "output misaligned");
     return QK_OK;

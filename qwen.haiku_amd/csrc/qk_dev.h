@@ -182,7 +182,7 @@ __device__ __forceinline__ float bcast8(float s) {
     const float s2 = __fadd_rn(s, s);
     const float s4 = __fadd_rn(s2, s2);
     const float s8 = __fadd_rn(s4, s4);
-    return __fdiv_rn(s8, 8.0f);
+    return __fmul_rn(s8, 0.125f);      // x / 8 and x * 2^-3 round the same exact value
 }
 
 // Q6_K term (all tiers, simd/quants.h:399): rn(rn(fp16(x.d)*y.d) * (float)v).

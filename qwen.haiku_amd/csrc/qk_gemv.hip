@@ -5,14 +5,20 @@
 // dispatch. A 256-thread workgroup computes row tiles of one descriptor
 // (grid-stride over tiles).
 //
-// Each workgroup streams tiles of consecutive rows (one contiguous byte
-// range) from HBM into LDS with fully coalesced 16-byte loads, double
-// buffered, and computes from LDS: an aligned group of 4 lanes owns one
-// 256-element super-block, each lane takes 32 quant bytes and runs
-// v_dot4 against the activation bytes; the group sums its int32 partials
-// with DPP. Super-block terms of a row are then added in block order by
-// one lane, so the float sum rounds exactly as the reference's sequential
-// `sum += term` (simd/quants.h:305, simd/avx.c:467).
+// Loads. A wave's work item is one contiguous byte range of W (whole rows,
+// or 16 super-blocks of one long row). The wave reads it with
+// lane-contiguous 16-byte loads, so every load instruction covers 1 KB of
+// consecutive bytes, into registers one item ahead of the arithmetic. The
+// registers are then written to a wave-private LDS window, from which each
+// lane reads the fields of its block. Memory instructions per byte are the
+// minimum, whatever the block size (34, 144, 176 or 210 bytes).
+//
+// Arithmetic. An aligned group of 4 lanes owns one 256-element super-block:
+// each lane takes 32 quant bytes and runs v_dot4 against the activation
+// row staged in LDS, and the group sums its int32 partials with DPP. The
+// super-block terms of a row are added in block order by one lane, so the
+// float sum rounds exactly as the reference's sequential `sum += term`
+// (simd/quants.h:305, simd/avx.c:467).
 //
 // Activations are staged once per workgroup into LDS with 16-byte
 // aligned quant rows (Q8_K: qs[nb][256] | bsums[nb][16] | d[nb]).
@@ -22,28 +28,88 @@
 namespace qk {
 
 // ---- activation staging ----------------------------------------------------
-__device__ __forceinline__ void stage_q8k(const uint8_t *__restrict__ xq, int nb, uint8_t *lds) {
-    uint32_t *qs = reinterpret_cast<uint32_t *>(lds);
-    uint32_t *bs = reinterpret_cast<uint32_t *>(lds + nb * 256);
-    float *d = reinterpret_cast<float *>(lds + nb * 288);
-    for (int i = threadIdx.x; i < nb * 73; i += blockDim.x) {
-        const int b = i / 73, r = i - b * 73;
-        const uint32_t v = ld32(xq + 4 * i);
-        if (r == 0) d[b] = __uint_as_float(v);
-        else if (r <= 64) qs[b * 64 + r - 1] = v;
-        else bs[b * 8 + r - 65] = v;
+// Dword i of the raw Q8_K row goes to its place in the LDS layout, in
+// rounds of 1024 dwords (4 per thread). Loads past the row return zeros
+// (buffer range check) and their stores land in `junk`, a spot that is
+// overwritten after the barrier that ends staging. The first round is
+// split: its loads go out before the weight loads (stage_q8k_first), its
+// stores after them (stage_q8k_rest), so the stores wait only for the
+// activations.
+struct Stage {
+    uint32_t v[4];
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t act_rsrc(const uint8_t *xq, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(xq), 0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ void stage_q8k_load(Stage &st, __amdgpu_buffer_rsrc_t r, int base, int tot) {
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+        if (base + 256 * u < tot)
+            st.v[u] = __builtin_amdgcn_raw_buffer_load_b32(r, 4 * (base + 256 * u + (int)threadIdx.x), 0, 0);
+}
+
+__device__ __forceinline__ void stage_q8k_store(const Stage &st, int base, int tot, int nb, uint8_t *lds,
+                                                uint8_t *junk) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        if (base + 256 * u < tot) {
+            const int i = base + 256 * u + (int)threadIdx.x;
+            const int b = i / 73, q = i - b * 73;
+            // q == 0: d; 1..64: qs dword q-1; 65..72: bsums dword q-65
+            const int to_d = nb * 288 + 4 * b;
+            const int to_qs = b * 256 + 4 * q - 4;
+            const int to_bs = nb * 256 + b * 32 + 4 * q - 260;
+            int dst = q > 64 ? to_bs : to_qs;
+            dst = q == 0 ? to_d : dst;
+            uint8_t *p = (i < tot) ? lds + dst : junk;
+            *(QK_LDS uint32_t *)(p) = st.v[u];
+        }
     }
+}
+
+// Rounds after the first (rows longer than 1024 dwords: k > 3584).
+__device__ __forceinline__ void stage_q8k_rest(const Stage &first, __amdgpu_buffer_rsrc_t r, int nb, uint8_t *lds,
+                                               uint8_t *junk) {
+    const int tot = nb * 73;
+    stage_q8k_store(first, 0, tot, nb, lds, junk);
+    for (int base = 1024; base < tot; base += 1024) {
+        Stage st;
+        stage_q8k_load(st, r, base, tot);
+        stage_q8k_store(st, base, tot, nb, lds, junk);
+    }
+}
+
+// Workgroup barrier that orders LDS only: it waits for the LDS stores
+// before it, not for global loads still in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // Q8_0 activation row: qs[nb][32] | d[nb] (fp16 widened once).
 __device__ __forceinline__ void stage_q80(const uint8_t *__restrict__ xq, int nb, uint8_t *lds) {
     uint16_t *qs = reinterpret_cast<uint16_t *>(lds);
     float *d = reinterpret_cast<float *>(lds + nb * 32);
-    for (int i = threadIdx.x; i < nb * 17; i += blockDim.x) {
-        const int b = i / 17, r = i - b * 17;
-        const uint32_t v = ld_u16(xq + 2 * i);
-        if (r == 0) d[b] = h2f(v);
-        else qs[b * 16 + r - 1] = (uint16_t)v;
+    const int tot = nb * 17;
+    for (int i0 = threadIdx.x; i0 < tot; i0 += 4 * blockDim.x) {
+        uint32_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = i0 + u * (int)blockDim.x;
+            if (i < tot) v[u] = ld_u16(xq + 2 * i);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = i0 + u * (int)blockDim.x;
+            if (i < tot) {
+                const int b = i / 17, r = i - b * 17;
+                if (r == 0) d[b] = h2f(v[u]);
+                else qs[b * 16 + r - 1] = (uint16_t)v[u];
+            }
+        }
     }
 }
 
@@ -57,12 +123,15 @@ __device__ __forceinline__ int32_t dot16(uint32_t w0, uint32_t w1, uint32_t w2, 
     return dot4(w3, a.w, s);
 }
 
-// ---- LDS reads (activation row) ------------------------------------------------
+// ---- LDS reads ---------------------------------------------------------------
 __device__ __forceinline__ uint4 lds16(const uint8_t *p) {          // 16-B aligned
     return *(const QK_LDS uint4 *)(p);
 }
 __device__ __forceinline__ uint32_t lds32(const uint8_t *p) {       // 4-B aligned
     return *(const QK_LDS uint32_t *)(p);
+}
+__device__ __forceinline__ uint32_t lds_u16(const uint8_t *p) {     // 2-B aligned
+    return *(const QK_LDS uint16_t *)(p);
 }
 
 __device__ __forceinline__ int32_t sum4(int32_t v) {
@@ -88,11 +157,72 @@ __device__ __forceinline__ int32_t bsum_pair(const uint8_t *act, int nb, int b, 
     return (int32_t)(int16_t)(v & 0xffffu) + (int32_t)(int16_t)(v >> 16);
 }
 
-// ---- per-super-block raw loads and terms ------------------------------------
-// A group of 4 lanes owns one 256-element super-block; lane j (0..3)
-// loads 32 quant bytes of it straight from HBM into registers. Loads are
-// split from the arithmetic so the next work item's bytes are in flight
-// while the current one is reduced.
+// ---- wave-contiguous weight staging -------------------------------------------
+// A wave item is the byte range [w + s, w + e). The wave loads its 16-byte
+// aligned superset (aligned in absolute address): piece p (16 bytes) goes
+// to lane p % 64 of load u = p / 64. The superset never reaches a 4 KB page
+// that the range itself does not touch, since pages are 16-byte aligned.
+// WBUF_BYTES bounds an item: 16 super-blocks (16 x 210 B) or 64 Q8_0
+// blocks (64 x 34 B), plus 30 bytes of alignment slack.
+#define WBUF_BYTES 4096
+#define WBUF_LOADS (WBUF_BYTES / 1024)
+
+struct Chunk {
+    uint4 v[WBUF_LOADS];
+};
+
+struct Span {
+    const uint8_t *base;   // 16-byte aligned start of the superset
+    int32_t ofs;           // first byte of the item, relative to base
+    int32_t npc;           // 16-byte pieces to load (0: empty item)
+};
+
+__device__ __forceinline__ Span make_span(const uint8_t *w, int64_t s, int64_t e) {
+    const uintptr_t ps = reinterpret_cast<uintptr_t>(w + s);
+    const uintptr_t pa = ps & ~(uintptr_t)15;
+    Span sp;
+    sp.base = reinterpret_cast<const uint8_t *>(pa);
+    sp.ofs = (int32_t)(ps - pa);
+    sp.npc = (int32_t)((reinterpret_cast<uintptr_t>(w + e) - pa + 15) >> 4);
+    return sp;
+}
+
+// Buffer loads: the range check of the buffer resource (num_records =
+// npc x 16) turns pieces past the item into zeros without a memory access,
+// so the loads need no per-lane guard. A load whose 64 pieces all lie past
+// the item is skipped (a uniform branch).
+__device__ __forceinline__ void chunk_load(Chunk &c, const Span &sp, int lane) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(sp.base), 0, sp.npc * 16, 0x00020000);
+#pragma unroll
+    for (int u = 0; u < WBUF_LOADS; u++) {
+        if (u * 64 < sp.npc) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16, u * 1024, 0);
+            c.v[u] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+    }
+}
+
+// Pieces past the item hold zeros from the range-checked loads; storing
+// them stays inside the window.
+__device__ __forceinline__ void chunk_store(const Chunk &c, uint8_t *wb, const Span &sp, int lane) {
+#pragma unroll
+    for (int u = 0; u < WBUF_LOADS; u++)
+        if (u * 64 < sp.npc) *(QK_LDS uint4 *)(wb + 1024 * u + 16 * lane) = c.v[u];
+}
+
+// Orders a wave's LDS accesses around a hand-off between its lanes. LDS
+// executes one wave's instructions in order, so no wait is needed; the
+// fences keep the compiler from moving accesses across.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ---- per-super-block fields and terms -------------------------------------------
+// Lane j (0..3) of a group reads its 32 quant bytes of the super-block
+// (and the header) from the wave's LDS window.
 template <int T> struct Raw;
 template <> struct Raw<12> { uint4 hdr, q0, q1; };
 template <> struct Raw<13> { uint4 hdr, q0, q1, h0, h1; };
@@ -101,11 +231,12 @@ template <> struct Raw<14> { uint32_t l[9], h[9], sh, sc, sc2, d; };
 // Q4_K (simd/quants.h:267-306): lane j holds chunk c = j, qs[32j..32j+32):
 // low nibbles pair with q8[64j..64j+32) under scale 2j, high nibbles with
 // q8[64j+32..64j+64) under scale 2j+1; mins 2j, 2j+1 meet bsum pairs 2j,
-// 2j+1.
-__device__ __forceinline__ void load_sb(Raw<12> &r, const uint8_t *__restrict__ blk, int j) {
-    r.hdr = ld16(blk);
-    r.q0 = ld16(blk + 16 + 32 * j);
-    r.q1 = ld16(blk + 32 + 32 * j);
+// 2j+1. off is 16-byte aligned (144-byte blocks; W is 16-byte aligned).
+__device__ __forceinline__ void read_sb(Raw<12> &r, const uint8_t *wb, int off, int j) {
+    const uint8_t *blk = wb + off;
+    r.hdr = lds16(blk);
+    r.q0 = lds16(blk + 16 + 32 * j);
+    r.q1 = lds16(blk + 32 + 32 * j);
 }
 
 template <bool FUSED>
@@ -129,12 +260,13 @@ __device__ __forceinline__ float term_sb(const Raw<12> &r, int b, int j, const u
 }
 
 // Q5_K (simd/quants.h:310-351): as Q4_K plus bit 2j / 2j+1 of qh[l].
-__device__ __forceinline__ void load_sb(Raw<13> &r, const uint8_t *__restrict__ blk, int j) {
-    r.hdr = ld16(blk);
-    r.h0 = ld16(blk + 16);
-    r.h1 = ld16(blk + 32);
-    r.q0 = ld16(blk + 48 + 32 * j);
-    r.q1 = ld16(blk + 64 + 32 * j);
+__device__ __forceinline__ void read_sb(Raw<13> &r, const uint8_t *wb, int off, int j) {
+    const uint8_t *blk = wb + off;
+    r.hdr = lds16(blk);
+    r.h0 = lds16(blk + 16);
+    r.h1 = lds16(blk + 32);
+    r.q0 = lds16(blk + 48 + 32 * j);
+    r.q1 = lds16(blk + 64 + 32 * j);
 }
 
 template <bool FUSED>
@@ -165,24 +297,23 @@ __device__ __forceinline__ float term_sb(const Raw<13> &r, int b, int j, const u
 // top bits come from qh[32h + l] bits 2qq and 2qq+4. Sub-blocks
 // 8h+2qq+{0,1} (low) and +4 (high). Each lane folds its share of
 // isum - 32*isum_mins, exact in int32, so one reduction suffices. 210-byte
-// blocks are 2-byte aligned: 32-byte runs are read as aligned 36-byte
+// blocks sit at even offsets: 32-byte runs are read as aligned 36-byte
 // windows (inside the block: the last ends at byte 196) and funnel-shifted.
-__device__ __forceinline__ void load_sb(Raw<14> &r, const uint8_t *__restrict__ blk, int j) {
+__device__ __forceinline__ void read_sb(Raw<14> &r, const uint8_t *wb, int off, int j) {
     const int h = j >> 1, qq = j & 1;
-    const uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(blk) & 3u;
+    const uint32_t sh = (uint32_t)off & 3u;
     r.sh = sh;
-    const uint8_t *wl = blk + 32 * j - sh;
-    const uint8_t *wh = blk + 128 + 32 * h - sh;
-    const u32x4a4 l0 = ld16_a4(wl), l1 = ld16_a4(wl + 16);
-    const u32x4a4 h0 = ld16_a4(wh), h1 = ld16_a4(wh + 16);
-    r.l[0] = l0.x; r.l[1] = l0.y; r.l[2] = l0.z; r.l[3] = l0.w;
-    r.l[4] = l1.x; r.l[5] = l1.y; r.l[6] = l1.z; r.l[7] = l1.w; r.l[8] = ld32(wl + 32);
-    r.h[0] = h0.x; r.h[1] = h0.y; r.h[2] = h0.z; r.h[3] = h0.w;
-    r.h[4] = h1.x; r.h[5] = h1.y; r.h[6] = h1.z; r.h[7] = h1.w; r.h[8] = ld32(wh + 32);
+    const uint8_t *wl = wb + off + 32 * j - sh;
+    const uint8_t *wh = wb + off + 128 + 32 * h - sh;
+#pragma unroll
+    for (int i = 0; i < 9; i++) {
+        r.l[i] = lds32(wl + 4 * i);
+        r.h[i] = lds32(wh + 4 * i);
+    }
     const int s = 8 * h + 2 * qq;
-    r.sc = ld_u16(blk + 192 + s);
-    r.sc2 = ld_u16(blk + 196 + s);
-    r.d = ld_u16(blk + 208);
+    r.sc = lds_u16(wb + off + 192 + s);
+    r.sc2 = lds_u16(wb + off + 196 + s);
+    r.d = lds_u16(wb + off + 208);
 }
 
 template <bool FUSED>
@@ -215,6 +346,29 @@ __device__ __forceinline__ float term_sb(const Raw<14> &r, int b, int j, const u
     return q6term(yd, r.d, tot);
 }
 
+// Device-side descriptor: 64 bytes, fetched by one scalar load once a
+// workgroup knows its descriptor index.
+struct KDesc {
+    const uint8_t *w;
+    const uint8_t *xq;
+    float *y;
+    int32_t n;
+    int32_t type;
+    int32_t nb;
+    int32_t p;
+    int32_t rows_per_tile;
+    int32_t ntiles;
+    int32_t nwg;
+    int32_t lds_act;
+    int32_t wg0;
+    int32_t pad;
+};
+static_assert(sizeof(KDesc) == 64, "KDesc is one 64-byte scalar load");
+
+struct alignas(64) KArgs {
+    KDesc d[QK_GROUP_MAX_DEV];
+};
+
 // Monotone 64-bit key: larger logit first, lower index on ties; -0 == +0
 // and NaN below everything (sample_argmax never picks a NaN).
 __device__ __forceinline__ uint64_t argkey(float v, int64_t row) {
@@ -225,49 +379,85 @@ __device__ __forceinline__ uint64_t argkey(float v, int64_t row) {
 }
 
 // Rows of one K-quant descriptor handled by this workgroup: tiles
-// lw, lw+nwg, ... of 4 waves x 16/P rows. A row's P groups each take every
-// P-th super-block; the P terms of a step are gathered with ds_bpermute
-// and added to the row sum in super-block order. Work items (tile, step)
-// are pipelined one deep: item i+1's loads are issued before item i is
-// reduced. The activation row is staged after the first loads are out.
-template <int TYPE, bool FUSED>
-__device__ __forceinline__ void run_kq(const GemvDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best) {
+// lw, lw+nwg, ... of 4 waves x 16/P rows. A row's P = 2^LP groups each take
+// one super-block of a step (P super-blocks); the P terms of a step are
+// gathered with ds_bpermute and added to the row sum in super-block order.
+// A wave item (tile, step) is one contiguous range of W: the wave's 16/P
+// whole rows when a row fits one step (nb <= P), else P super-blocks of
+// its one row (P = 16). Items are pipelined one deep: item i+1's loads are
+// issued before item i is reduced, and the first item's loads go out
+// before the activation row is staged. Item offsets are 32-bit: the API
+// limits a matrix to 4 GB.
+template <int TYPE, int LP, bool FUSED>
+__device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best) {
     constexpr int BB = TYPE == 12 ? Q4K_BYTES : (TYPE == 13 ? Q5K_BYTES : Q6K_BYTES);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int P = 1 << LP;
+    constexpr int RPW = 16 >> LP;                      // rows per wave item
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int grp = lane >> 2, j = lane & 3;
-    const int lp = 31 - __builtin_clz(D.p);
-    const int P = 1 << lp;
-    const int team = grp >> lp, g = grp & (P - 1);
-    const int nb = D.nb, rpt = D.rows_per_tile, ntiles = D.ntiles;
-    const int niter = (nb + P - 1) >> lp;
-    const int64_t n = D.n;
+    const int team = grp >> LP, g = grp & (P - 1);
+    const int nb = D.nb, ntiles = D.ntiles, n = D.n;
+    const int niter = (nb + P - 1) >> LP;
+    const uint32_t rowb = (uint32_t)nb * BB;
     const uint8_t *__restrict__ w = D.w;
     float *__restrict__ y = D.y;
+    uint8_t *wb = lds + D.lds_act + wave * WBUF_BYTES;
     const int src0 = team * P * 4;
-    const int64_t rofs = (int64_t)wave * (16 >> lp) + team;
-    auto issue = [&](Raw<TYPE> &r, int t, int i) {
-        const int64_t row = (int64_t)t * rpt + rofs;
-        const int b = i * P + g;
-        if (t < ntiles && row < n && b < nb) load_sb(r, w + (row * nb + b) * BB, j);
+    const int lofs = (team * nb + g) * BB;             // block offset inside the item
+    auto span = [&](int t, int i) -> Span {
+        const int r0 = t * (4 * RPW) + wave * RPW;
+        uint32_t len;
+        if (niter == 1) {
+            const int nr = (n - r0 < RPW) ? n - r0 : RPW;
+            len = (uint32_t)nr * rowb;
+        } else {
+            const int nbl = (nb - i * P < P) ? nb - i * P : P;
+            len = (uint32_t)nbl * BB;
+        }
+        if (t >= ntiles || r0 >= n) len = 0;
+        const uint32_t s0 = (uint32_t)r0 * rowb + (uint32_t)(i * P * BB);
+        const uint32_t a0 = s0 & ~15u;
+        Span sp;
+        sp.base = w + a0;
+        sp.ofs = (int32_t)(s0 - a0);
+        sp.npc = len ? (int32_t)((s0 + len - a0 + 15) >> 4) : 0;
+        return sp;
     };
+    // activation loads first, then the first item's weights; the staging
+    // stores then wait only for the activations
+    const __amdgpu_buffer_rsrc_t ar = act_rsrc(D.xq, nb * Q8K_BYTES);
+    Stage st0;
+    stage_q8k_load(st0, ar, 0, nb * 73);
     int tile = lw, it = 0;
-    Raw<TYPE> cur;
-    issue(cur, tile, it);
-    stage_q8k(D.xq, nb, lds);
-    __syncthreads();
+    Span sp = span(tile, it);
+    Chunk cur;
+    chunk_load(cur, sp, lane);
+    int ntile = tile, nit = it + 1;
+    if (nit == niter) { nit = 0; ntile += nwg; }
+    Span nsp = span(ntile, nit);                       // computed while the loads are in flight
+    stage_q8k_rest(st0, ar, nb, lds, lds + D.lds_act);
+    lds_barrier();
     float sum = 0.0f;
     while (tile < ntiles) {
-        int ntile = tile, nit = it + 1;
-        if (nit == niter) { nit = 0; ntile += nwg; }
-        Raw<TYPE> nxt;
-        issue(nxt, ntile, nit);
-        const int64_t row = (int64_t)tile * rpt + rofs;
-        const int b = it * P + g;
-        float t = 0.0f;
-        if (row < n && b < nb) t = term_sb<FUSED>(cur, b, j, lds, nb);
+        Chunk nxt;
+        chunk_load(nxt, nsp, lane);
+        chunk_store(cur, wb, sp, lane);
+        wave_sync();
+        // Lanes of a block past the row end or of a row past n compute a
+        // term from in-range LDS bytes that is never added or stored.
+        Raw<TYPE> r;
+        read_sb(r, wb, sp.ofs + lofs, j);
+        const float t = term_sb<FUSED>(r, it * P + g, j, lds, nb);
+        float tg[P];
+#pragma unroll
+        for (int g2 = 0; g2 < P; g2++) tg[g2] = __shfl(t, src0 + 4 * g2);
         const int lim = (nb - it * P < P) ? nb - it * P : P;
-        for (int g2 = 0; g2 < lim; g2++) sum += __shfl(t, src0 + 4 * g2);
+#pragma unroll
+        for (int g2 = 0; g2 < P; g2++)
+            if (g2 < lim) sum += tg[g2];
         if (it == niter - 1) {
+            const int row = tile * (4 * RPW) + wave * RPW + team;
             if (FUSED) sum = bcast8(sum);
             if (row < n && g == 0 && j == 0) {
                 *(QK_GLOBAL float *)(y + row) = sum;
@@ -276,55 +466,82 @@ __device__ __forceinline__ void run_kq(const GemvDesc &D, int lw, int nwg, uint8
             }
             sum = 0.0f;
         }
+        wave_sync();                                   // window reads done before the next store
         cur = nxt;
+        sp = nsp;
         tile = ntile;
         it = nit;
+        ntile = tile;
+        nit = it + 1;
+        if (nit == niter) { nit = 0; ntile += nwg; }
+        nsp = span(ntile, nit);
     }
 }
 
 // Q8_0 (q8_0_dot_q8_0, simd/avx.c:65-158, simd/quants.h:244-256): one row
-// per wave. Lane = slot s (bytes 4s..4s+3 of a block, the AVX lane) +
-// 8 x phase; phases take blocks b = phase + 8i, so a chunk of 64 blocks
-// is loaded by the whole wave at once. The per-block slot partials p and
-// scales go through LDS to 8 chain lanes, which run the reference's
-// sequential accumulation over blocks:
+// per wave, in chunks of up to 64 blocks (one wave item, pipelined like the
+// K-quants). Lane = slot s (bytes 4s..4s+3 of a block, the AVX lane) +
+// 8 x phase; phases take blocks b = phase + 8i of the chunk. The per-block
+// slot partials p and scales go back through the wave's LDS window to 8
+// chain lanes, which run the reference's sequential accumulation over
+// blocks:
 //  fused (AVX2/VNNI): acc_s = fma((float)p_s, s_b, acc_s), then
 //        ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7));
 //  separate (scalar/AVX1): sum = sum + (float)(sum_s p_s) * s_b.
 template <bool FUSED>
-__device__ __forceinline__ void run_q80(const GemvDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__device__ __forceinline__ void run_q80(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int s = lane & 7, ph = lane >> 3;
     const int nb = D.nb, ntiles = D.ntiles;
+    const int nchunk = (nb + 63) >> 6;
     const int64_t n = D.n;
     const uint8_t *__restrict__ w = D.w;
     float *__restrict__ y = D.y;
+    uint8_t *wb = lds + D.lds_act + wave * WBUF_BYTES;
+    // after a chunk's raw bytes are read: 8 slots x 64 blocks of partials
+    // (slot-major, so a chain lane reads contiguous 16-byte vectors) and 64
+    // block scales, in the same window
+    QK_LDS int32_t *xp = (QK_LDS int32_t *)(wb);
+    QK_LDS float *xs = (QK_LDS float *)(xp + 64 * 8);
+    auto span = [&](int t, int c) -> Span {
+        const int64_t row = (int64_t)t * 4 + wave;
+        if (t >= ntiles || row >= n) return Span{w, 0, 0};
+        const int b1 = (c * 64 + 64 < nb) ? c * 64 + 64 : nb;
+        return make_span(w, (row * nb + (int64_t)c * 64) * Q80_BYTES, (row * nb + b1) * Q80_BYTES);
+    };
+    int tile = lw, c = 0;
+    Span sp = span(tile, c);
+    Chunk cur;
+    chunk_load(cur, sp, lane);
     stage_q80(D.xq, nb, lds);
     __syncthreads();
     const QK_LDS uint32_t *aq = (const QK_LDS uint32_t *)(lds);
     const QK_LDS float *ad = (const QK_LDS float *)(lds + nb * 32);
-    // per-wave exchange area after the staged activations: 8 slots x 64
-    // blocks of partials (slot-major, so a chain lane reads contiguous
-    // 16-byte vectors) and 64 block scales
-    QK_LDS int32_t *xp = (QK_LDS int32_t *)(lds + D.lds_act + wave * 64 * 36);
-    QK_LDS float *xs = (QK_LDS float *)(xp + 64 * 8);
-    for (int tile = lw; tile < ntiles; tile += nwg) {
+    float acc = 0.0f;
+    while (tile < ntiles) {
+        int ntile = tile, nc = c + 1;
+        if (nc == nchunk) { nc = 0; ntile += nwg; }
+        const Span nsp = span(ntile, nc);
+        Chunk nxt;
+        chunk_load(nxt, nsp, lane);
         const int64_t row = (int64_t)tile * 4 + wave;
-        if (row >= n) continue;                        // wave-uniform
-        const uint8_t *rowp = w + row * (int64_t)nb * Q80_BYTES;
-        float acc = 0.0f;
-        for (int c0 = 0; c0 < nb; c0 += 64) {
+        if (row < n) {                                 // wave-uniform
+            chunk_store(cur, wb, sp, lane);
+            wave_sync();
+            const int c0 = c * 64;
             const int cn = (nb - c0 < 64) ? nb - c0 : 64;
             uint32_t wq[8], wd[8];
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                const int b = c0 + ph + 8 * i;
-                if (ph + 8 * i < cn) {
-                    const uint8_t *blk = rowp + (int64_t)b * Q80_BYTES;
-                    wq[i] = ld_u16(blk + 2 + 4 * s) | (ld_u16(blk + 4 + 4 * s) << 16);
-                    wd[i] = ld_u16(blk);
+                const int bl = ph + 8 * i;
+                if (bl < cn) {
+                    const uint8_t *blk = wb + sp.ofs + bl * Q80_BYTES;
+                    wq[i] = lds_u16(blk + 2 + 4 * s) | (lds_u16(blk + 4 + 4 * s) << 16);
+                    wd[i] = lds_u16(blk);
                 }
             }
+            wave_sync();                               // raw reads done before xp/xs reuse the window
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const int bl = ph + 8 * i;
@@ -341,9 +558,7 @@ __device__ __forceinline__ void run_q80(const GemvDesc &D, int lw, int nwg, uint
                     }
                 }
             }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            wave_sync();
             if (ph == 0) {
                 int bl = 0;
                 if (FUSED) {
@@ -367,40 +582,76 @@ __device__ __forceinline__ void run_q80(const GemvDesc &D, int lw, int nwg, uint
                     for (; bl < cn; bl++) acc = __fadd_rn(acc, xs[bl]);
                 }
             }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            wave_sync();                               // chain reads done before the next chunk
+            if (c == nchunk - 1) {
+                float r = acc;
+                if (FUSED) {
+                    r = __fadd_rn(r, swz_xor4(r));
+                    r = __fadd_rn(r, swz_xor1(r));
+                    r = __fadd_rn(r, swz_xor2(r));
+                }
+                if (lane == 0) {
+                    *(QK_GLOBAL float *)(y + row) = r;
+                    const uint64_t k = argkey(r, row);
+                    best = k > best ? k : best;
+                }
+                acc = 0.0f;
+            }
         }
-        float r = acc;
-        if (FUSED) {
-            r = __fadd_rn(r, swz_xor4(r));
-            r = __fadd_rn(r, swz_xor1(r));
-            r = __fadd_rn(r, swz_xor2(r));
-        }
-        if (lane == 0) {
-            *(QK_GLOBAL float *)(y + row) = r;
-            const uint64_t k = argkey(r, row);
-            best = k > best ? k : best;
-        }
+        cur = nxt;
+        sp = nsp;
+        tile = ntile;
+        c = nc;
     }
 }
 
 // One launch, up to 16 descriptors. Workgroups [wg0, wg0 + nwg) of a
-// launch belong to descriptor d.
+// launch belong to descriptor d. The first workgroup of every descriptor
+// travels as 16-bit fields of the first eight arguments, which the build
+// preloads into SGPRs (-amdgpu-kernarg-preload-count=8): a workgroup finds
+// its descriptor without a memory round trip, then fetches the 64-byte
+// descriptor with one scalar load. Kernel-argument loads are on every
+// workgroup's critical path and each dependent one costs a trip to memory,
+// so a search that reads wg0 descriptor by descriptor would cost one trip
+// per descriptor passed.
+__device__ __forceinline__ int wg0_of(uint32_t t, int hi) { return (int)(hi ? t >> 16 : t & 0xffffu); }
+
 template <bool FUSED>
-__global__ __launch_bounds__(256, 6) void k_gemv(GemvArgs args, uint64_t *__restrict__ amax_partial,
+__global__ __launch_bounds__(256, 5) void k_gemv(uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3,
+                                              uint32_t t4, uint32_t t5, uint32_t t6, uint32_t t7,
+                                              KArgs args, uint64_t *__restrict__ amax_partial,
                                               uint32_t *__restrict__ zero_ctr) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    if (zero_ctr && blockIdx.x == 0 && threadIdx.x == 0) *zero_ctr = 0;   // top-k candidate counter
+    const uint32_t tab[8] = {t0, t1, t2, t3, t4, t5, t6, t7};
+    const int bx = (int)blockIdx.x;
+    // di = number of later descriptors whose first workgroup is <= bx,
+    // counted with sign bits (scalar arithmetic, no lane masks)
     int di = 0;
-    while (di + 1 < args.count && (int)blockIdx.x >= args.d[di + 1].wg0) di++;
-    const GemvDesc &D = args.d[di];
+#pragma unroll
+    for (int i = 1; i < QK_GROUP_MAX_DEV; i++) di += (int)((uint32_t)(wg0_of(tab[i >> 1], i & 1) - 1 - bx) >> 31);
+    // the whole descriptor in one s_load_dwordx16
+    typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+    const u32x16 raw = *reinterpret_cast<const u32x16 *>(&args.d[di]);
+    KDesc D;
+    __builtin_memcpy(&D, &raw, sizeof(KDesc));
     const int lw = (int)blockIdx.x - D.wg0;
     uint64_t best = 0;
     switch (D.type) {
-        case 12: run_kq<12, FUSED>(D, lw, D.nwg, lds, best); break;
-        case 13: run_kq<13, FUSED>(D, lw, D.nwg, lds, best); break;
-        case 14: run_kq<14, FUSED>(D, lw, D.nwg, lds, best); break;
+        case 12:
+            if (D.p == 4) run_kq<12, 2, FUSED>(D, lw, D.nwg, lds, best);
+            else if (D.p == 8) run_kq<12, 3, FUSED>(D, lw, D.nwg, lds, best);
+            else run_kq<12, 4, FUSED>(D, lw, D.nwg, lds, best);
+            break;
+        case 13:
+            if (D.p == 4) run_kq<13, 2, FUSED>(D, lw, D.nwg, lds, best);
+            else if (D.p == 8) run_kq<13, 3, FUSED>(D, lw, D.nwg, lds, best);
+            else run_kq<13, 4, FUSED>(D, lw, D.nwg, lds, best);
+            break;
+        case 14:
+            if (D.p == 4) run_kq<14, 2, FUSED>(D, lw, D.nwg, lds, best);
+            else if (D.p == 8) run_kq<14, 3, FUSED>(D, lw, D.nwg, lds, best);
+            else run_kq<14, 4, FUSED>(D, lw, D.nwg, lds, best);
+            break;
         default: run_q80<FUSED>(D, lw, D.nwg, lds, best); break;
     }
     if (amax_partial) {
@@ -422,6 +673,9 @@ __global__ __launch_bounds__(256, 6) void k_gemv(GemvArgs args, uint64_t *__rest
             amax_partial[blockIdx.x] = m;
         }
     }
+    // Top-k candidate counter for the LM head's filter kernel, which runs
+    // after this one on the same stream.
+    if (zero_ctr && blockIdx.x == 0 && threadIdx.x == 0) *zero_ctr = 0;
 }
 
 void gemv_plan(GemvDesc &d) {
@@ -433,8 +687,9 @@ void gemv_plan(GemvDesc &d) {
     } else {
         d.nb = (int32_t)(d.k / QK_K);
         // groups per row: enough to cover the row in one step up to 16
-        // super-blocks (k <= 4096), so a row costs one memory latency
-        int p = 1;
+        // super-blocks (k <= 4096), so a row costs one memory latency;
+        // at least 4 (the kernel is instantiated for 4, 8 and 16)
+        int p = 4;
         while (p < 16 && p < d.nb) p *= 2;
         d.p = p;
         d.rows_per_tile = 4 * (16 / p);
@@ -446,8 +701,8 @@ void gemv_plan(GemvDesc &d) {
     d.nwg = d.ntiles;
 }
 
-// Rows are not staged, so any row length up to the activation limit works.
-int64_t gemv_max_row_bytes() { return (int64_t)1 << 40; }
+// Item offsets inside a matrix are 32-bit byte offsets.
+int64_t gemv_max_matrix_bytes() { return (int64_t)0xffffffffLL; }
 
 static hipError_t launch_gemv_impl(GemvArgs &a, int max_wg_per_desc, uint64_t *amax_partial,
                                    uint32_t *zero_ctr, int *grid_out, hipStream_t s) {
@@ -461,21 +716,45 @@ static hipError_t launch_gemv_impl(GemvArgs &a, int max_wg_per_desc, uint64_t *a
         while (k >= 0 && rank(a.d[k]) > rank(t)) { a.d[k + 1] = a.d[k]; k--; }
         a.d[k + 1] = t;
     }
+    // Descriptor starts are 16-bit fields: the grid stays below 2^16
+    // workgroups (grid-stride covers the rest of a large matrix).
+    const int cap = (0xffff / a.count < max_wg_per_desc) ? 0xffff / a.count : max_wg_per_desc;
     int32_t wg = 0, lds = 0;
+    KArgs ka;
+    uint32_t tab[8];
+    for (int i = 0; i < 8; i++) tab[i] = 0xffffffffu;  // unused descriptors: first workgroup 0xffff
     for (int i = 0; i < a.count; i++) {
         GemvDesc &d = a.d[i];
-        d.nwg = d.ntiles < max_wg_per_desc ? d.ntiles : max_wg_per_desc;
+        d.nwg = d.ntiles < cap ? d.ntiles : cap;
         d.wg0 = wg;
         wg += d.nwg;
-        const int32_t need = d.lds_act + (d.type == 8 ? 4 * 64 * 36 : 0);
+        const int32_t need = d.lds_act + 4 * WBUF_BYTES;   // activation row | 4 wave windows
         lds = need > lds ? need : lds;
+        KDesc &k = ka.d[i];
+        k.w = d.w;
+        k.xq = d.xq;
+        k.y = d.y;
+        k.n = (int32_t)d.n;
+        k.type = d.type;
+        k.nb = d.nb;
+        k.p = d.p;
+        k.rows_per_tile = d.rows_per_tile;
+        k.ntiles = d.ntiles;
+        k.nwg = d.nwg;
+        k.lds_act = d.lds_act;
+        k.wg0 = d.wg0;
+        k.pad = 0;
+        const uint32_t sh = 16u * (uint32_t)(i & 1);
+        tab[i >> 1] = (tab[i >> 1] & ~(0xffffu << sh)) | ((uint32_t)d.wg0 << sh);
     }
     a.lds_bytes = lds;
     if (grid_out) *grid_out = wg;
     if (a.fused)
-        hipLaunchKernelGGL(k_gemv<true>, dim3(wg), dim3(256), lds, s, a, amax_partial, zero_ctr);
+        hipLaunchKernelGGL(k_gemv<true>, dim3(wg), dim3(256), lds, s, tab[0], tab[1], tab[2], tab[3], tab[4],
+                           tab[5], tab[6], tab[7], ka, amax_partial, zero_ctr);
     else
-        hipLaunchKernelGGL(k_gemv<false>, dim3(wg), dim3(256), lds, s, a, amax_partial, zero_ctr);
+        hipLaunchKernelGGL(k_gemv<false>, dim3(wg), dim3(256), lds, s, tab[0], tab[1], tab[2], tab[3], tab[4],
+                           tab[5], tab[6], tab[7], ka, amax_partial, zero_ctr);
     return hipGetLastError();
 }
 

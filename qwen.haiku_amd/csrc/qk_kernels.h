@@ -13,7 +13,7 @@ namespace qk {
 // One GEMV of a launch (a row range of one weight matrix).
 struct GemvDesc {
     int32_t type;          // 8, 12, 13, 14
-    int32_t p;             // 8-lane groups cooperating on one row (1,2,4,8)
+    int32_t p;             // 4-lane groups cooperating on one row (4, 8, 16)
     int64_t n, k;
     const uint8_t *w;
     const uint8_t *xq;
@@ -37,7 +37,7 @@ struct GemvArgs {
 
 // Fill p / rows_per_tile / nb for a descriptor.
 void gemv_plan(GemvDesc &d);
-int64_t gemv_max_row_bytes();
+int64_t gemv_max_matrix_bytes();
 // max_wg: workgroups per descriptor at most (the rest grid-stride).
 hipError_t launch_gemv(GemvArgs &a, int max_wg, hipStream_t s);
 
