@@ -220,6 +220,24 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Scales and mins of sub-blocks 2j and 2j+1 (q4k_get_scale_min,
+// simd/quants.h:215-224) without branches: lanes j < 2 and j >= 2 take
+// different forms, and a branch would run both under lane masks.
+__device__ __forceinline__ void scale_min_pair(uint32_t s0, uint32_t s1, uint32_t s2, int j, int32_t &sc0,
+                                               int32_t &m0, int32_t &sc1, int32_t &m1) {
+    const bool hi = j >= 2;
+    const uint32_t sh0 = 16u * (uint32_t)(j & 1), sh1 = sh0 + 8u;   // byte (2j) & 3, (2j+1) & 3
+    auto one = [&](uint32_t sh, int32_t &sc, int32_t &m) {
+        const uint32_t lo_sc = __builtin_amdgcn_ubfe(s0, sh, 6), lo_m = __builtin_amdgcn_ubfe(s1, sh, 6);
+        const uint32_t hi_sc = __builtin_amdgcn_ubfe(s2, sh, 4) | (__builtin_amdgcn_ubfe(s0, sh + 6, 2) << 4);
+        const uint32_t hi_m = __builtin_amdgcn_ubfe(s2, sh + 4, 4) | (__builtin_amdgcn_ubfe(s1, sh + 6, 2) << 4);
+        sc = (int32_t)(hi ? hi_sc : lo_sc);
+        m = (int32_t)(hi ? hi_m : lo_m);
+    };
+    one(sh0, sc0, m0);
+    one(sh1, sc1, m1);
+}
+
 // ---- per-super-block fields and terms -------------------------------------------
 // Lane j (0..3) of a group reads its 32 quant bytes of the super-block
 // (and the header) from the wave's LDS window.
@@ -251,10 +269,9 @@ __device__ __forceinline__ float term_sb(const Raw<12> &r, int b, int j, const u
     const uint8_t *a = act + b * 256 + 64 * j;
     const int32_t slo = dot32(lo, a), shi = dot32(hi, a + 32);
     int32_t sc0, m0, sc1, m1;
-    scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * j, sc0, m0);
-    scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * j + 1, sc1, m1);
-    const int32_t isum = sum4(slo * sc0 + shi * sc1);
-    const int32_t mins = sum4(m0 * bsum_pair(act, nb, b, 2 * j) + m1 * bsum_pair(act, nb, b, 2 * j + 1));
+    scale_min_pair(r.hdr.y, r.hdr.z, r.hdr.w, j, sc0, m0, sc1, m1);
+    const int32_t isum = sum4(__mul24(slo, sc0) + __mul24(shi, sc1));
+    const int32_t mins = sum4(__mul24(m0, bsum_pair(act, nb, b, 2 * j)) + __mul24(m1, bsum_pair(act, nb, b, 2 * j + 1)));
     const float yd = ((const QK_LDS float *)(act + nb * 288))[b];
     return kterm<FUSED>(yd, r.hdr.x & 0xffffu, r.hdr.x >> 16, isum, mins);
 }
@@ -283,10 +300,9 @@ __device__ __forceinline__ float term_sb(const Raw<13> &r, int b, int j, const u
     const uint8_t *a = act + b * 256 + 64 * j;
     const int32_t slo = dot32(lo, a), shi = dot32(hi, a + 32);
     int32_t sc0, m0, sc1, m1;
-    scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * j, sc0, m0);
-    scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * j + 1, sc1, m1);
-    const int32_t isum = sum4(slo * sc0 + shi * sc1);
-    const int32_t mins = sum4(m0 * bsum_pair(act, nb, b, 2 * j) + m1 * bsum_pair(act, nb, b, 2 * j + 1));
+    scale_min_pair(r.hdr.y, r.hdr.z, r.hdr.w, j, sc0, m0, sc1, m1);
+    const int32_t isum = sum4(__mul24(slo, sc0) + __mul24(shi, sc1));
+    const int32_t mins = sum4(__mul24(m0, bsum_pair(act, nb, b, 2 * j)) + __mul24(m1, bsum_pair(act, nb, b, 2 * j + 1)));
     const float yd = ((const QK_LDS float *)(act + nb * 288))[b];
     return kterm<FUSED>(yd, r.hdr.x & 0xffffu, r.hdr.x >> 16, isum, mins);
 }
@@ -340,7 +356,8 @@ __device__ __forceinline__ float term_sb(const Raw<14> &r, int b, int j, const u
     const uint32_t bh = lds32(act + nb * 256 + b * 32 + 2 * s + 8);
     const int32_t b0 = (int16_t)(bl & 0xffffu), b1 = (int16_t)(bl >> 16);
     const int32_t b4 = (int16_t)(bh & 0xffffu), b5 = (int16_t)(bh >> 16);
-    const int32_t v = d0 * sc0 + d1 * sc1 + d4 * sc4 + d5 * sc5 - 32 * (b0 * sc0 + b1 * sc1 + b4 * sc4 + b5 * sc5);
+    const int32_t v = __mul24(d0, sc0) + __mul24(d1, sc1) + __mul24(d4, sc4) + __mul24(d5, sc5) -
+                      32 * (__mul24(b0, sc0) + __mul24(b1, sc1) + __mul24(b4, sc4) + __mul24(b5, sc5));
     const int32_t tot = sum4(v);
     const float yd = ((const QK_LDS float *)(act + nb * 288))[b];
     return q6term(yd, r.d, tot);
@@ -624,11 +641,14 @@ __global__ __launch_bounds__(256, 5) void k_gemv(uint32_t t0, uint32_t t1, uint3
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint32_t tab[8] = {t0, t1, t2, t3, t4, t5, t6, t7};
     const int bx = (int)blockIdx.x;
-    // di = number of later descriptors whose first workgroup is <= bx,
-    // counted with sign bits (scalar arithmetic, no lane masks)
+    // di = the last descriptor whose first workgroup is <= bx (first
+    // workgroups increase with the index; unused entries hold 0xffff)
     int di = 0;
 #pragma unroll
-    for (int i = 1; i < QK_GROUP_MAX_DEV; i++) di += (int)((uint32_t)(wg0_of(tab[i >> 1], i & 1) - 1 - bx) >> 31);
+    for (int i = 1; i < QK_GROUP_MAX_DEV; i++) {
+        if (wg0_of(tab[i >> 1], i & 1) > bx) break;
+        di = i;
+    }
     // the whole descriptor in one s_load_dwordx16
     typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
     const u32x16 raw = *reinterpret_cast<const u32x16 *>(&args.d[di]);
