@@ -162,14 +162,18 @@ __device__ __forceinline__ int32_t bsum_pair(const uint8_t *act, int nb, int b, 
 // aligned superset (aligned in absolute address): piece p (16 bytes) goes
 // to lane p % 64 of load u = p / 64. The superset never reaches a 4 KB page
 // that the range itself does not touch, since pages are 16-byte aligned.
-// WBUF_BYTES bounds an item: 16 super-blocks (16 x 210 B) or 64 Q8_0
-// blocks (64 x 34 B), plus 30 bytes of alignment slack.
-#define WBUF_BYTES 4096
-#define WBUF_LOADS (WBUF_BYTES / 1024)
+// An item is at most 16 super-blocks (16 x 210 B), 4 Q8_0 rows of 32
+// blocks (4 x 1088 B) or 64 Q8_0 blocks (64 x 34 B), plus 30 bytes of
+// alignment slack. A wave loads NL x 1 KB (NL = 4 for the K-quants, 5 for
+// Q8_0 rows) and chunk_store writes every load it issued whole, so the
+// window holds 5 x 1 KB.
+#define WBUF_BYTES 5120
 
-struct Chunk {
-    uint4 v[WBUF_LOADS];
+template <int NL>
+struct ChunkN {
+    uint4 v[NL];
 };
+typedef ChunkN<4> Chunk;
 
 struct Span {
     const uint8_t *base;   // 16-byte aligned start of the superset
@@ -191,11 +195,12 @@ __device__ __forceinline__ Span make_span(const uint8_t *w, int64_t s, int64_t e
 // npc x 16) turns pieces past the item into zeros without a memory access,
 // so the loads need no per-lane guard. A load whose 64 pieces all lie past
 // the item is skipped (a uniform branch).
-__device__ __forceinline__ void chunk_load(Chunk &c, const Span &sp, int lane) {
+template <int NL>
+__device__ __forceinline__ void chunk_load(ChunkN<NL> &c, const Span &sp, int lane) {
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(sp.base), 0, sp.npc * 16, 0x00020000);
 #pragma unroll
-    for (int u = 0; u < WBUF_LOADS; u++) {
+    for (int u = 0; u < NL; u++) {
         if (u * 64 < sp.npc) {
             const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16, u * 1024, 0);
             c.v[u] = make_uint4(v[0], v[1], v[2], v[3]);
@@ -205,9 +210,10 @@ __device__ __forceinline__ void chunk_load(Chunk &c, const Span &sp, int lane) {
 
 // Pieces past the item hold zeros from the range-checked loads; storing
 // them stays inside the window.
-__device__ __forceinline__ void chunk_store(const Chunk &c, uint8_t *wb, const Span &sp, int lane) {
+template <int NL>
+__device__ __forceinline__ void chunk_store(const ChunkN<NL> &c, uint8_t *wb, const Span &sp, int lane) {
 #pragma unroll
-    for (int u = 0; u < WBUF_LOADS; u++)
+    for (int u = 0; u < NL; u++)
         if (u * 64 < sp.npc) *(QK_LDS uint4 *)(wb + 1024 * u + 16 * lane) = c.v[u];
 }
 
@@ -622,6 +628,119 @@ __device__ __forceinline__ void run_q80(const KDesc &D, int lw, int nwg, uint8_t
     }
 }
 
+// Q8_0 rows of 16 or 32 blocks (k = 512 or 1024; the model's Q8_0 width).
+// 4 rows per wave: lane = 16r + 8h + s (row r, parity h, slot s = the AVX
+// lane of bytes 4s..4s+3), 16 rows per workgroup. The wave's 4 rows are
+// one contiguous range (at most 4 x 1088 B) staged through the LDS window.
+// Lane (r, h, s) forms the slot partial p and the scale of the blocks of
+// parity h; lane (r, 0, s) runs the reference's sequential chain over
+// blocks, taking odd blocks from lane (r, 1, s) by DPP (row_shl:8):
+//  fused (AVX2/VNNI): acc_s = fma((float)p_s, s_b, acc_s), then
+//        ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)) over the 8 slot lanes;
+//  separate (scalar/AVX1): sum = sum + (float)(sum_s p_s) * s_b, the slot
+//        sum by DPP inside each 8-lane group.
+// Rows of 16n blocks are 16-byte multiples, so blocks sit at offsets
+// 34b from a 16-byte aligned row start.
+__device__ __forceinline__ int32_t dpp_shl8(int32_t v) {
+    return __builtin_amdgcn_mov_dpp(v, 0x108, 0xF, 0xF, true);   // row_shl:8
+}
+
+template <int NB, bool FUSED>
+__device__ __forceinline__ void run_q80r(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best) {
+    constexpr int ROWB = NB * Q80_BYTES;               // 544 or 1088
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane >> 4, h = (lane >> 3) & 1, s = lane & 7;
+    const int n = D.n, ntiles = D.ntiles;
+    const uint8_t *__restrict__ w = D.w;
+    float *__restrict__ y = D.y;
+    uint8_t *wb = lds + D.lds_act + wave * WBUF_BYTES;
+    auto span = [&](int t) -> Span {
+        const int r0 = t * 16 + wave * 4;
+        const int nr = (n - r0 < 4) ? n - r0 : 4;
+        Span sp;
+        sp.base = w + (uint32_t)r0 * ROWB;
+        sp.ofs = 0;
+        sp.npc = (t < ntiles && nr > 0) ? nr * (ROWB / 16) : 0;
+        return sp;
+    };
+    // activation loads (u16: qs pairs and d) first, then the weights
+    constexpr int TOT = NB * 17, NR = (TOT + 255) / 256;
+    const __amdgpu_buffer_rsrc_t ar = act_rsrc(D.xq, NB * Q80_BYTES);
+    uint32_t av[NR];
+#pragma unroll
+    for (int u = 0; u < NR; u++)
+        av[u] = __builtin_amdgcn_raw_buffer_load_b16(ar, 2 * (256 * u + (int)threadIdx.x), 0, 0);
+    int tile = lw;
+    Span sp = span(tile);
+    ChunkN<5> cur;
+    chunk_load(cur, sp, lane);
+    {
+        // qs[NB][32] as u16 pairs | d[NB] widened to float
+        uint8_t *junk = lds + D.lds_act;
+#pragma unroll
+        for (int u = 0; u < NR; u++) {
+            const int i = 256 * u + (int)threadIdx.x;
+            const int b = i / 17, q = i - b * 17;
+            const uint32_t val = q == 0 ? __float_as_uint(h2f(av[u])) : av[u];
+            uint8_t *dst = q == 0 ? lds + NB * 32 + 4 * b : lds + b * 32 + 2 * q - 2;
+            dst = i < TOT ? dst : junk;
+            if (q == 0) *(QK_LDS uint32_t *)(dst) = val;
+            else *(QK_LDS uint16_t *)(dst) = (uint16_t)val;
+        }
+    }
+    lds_barrier();
+    const QK_LDS uint32_t *aq = (const QK_LDS uint32_t *)(lds);
+    const QK_LDS float *ad = (const QK_LDS float *)(lds + NB * 32);
+    while (tile < ntiles) {
+        const int ntile = tile + nwg;
+        const Span nsp = span(ntile);
+        ChunkN<5> nxt;
+        chunk_load(nxt, nsp, lane);
+        chunk_store(cur, wb, sp, lane);
+        wave_sync();
+        const int nr = sp.npc / (ROWB / 16);
+        const uint8_t *rowp = wb + r * ROWB;
+        float acc = 0.0f;
+#pragma unroll 4
+        for (int i = 0; i < NB / 2; i++) {
+            const int b = 2 * i + h;
+            const int off = b * Q80_BYTES + 2 + 4 * s;     // 2 mod 4 for even b, 0 for odd
+            const int a4 = off & ~3;
+            const uint32_t x0 = lds32(rowp + a4), x1 = lds32(rowp + a4 + 4);
+            const uint32_t w4 = __builtin_amdgcn_alignbyte(x1, x0, (uint32_t)(off & 3));
+            const int32_t p = dot4(w4, aq[b * 8 + s], 0);
+            const float sc = __fmul_rn(h2f(lds_u16(rowp + b * Q80_BYTES)), ad[b]);
+            if (FUSED) {
+                const float po = __int_as_float(dpp_shl8(__float_as_int((float)p)));
+                const float so = __int_as_float(dpp_shl8(__float_as_int(sc)));
+                acc = __builtin_fmaf((float)p, sc, acc);
+                acc = __builtin_fmaf(po, so, acc);
+            } else {
+                const float t = __fmul_rn((float)sum8(p), sc);
+                const float to = __int_as_float(dpp_shl8(__float_as_int(t)));
+                acc = __fadd_rn(acc, t);
+                acc = __fadd_rn(acc, to);
+            }
+        }
+        if (FUSED) {
+            acc = __fadd_rn(acc, swz_xor4(acc));
+            acc = __fadd_rn(acc, swz_xor1(acc));
+            acc = __fadd_rn(acc, swz_xor2(acc));
+        }
+        const int row = tile * 16 + wave * 4 + r;
+        if (r < nr && h == 0 && s == 0) {
+            *(QK_GLOBAL float *)(y + row) = acc;
+            const uint64_t k = argkey(acc, row);
+            best = k > best ? k : best;
+        }
+        wave_sync();                                   // window reads done before the next store
+        cur = nxt;
+        sp = nsp;
+        tile = ntile;
+    }
+}
+
 // One launch, up to 16 descriptors. Workgroups [wg0, wg0 + nwg) of a
 // launch belong to descriptor d. The first workgroup of every descriptor
 // travels as 16-bit fields of the first eight arguments, which the build
@@ -672,7 +791,11 @@ __global__ __launch_bounds__(256, 5) void k_gemv(uint32_t t0, uint32_t t1, uint3
             else if (D.p == 8) run_kq<14, 3, FUSED>(D, lw, D.nwg, lds, best);
             else run_kq<14, 4, FUSED>(D, lw, D.nwg, lds, best);
             break;
-        default: run_q80<FUSED>(D, lw, D.nwg, lds, best); break;
+        default:
+            if (D.p == 4 && D.nb == 32) run_q80r<32, FUSED>(D, lw, D.nwg, lds, best);
+            else if (D.p == 4) run_q80r<16, FUSED>(D, lw, D.nwg, lds, best);
+            else run_q80<FUSED>(D, lw, D.nwg, lds, best);
+            break;
     }
     if (amax_partial) {
         // Workgroup maximum of the argmax keys of every row it wrote.
@@ -701,8 +824,10 @@ __global__ __launch_bounds__(256, 5) void k_gemv(uint32_t t0, uint32_t t1, uint3
 void gemv_plan(GemvDesc &d) {
     if (d.type == 8) {
         d.nb = (int32_t)(d.k / QK8_0);
-        d.p = 1;
-        d.rows_per_tile = 4;
+        // k = 512 / 1024: 4 rows per wave (p = 4); else one row per wave
+        const bool rows4 = d.nb == 16 || d.nb == 32;
+        d.p = rows4 ? 4 : 1;
+        d.rows_per_tile = rows4 ? 16 : 4;
         d.lds_act = (d.nb * 36 + 15) & ~15;
     } else {
         d.nb = (int32_t)(d.k / QK_K);

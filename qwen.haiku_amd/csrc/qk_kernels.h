@@ -13,7 +13,7 @@ namespace qk {
 // One GEMV of a launch (a row range of one weight matrix).
 struct GemvDesc {
     int32_t type;          // 8, 12, 13, 14
-    int32_t p;             // 4-lane groups cooperating on one row (4, 8, 16)
+    int32_t p;             // K-quants: 4-lane groups per row (4, 8, 16); Q8_0: rows per wave (4 or 1)
     int64_t n, k;
     const uint8_t *w;
     const uint8_t *xq;
