@@ -5,13 +5,16 @@
 // dispatch. A 256-thread workgroup computes row tiles of one descriptor
 // (grid-stride over tiles).
 //
-// Loads. A wave's work item is one contiguous byte range of W (whole rows,
-// or 16 super-blocks of one long row). The wave reads it with
-// lane-contiguous 16-byte loads, so every load instruction covers 1 KB of
-// consecutive bytes, into registers one item ahead of the arithmetic. The
-// registers are then written to a wave-private LDS window, from which each
-// lane reads the fields of its block. Memory instructions per byte are the
-// minimum, whatever the block size (34, 144, 176 or 210 bytes).
+// Loads. All weight loads are buffer loads whose range check covers the
+// wave's current work item (rows of one tile), so no lane needs a guard.
+//  - Q4_K / Q5_K (144 / 176-byte blocks, 16-byte aligned): each lane loads
+//    the fields of its block straight into registers (3 / 5 loads).
+//  - Q6_K / Q8_0 (210 / 34-byte blocks): the wave reads its item with
+//    lane-contiguous 16-byte loads (each load instruction covers 1 KB of
+//    consecutive bytes) and passes it through a wave-private LDS window,
+//    from which lanes read their fields at any alignment. Direct loads
+//    would take 9 (Q6_K) or 24 (Q8_0) instructions per lane.
+// Loads run one work item ahead of the arithmetic.
 //
 // Arithmetic. An aligned group of 4 lanes owns one 256-element super-block:
 // each lane takes 32 quant bytes and runs v_dot4 against the activation
@@ -245,8 +248,8 @@ __device__ __forceinline__ void scale_min_pair(uint32_t s0, uint32_t s1, uint32_
 }
 
 // ---- per-super-block fields and terms -------------------------------------------
-// Lane j (0..3) of a group reads its 32 quant bytes of the super-block
-// (and the header) from the wave's LDS window.
+// Lane j (0..3) of a group holds its 32 quant bytes of the super-block and
+// the header (Q4_K / Q5_K: loaded directly; Q6_K: read from the window).
 template <int T> struct Raw;
 template <> struct Raw<12> { uint4 hdr, q0, q1; };
 template <> struct Raw<13> { uint4 hdr, q0, q1, h0, h1; };
@@ -255,14 +258,7 @@ template <> struct Raw<14> { uint32_t l[9], h[9], sh, sc, sc2, d; };
 // Q4_K (simd/quants.h:267-306): lane j holds chunk c = j, qs[32j..32j+32):
 // low nibbles pair with q8[64j..64j+32) under scale 2j, high nibbles with
 // q8[64j+32..64j+64) under scale 2j+1; mins 2j, 2j+1 meet bsum pairs 2j,
-// 2j+1. off is 16-byte aligned (144-byte blocks; W is 16-byte aligned).
-__device__ __forceinline__ void read_sb(Raw<12> &r, const uint8_t *wb, int off, int j) {
-    const uint8_t *blk = wb + off;
-    r.hdr = lds16(blk);
-    r.q0 = lds16(blk + 16 + 32 * j);
-    r.q1 = lds16(blk + 32 + 32 * j);
-}
-
+// 2j+1.
 template <bool FUSED>
 __device__ __forceinline__ float term_sb(const Raw<12> &r, int b, int j, const uint8_t *act, int nb) {
     const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
@@ -283,15 +279,6 @@ __device__ __forceinline__ float term_sb(const Raw<12> &r, int b, int j, const u
 }
 
 // Q5_K (simd/quants.h:310-351): as Q4_K plus bit 2j / 2j+1 of qh[l].
-__device__ __forceinline__ void read_sb(Raw<13> &r, const uint8_t *wb, int off, int j) {
-    const uint8_t *blk = wb + off;
-    r.hdr = lds16(blk);
-    r.h0 = lds16(blk + 16);
-    r.h1 = lds16(blk + 32);
-    r.q0 = lds16(blk + 48 + 32 * j);
-    r.q1 = lds16(blk + 64 + 32 * j);
-}
-
 template <bool FUSED>
 __device__ __forceinline__ float term_sb(const Raw<13> &r, int b, int j, const uint8_t *act, int nb) {
     const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
@@ -401,7 +388,7 @@ __device__ __forceinline__ uint64_t argkey(float v, int64_t row) {
     return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)row);
 }
 
-// Rows of one K-quant descriptor handled by this workgroup: tiles
+// Q6_K rows handled by this workgroup (the LDS-window path): tiles
 // lw, lw+nwg, ... of 4 waves x 16/P rows. A row's P = 2^LP groups each take
 // one super-block of a step (P super-blocks); the P terms of a step are
 // gathered with ds_bpermute and added to the row sum in super-block order.
@@ -498,6 +485,96 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
         nit = it + 1;
         if (nit == niter) { nit = 0; ntile += nwg; }
         nsp = span(ntile, nit);
+    }
+}
+
+// Q4_K / Q5_K: the same tiles and gather as run_kq, with each lane's block
+// fields loaded straight into registers (buffer loads, range-checked by
+// the item).
+__device__ __forceinline__ uint4 bl128(__amdgpu_buffer_rsrc_t r, int off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void load_direct(Raw<12> &r, __amdgpu_buffer_rsrc_t rs, int off, int j) {
+    r.hdr = bl128(rs, off);
+    r.q0 = bl128(rs, off + 16 + 32 * j);
+    r.q1 = bl128(rs, off + 32 + 32 * j);
+}
+__device__ __forceinline__ void load_direct(Raw<13> &r, __amdgpu_buffer_rsrc_t rs, int off, int j) {
+    r.hdr = bl128(rs, off);
+    r.h0 = bl128(rs, off + 16);
+    r.h1 = bl128(rs, off + 32);
+    r.q0 = bl128(rs, off + 48 + 32 * j);
+    r.q1 = bl128(rs, off + 64 + 32 * j);
+}
+template <int TYPE, int LP, bool FUSED>
+__device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best) {
+    constexpr int BB = TYPE == 12 ? Q4K_BYTES : Q5K_BYTES;
+    constexpr int P = 1 << LP;
+    constexpr int RPW = 16 >> LP;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = lane >> 2, j = lane & 3;
+    const int team = grp >> LP, g = grp & (P - 1);
+    const int nb = D.nb, ntiles = D.ntiles, n = D.n;
+    const int niter = (nb + P - 1) >> LP;
+    const uint32_t rowb = (uint32_t)nb * BB;
+    const uint8_t *__restrict__ w = D.w;
+    float *__restrict__ y = D.y;
+    const int src0 = team * P * 4;
+    const int lofs = (team * nb + g) * BB;
+    auto rsrc = [&](int t, int i) -> __amdgpu_buffer_rsrc_t {
+        const int r0 = t * (4 * RPW) + wave * RPW;
+        uint32_t len;
+        if (niter == 1) {
+            const int nr = (n - r0 < RPW) ? n - r0 : RPW;
+            len = (uint32_t)nr * rowb;
+        } else {
+            const int nbl = (nb - i * P < P) ? nb - i * P : P;
+            len = (uint32_t)nbl * BB;
+        }
+        if (t >= ntiles || r0 >= n) len = 0;
+        const uint32_t s0 = (uint32_t)r0 * rowb + (uint32_t)(i * P * BB);
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w + s0), 0, (int)len, 0x00020000);
+    };
+    const __amdgpu_buffer_rsrc_t ar = act_rsrc(D.xq, nb * Q8K_BYTES);
+    Stage st0;
+    stage_q8k_load(st0, ar, 0, nb * 73);
+    int tile = lw, it = 0;
+    Raw<TYPE> cur;
+    load_direct(cur, rsrc(tile, it), lofs, j);
+    int ntile = tile, nit = it + 1;
+    if (nit == niter) { nit = 0; ntile += nwg; }
+    stage_q8k_rest(st0, ar, nb, lds, lds + D.lds_act);
+    lds_barrier();
+    float sum = 0.0f;
+    while (tile < ntiles) {
+        Raw<TYPE> nxt;
+        load_direct(nxt, rsrc(ntile, nit), lofs, j);
+        const float t = term_sb<FUSED>(cur, it * P + g, j, lds, nb);
+        float tg[P];
+#pragma unroll
+        for (int g2 = 0; g2 < P; g2++) tg[g2] = __shfl(t, src0 + 4 * g2);
+        const int lim = (nb - it * P < P) ? nb - it * P : P;
+#pragma unroll
+        for (int g2 = 0; g2 < P; g2++)
+            if (g2 < lim) sum += tg[g2];
+        if (it == niter - 1) {
+            const int row = tile * (4 * RPW) + wave * RPW + team;
+            if (FUSED) sum = bcast8(sum);
+            if (row < n && g == 0 && j == 0) {
+                *(QK_GLOBAL float *)(y + row) = sum;
+                const uint64_t k = argkey(sum, row);
+                best = k > best ? k : best;
+            }
+            sum = 0.0f;
+        }
+        cur = nxt;
+        tile = ntile;
+        it = nit;
+        ntile = tile;
+        nit = it + 1;
+        if (nit == niter) { nit = 0; ntile += nwg; }
     }
 }
 
@@ -777,14 +854,14 @@ __global__ __launch_bounds__(256, 5) void k_gemv(uint32_t t0, uint32_t t1, uint3
     uint64_t best = 0;
     switch (D.type) {
         case 12:
-            if (D.p == 4) run_kq<12, 2, FUSED>(D, lw, D.nwg, lds, best);
-            else if (D.p == 8) run_kq<12, 3, FUSED>(D, lw, D.nwg, lds, best);
-            else run_kq<12, 4, FUSED>(D, lw, D.nwg, lds, best);
+            if (D.p == 4) run_kqd<12, 2, FUSED>(D, lw, D.nwg, lds, best);
+            else if (D.p == 8) run_kqd<12, 3, FUSED>(D, lw, D.nwg, lds, best);
+            else run_kqd<12, 4, FUSED>(D, lw, D.nwg, lds, best);
             break;
         case 13:
-            if (D.p == 4) run_kq<13, 2, FUSED>(D, lw, D.nwg, lds, best);
-            else if (D.p == 8) run_kq<13, 3, FUSED>(D, lw, D.nwg, lds, best);
-            else run_kq<13, 4, FUSED>(D, lw, D.nwg, lds, best);
+            if (D.p == 4) run_kqd<13, 2, FUSED>(D, lw, D.nwg, lds, best);
+            else if (D.p == 8) run_kqd<13, 3, FUSED>(D, lw, D.nwg, lds, best);
+            else run_kqd<13, 4, FUSED>(D, lw, D.nwg, lds, best);
             break;
         case 14:
             if (D.p == 4) run_kq<14, 2, FUSED>(D, lw, D.nwg, lds, best);
