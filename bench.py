@@ -208,8 +208,22 @@ def cpu_baseline(synth, seconds=10.0):
                       f"through tensor_matmul_*_f32, {dt:.1f} s, dispatch {label}"}
 
 
-def config3_extras(torch, qk, synth, lib, steps):
-    """Config 3 at M = 512 / 128 / 2048 (Q4_K) and the Q6_K down projection."""
+def mfma_peak():
+    """Dense int8 MFMA throughput measured on this GPU by
+    qwen.haiku_amd/mfma_peak (built with libqk), or None if it is not built."""
+    import subprocess
+    exe = os.path.join(ROOT, "qwen.haiku_amd", "mfma_peak")
+    if not os.path.exists(exe):
+        return None
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    if r.returncode != 0:
+        raise RuntimeError(f"mfma_peak failed: {r.stderr.strip()}")
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def config3_extras(torch, qk, synth, lib, steps, peak_tops=None):
+    """Config 3 at M = 512 / 128 / 2048 (Q4_K) and the Q6_K down projection.
+    peak_tops: the measured int8 MFMA throughput, for a second fraction."""
     extra = {}
     for (t, n3, k3, m3) in ((12, 3584, 1024, 512), (12, 3584, 1024, 128), (12, 3584, 1024, 2048),
                             (14, 1024, 3584, 512)):
@@ -224,6 +238,9 @@ def config3_extras(torch, qk, synth, lib, steps):
             "frac_of_5POPS": round(ops * steps / sb / 5.0e15, 4),
             "frac_of_bw_x_ai": round((ops * steps / sb) / (HBM_PEAK_GBS * 1e9 * ops / alg), 4),
             "copies": c3}
+        if peak_tops:
+            extra[f"config3_gemm_{name}_m{m3}_n{n3}_k{k3}"]["frac_of_measured_mfma_peak"] = round(
+                ops * steps / sb / (peak_tops * 1e12), 4)
     return extra
 
 
@@ -287,7 +304,11 @@ def main():
         p2, c2, s2 = bench_config2(torch, qk, synth, lib, st2, 5)
         extra["config2_lmhead_q6k_argmax_top40"] = {"GB/s": round(p2 * st2 / s2 / 1e9, 2),
                                                     "us_per_call": round(s2 / st2 * 1e6, 3), "copies": c2}
-        extra.update(config3_extras(torch, qk, synth, lib, max(20, a.steps // 10)))
+        peak = mfma_peak()
+        if peak:
+            extra["mfma_int8_peak_measured"] = peak
+        peak_tops = peak["mfma_i32_32x32x32_i8_tops"] if peak else None
+        extra.update(config3_extras(torch, qk, synth, lib, max(20, a.steps // 10), peak_tops))
         out["extra"] = extra
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(synth, a.cpu_seconds)

@@ -323,6 +323,15 @@ __device__ __forceinline__ void store_w(GL &s, const WRaw14 &a, int r, int q) {
     lds_st16(&s.b[0][r][128 * h + 96 + l0], o3[0], o3[1], o3[2], o3[3]);
 }
 
+// Workgroup barrier over LDS only: it waits for this thread's LDS
+// accesses, not for global loads in flight, so the next super-block's
+// loads stay outstanding across it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <int TYPE> struct WRawOf;
 template <> struct WRawOf<12> { typedef WRaw12 T; };
 template <> struct WRawOf<13> { typedef WRaw13 T; };
@@ -357,14 +366,14 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t *__restrict__ w, int
     const v16i zero = {0};
 
     for (int i = 0; i < nb; i++) {
-        __syncthreads();                                     // previous super-block's reads done
+        lds_barrier();                                       // previous super-block's reads done
         store_act(s, ar, st, sq);
         store_w(s, wr, st, sq);
         if (i + 1 < nb) {                                    // next super-block in flight during compute
             load_act(ar, xrow, sq, i + 1);
             load_w(wr, wrow, sq, i + 1);
         }
-        __syncthreads();
+        lds_barrier();
 
         int32_t isum[16];
         if (TYPE == 14) {
