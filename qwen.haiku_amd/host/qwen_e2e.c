@@ -32,13 +32,24 @@
  * Output: one JSON line on stdout with the token stream, prefill and
  * decode tok/s, and non-degeneracy figures; progress lines on stderr.
  *
+ * GGUF round trip: --write-gguf PATH also writes the random model as a
+ * GGUF v3 file (gguf_write.c: the qwen35 config keys slm_load_config
+ * reads, slm/qwen.c:59-160; a synthetic vocabulary of distinct strings for
+ * tokenizer_load, slm/tokenizer.c:216-275; every tensor under the names
+ * slm_load_weights resolves, slm/qwen.c:174-252). --gguf PATH loads a
+ * model through the reference's own slm_model_load (slm/model.c:1130) in
+ * place of building one; the prompt comes from its own seeded stream, so
+ * both modes run the same workload.
+ *
  * Usage: qwen_e2e [--prompt P] [--gen G] [--seed S] [--layers L]
+ *                 [--write-gguf PATH | --gguf PATH]
  */
 #if defined(QK_E2E_GPU)
 #include "qk_seam.c"
 #endif
 #include "qwen.c"
 #include "sampler.c"
+#include "gguf_write.c"
 
 #include <time.h>
 
@@ -55,6 +66,18 @@ static uint64_t e2e_u64(void) {
 static double e2e_unif(void) { return (double)(e2e_u64() >> 11) * (1.0 / 9007199254740992.0); }
 
 static int32_t e2e_int(int32_t lo, int32_t hi) { return lo + (int32_t)(e2e_u64() % (uint64_t)(hi - lo + 1)); }
+
+/* The prompt's own stream: the same tokens whether the weights are drawn
+ * here or loaded from a file. */
+static uint64_t e2e_prompt_state;
+
+static int32_t e2e_prompt_token(int32_t vocab) {
+    uint64_t z = (e2e_prompt_state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (int32_t)(z % (uint64_t)vocab);
+}
 
 static uint16_t e2e_f16(double v) {
     _Float16 h = (_Float16)(float)v;
@@ -131,7 +154,12 @@ static void e2e_q8_0(q8_0_block *b, int64_t n, double sigma) {
     }
 }
 
-static void e2e_set(struct slm_tensor *t, const void *data, int32_t type, int64_t n0, int64_t n1) {
+/* When writing a GGUF: every tensor built is also recorded under its
+ * slm_load_weights name. */
+static struct gw *e2e_gw;
+
+static void e2e_set(struct slm_tensor *t, const char *name, const void *data, int32_t type, int64_t n0,
+                    int64_t n1, uint64_t bytes) {
     t->data = data;
     t->type = type;
     t->n_dims = n1 > 1 ? 2 : 1;
@@ -139,40 +167,78 @@ static void e2e_set(struct slm_tensor *t, const void *data, int32_t type, int64_
     t->shape[1] = n1;
     t->shape[2] = 1;
     t->shape[3] = 1;
+    if (e2e_gw) {
+        const uint64_t shape[2] = {(uint64_t)n0, (uint64_t)n1};
+        gw_tensor(e2e_gw, name, (uint32_t)type, (uint32_t)t->n_dims, shape, data, bytes);
+    }
 }
 
 /* Quantized weight (GGUF shape (k, out_f)): out_f rows of k elements. */
-static void e2e_mat(struct slm_tensor *t, int32_t type, int64_t k, int64_t out_f, double scale) {
+static void e2e_mat(struct slm_tensor *t, const char *name, int32_t type, int64_t k, int64_t out_f, double scale) {
     const double sigma = scale / sqrt((double)k);
     void *p = NULL;
+    uint64_t bytes = 0;
     switch (type) {
         case GGUF_TT_Q4_K:
             p = oom(calloc((size_t)(out_f * k / QK_K), sizeof(q4k_block)));
             e2e_q4k(p, out_f * k / QK_K, sigma);
+            bytes = (uint64_t)(out_f * k / QK_K) * sizeof(q4k_block);
             break;
         case GGUF_TT_Q5_K:
             p = oom(calloc((size_t)(out_f * k / QK_K), sizeof(q5k_block)));
             e2e_q5k(p, out_f * k / QK_K, sigma);
+            bytes = (uint64_t)(out_f * k / QK_K) * sizeof(q5k_block);
             break;
         case GGUF_TT_Q6_K:
             p = oom(calloc((size_t)(out_f * k / QK_K), sizeof(q6k_block)));
             e2e_q6k(p, out_f * k / QK_K, sigma);
+            bytes = (uint64_t)(out_f * k / QK_K) * sizeof(q6k_block);
             break;
         default:
             p = oom(calloc((size_t)(out_f * k / QK8_0), sizeof(q8_0_block)));
             e2e_q8_0(p, out_f * k / QK8_0, sigma);
+            bytes = (uint64_t)(out_f * k / QK8_0) * sizeof(q8_0_block);
             break;
     }
-    e2e_set(t, p, type, k, out_f);
+    e2e_set(t, name, p, type, k, out_f, bytes);
 #if defined(QK_E2E_GPU)
     qk_seam_register(p, type, k, out_f);
 #endif
 }
 
-static void e2e_vec(struct slm_tensor *t, int64_t n0, int64_t n1, double base, double spread) {
+static void e2e_vec(struct slm_tensor *t, const char *name, int64_t n0, int64_t n1, double base, double spread) {
     float *p = (float *)oom(calloc((size_t)(n0 * n1), sizeof(float)));
     for (int64_t i = 0; i < n0 * n1; i++) p[i] = (float)(base + spread * (2.0 * e2e_unif() - 1.0));
-    e2e_set(t, p, GGUF_TT_F32, n0, n1);
+    e2e_set(t, name, p, GGUF_TT_F32, n0, n1, (uint64_t)(n0 * n1) * sizeof(float));
+}
+
+/* Vocabulary strings of the written GGUF: distinct, none of them a chat
+ * special, so tokenizer_load finds no specials and eot_id stays -1 as in
+ * the built model. */
+static size_t e2e_token_name(uint64_t i, char *buf, size_t cap) {
+    return (size_t)snprintf(buf, cap, "<t%llu>", (unsigned long long)i);
+}
+
+/* The qwen35 keys slm_load_config reads (slm/qwen.c:59-160). */
+static void e2e_write_config(struct gw *w, const struct slm_config *c) {
+    gw_kv_str(w, "general.architecture", "qwen35");
+    gw_kv_u32(w, "general.alignment", 32);
+    gw_kv_u32(w, "qwen35.embedding_length", (uint32_t)c->hidden_dim);
+    gw_kv_u32(w, "qwen35.block_count", (uint32_t)c->n_layers);
+    gw_kv_u32(w, "qwen35.attention.head_count", (uint32_t)c->n_heads);
+    gw_kv_u32(w, "qwen35.attention.head_count_kv", (uint32_t)c->n_kv_heads);
+    gw_kv_u32(w, "qwen35.feed_forward_length", (uint32_t)c->ffn_dim);
+    gw_kv_u32(w, "qwen35.context_length", 4096);
+    gw_kv_f32(w, "qwen35.rope.freq_base", c->rope_theta);
+    gw_kv_f32(w, "qwen35.attention.layer_norm_rms_epsilon", c->norm_eps);
+    gw_kv_u32(w, "qwen35.attention.key_length", (uint32_t)c->head_dim);
+    gw_kv_u32(w, "qwen35.rope.dimension_count", (uint32_t)c->rope_dim);
+    gw_kv_i32_array(w, "qwen35.rope.dimension_sections", c->rope_sections, 4);
+    gw_kv_u32(w, "qwen35.full_attention_interval", (uint32_t)c->full_attn_interval);
+    gw_kv_u32(w, "qwen35.ssm.group_count", (uint32_t)c->linear_n_heads);
+    gw_kv_u32(w, "qwen35.ssm.state_size", (uint32_t)c->linear_k_head_dim);
+    gw_kv_u32(w, "qwen35.ssm.conv_kernel", (uint32_t)c->linear_conv_kernel);
+    gw_kv_str_array(w, "tokenizer.ggml.tokens", (uint64_t)c->vocab_size, e2e_token_name);
 }
 
 static double e2e_now(void) {
@@ -184,18 +250,23 @@ static double e2e_now(void) {
 int main(int argc, char **argv) {
     int32_t n_prompt = 512, n_gen = 256, n_layers = 24;
     uint64_t seed = 0;
+    const char *write_path = NULL, *load_path = NULL;
     for (int i = 1; i + 1 < argc; i += 2) {
         if (strcmp(argv[i], "--prompt") == 0) n_prompt = atoi(argv[i + 1]);
         else if (strcmp(argv[i], "--gen") == 0) n_gen = atoi(argv[i + 1]);
         else if (strcmp(argv[i], "--seed") == 0) seed = (uint64_t)strtoull(argv[i + 1], NULL, 10);
         else if (strcmp(argv[i], "--layers") == 0) n_layers = atoi(argv[i + 1]);
+        else if (strcmp(argv[i], "--write-gguf") == 0) write_path = argv[i + 1];
+        else if (strcmp(argv[i], "--gguf") == 0) load_path = argv[i + 1];
     }
-    if (n_prompt < 2 || n_gen < 1 || n_layers < 1) {
-        fprintf(stderr, "usage: %s [--prompt P>=2] [--gen G>=1] [--seed S] [--layers L>=1]\n", argv[0]);
+    if (n_prompt < 2 || n_gen < 1 || n_layers < 1 || (write_path && load_path)) {
+        fprintf(stderr, "usage: %s [--prompt P>=2] [--gen G>=1] [--seed S] [--layers L>=1] "
+                        "[--write-gguf PATH | --gguf PATH]\n", argv[0]);
         return 2;
     }
     simd_init();
     e2e_state = seed * 0x2545F4914F6CDD1Dull + 1;
+    e2e_prompt_state = seed * 0x2545F4914F6CDD1Dull + 2;
 
     struct slm_config cfg;
     memset(&cfg, 0, sizeof(cfg));
@@ -228,52 +299,92 @@ int main(int argc, char **argv) {
     const int64_t QKV = 2 * 16 * 128 + 16 * 128, INNER = 16 * 128;
 
     double tb = e2e_now();
-    struct slm_model *m = (struct slm_model *)oom(calloc(1, sizeof(struct slm_model)));
-    m->cfg = cfg;
-    struct slm_weights *W = &m->W;
-    e2e_mat(&W->tok_embd, GGUF_TT_Q6_K, H, V, 1.5);
-    W->output = W->tok_embd;                                   /* tied (slm/qwen.c:182-183) */
-    e2e_vec(&W->output_norm, H, 1, 1.0, 0.02);
-    W->layers = (struct slm_layer *)oom(calloc((size_t)n_layers, sizeof(struct slm_layer)));
-    for (int32_t L = 0; L < n_layers; L++) {
-        struct slm_layer *Lw = &W->layers[L];
-        Lw->is_ssm = (L % cfg.full_attn_interval) != cfg.full_attn_interval - 1;
-        e2e_vec(&Lw->attn_norm, H, 1, 1.0, 0.02);
-        e2e_vec(&Lw->ffn_norm, H, 1, 1.0, 0.02);
-        e2e_mat(&Lw->ffn_gate, GGUF_TT_Q4_K, H, F, 1.0);
-        e2e_mat(&Lw->ffn_up, GGUF_TT_Q4_K, H, F, 1.0);
-        e2e_mat(&Lw->ffn_down, GGUF_TT_Q6_K, F, H, 0.5);
-        if (Lw->is_ssm) {
-            e2e_mat(&Lw->attn_qkv, GGUF_TT_Q5_K, H, QKV, 1.0);
-            e2e_mat(&Lw->attn_gate, GGUF_TT_Q4_K, H, INNER, 1.0);
-            e2e_vec(&Lw->ssm_a, 16, 1, -1.25, 0.75);
-            e2e_mat(&Lw->ssm_alpha, GGUF_TT_Q8_0, H, 16, 1.0);
-            e2e_mat(&Lw->ssm_beta, GGUF_TT_Q8_0, H, 16, 1.0);
-            e2e_vec(&Lw->ssm_conv1d, 4, QKV, 0.0, 0.5);
-            e2e_vec(&Lw->ssm_dt_bias, 16, 1, 0.0, 0.1);
-            e2e_vec(&Lw->ssm_norm, 128, 1, 1.0, 0.02);
-            e2e_mat(&Lw->ssm_out, GGUF_TT_Q5_K, INNER, H, 0.5);
-        } else {
-            e2e_mat(&Lw->attn_q, GGUF_TT_Q5_K, H, 2 * 8 * 256, 1.0);
-            e2e_mat(&Lw->attn_k, GGUF_TT_Q4_K, H, 2 * 256, 1.0);
-            e2e_mat(&Lw->attn_v, GGUF_TT_Q6_K, H, 2 * 256, 1.0);
-            e2e_vec(&Lw->attn_q_norm, 256, 1, 1.0, 0.02);
-            e2e_vec(&Lw->attn_k_norm, 256, 1, 1.0, 0.02);
-            e2e_mat(&Lw->attn_out, GGUF_TT_Q4_K, 8 * 256, H, 0.5);
+    struct slm_model *m = NULL;
+    struct gw gw;
+    if (load_path) {
+        /* the reference's loader: config keys, tensor names, tokenizer */
+        m = slm_model_load(load_path);
+        if (!slm_model_loaded(m)) {
+            fprintf(stderr, "[e2e] slm_model_load(%s): %s\n", load_path, slm_model_error(m));
+            return 1;
+        }
+        if (m->cfg.n_layers != n_layers || m->cfg.vocab_size != cfg.vocab_size) {
+            fprintf(stderr, "[e2e] %s holds %d layers / vocab %d; expected %d / %d\n", load_path,
+                    m->cfg.n_layers, m->cfg.vocab_size, n_layers, cfg.vocab_size);
+            return 1;
+        }
+        /* the run's KV-cache length and ids, as the built model sets them
+           (the forward pass reads neither bos nor eos) */
+        m->cfg.max_position = cfg.max_position;
+        m->cfg.bos_id = cfg.bos_id;
+        m->cfg.eos_id = cfg.eos_id;
+    } else {
+        if (write_path) {
+            gw_init(&gw);
+            e2e_write_config(&gw, &cfg);
+            e2e_gw = &gw;
+        }
+        m = (struct slm_model *)oom(calloc(1, sizeof(struct slm_model)));
+        m->cfg = cfg;
+        struct slm_weights *W = &m->W;
+        e2e_mat(&W->tok_embd, "token_embd.weight", GGUF_TT_Q6_K, H, V, 1.5);
+        W->output = W->tok_embd;                               /* tied (slm/qwen.c:182-183) */
+        e2e_vec(&W->output_norm, "output_norm.weight", H, 1, 1.0, 0.02);
+        W->layers = (struct slm_layer *)oom(calloc((size_t)n_layers, sizeof(struct slm_layer)));
+        char nm[96];
+#define NM(fmt) (snprintf(nm, sizeof(nm), fmt, L), nm)
+        for (int32_t L = 0; L < n_layers; L++) {
+            struct slm_layer *Lw = &W->layers[L];
+            Lw->is_ssm = (L % cfg.full_attn_interval) != cfg.full_attn_interval - 1;
+            e2e_vec(&Lw->attn_norm, NM("blk.%d.attn_norm.weight"), H, 1, 1.0, 0.02);
+            e2e_vec(&Lw->ffn_norm, NM("blk.%d.post_attention_norm.weight"), H, 1, 1.0, 0.02);
+            e2e_mat(&Lw->ffn_gate, NM("blk.%d.ffn_gate.weight"), GGUF_TT_Q4_K, H, F, 1.0);
+            e2e_mat(&Lw->ffn_up, NM("blk.%d.ffn_up.weight"), GGUF_TT_Q4_K, H, F, 1.0);
+            e2e_mat(&Lw->ffn_down, NM("blk.%d.ffn_down.weight"), GGUF_TT_Q6_K, F, H, 0.5);
+            if (Lw->is_ssm) {
+                e2e_mat(&Lw->attn_qkv, NM("blk.%d.attn_qkv.weight"), GGUF_TT_Q5_K, H, QKV, 1.0);
+                e2e_mat(&Lw->attn_gate, NM("blk.%d.attn_gate.weight"), GGUF_TT_Q4_K, H, INNER, 1.0);
+                e2e_vec(&Lw->ssm_a, NM("blk.%d.ssm_a"), 16, 1, -1.25, 0.75);
+                e2e_mat(&Lw->ssm_alpha, NM("blk.%d.ssm_alpha.weight"), GGUF_TT_Q8_0, H, 16, 1.0);
+                e2e_mat(&Lw->ssm_beta, NM("blk.%d.ssm_beta.weight"), GGUF_TT_Q8_0, H, 16, 1.0);
+                e2e_vec(&Lw->ssm_conv1d, NM("blk.%d.ssm_conv1d.weight"), 4, QKV, 0.0, 0.5);
+                e2e_vec(&Lw->ssm_dt_bias, NM("blk.%d.ssm_dt.bias"), 16, 1, 0.0, 0.1);
+                e2e_vec(&Lw->ssm_norm, NM("blk.%d.ssm_norm.weight"), 128, 1, 1.0, 0.02);
+                e2e_mat(&Lw->ssm_out, NM("blk.%d.ssm_out.weight"), GGUF_TT_Q5_K, INNER, H, 0.5);
+            } else {
+                e2e_mat(&Lw->attn_q, NM("blk.%d.attn_q.weight"), GGUF_TT_Q5_K, H, 2 * 8 * 256, 1.0);
+                e2e_mat(&Lw->attn_k, NM("blk.%d.attn_k.weight"), GGUF_TT_Q4_K, H, 2 * 256, 1.0);
+                e2e_mat(&Lw->attn_v, NM("blk.%d.attn_v.weight"), GGUF_TT_Q6_K, H, 2 * 256, 1.0);
+                e2e_vec(&Lw->attn_q_norm, NM("blk.%d.attn_q_norm.weight"), 256, 1, 1.0, 0.02);
+                e2e_vec(&Lw->attn_k_norm, NM("blk.%d.attn_k_norm.weight"), 256, 1, 1.0, 0.02);
+                e2e_mat(&Lw->attn_out, NM("blk.%d.attn_output.weight"), GGUF_TT_Q4_K, 8 * 256, H, 0.5);
+            }
+        }
+#undef NM
+        m->loaded = 1;
+        if (write_path) {
+            uint64_t total = 0;
+            if (gw_write(&gw, write_path, &total) != 0) {
+                fprintf(stderr, "[e2e] writing %s failed\n", write_path);
+                return 1;
+            }
+            fprintf(stderr, "[e2e] wrote %s: %llu bytes, %llu tensors\n", write_path, (unsigned long long)total,
+                    (unsigned long long)gw.n_t);
+            gw_free(&gw);
+            e2e_gw = NULL;
         }
     }
-    m->loaded = 1;
     struct slm_ctx *c = slm_ctx_create(m);
     int32_t *prompt = (int32_t *)oom(calloc((size_t)n_prompt, sizeof(int32_t)));
-    for (int32_t i = 0; i < n_prompt; i++) prompt[i] = e2e_int(0, (int32_t)V - 1);
+    for (int32_t i = 0; i < n_prompt; i++) prompt[i] = e2e_prompt_token((int32_t)V);
     int32_t *toks = (int32_t *)oom(calloc((size_t)n_gen, sizeof(int32_t)));
-    fprintf(stderr, "[e2e] %s: model built in %.2f s (%d layers), prefill %d tokens\n",
+    fprintf(stderr, "[e2e] %s: model %s in %.2f s (%d layers), prefill %d tokens\n",
 #if defined(QK_E2E_GPU)
             "gpu",
 #else
             "cpu",
 #endif
-            e2e_now() - tb, n_layers, n_prompt);
+            load_path ? "loaded" : "built", e2e_now() - tb, n_layers, n_prompt);
 
     /* prefill (slm/slm.c:278-283) */
     double t0 = e2e_now();
@@ -317,7 +428,7 @@ int main(int argc, char **argv) {
         distinct += !seen;
     }
     const double nv = (double)cfg.vocab_size;
-    printf("{\"mode\": \"%s\", \"tier\": \"%s\", \"layers\": %d, \"prompt\": %d, \"gen\": %d, \"seed\": %llu, "
+    printf("{\"mode\": \"%s\", \"source\": \"%s\", \"tier\": \"%s\", \"layers\": %d, \"prompt\": %d, \"gen\": %d, \"seed\": %llu, "
            "\"prefill_s\": %.6f, \"decode_s\": %.6f, \"prefill_tok_s\": %.3f, \"decode_tok_s\": %.3f, "
            "\"distinct_tokens\": %d, \"nonfinite_logits\": %lld, \"last_logits\": {\"min\": %.6g, \"max\": %.6g, "
            "\"mean\": %.6g, \"std\": %.6g}, \"tokens\": [",
@@ -326,7 +437,7 @@ int main(int argc, char **argv) {
 #else
            "cpu",
 #endif
-           simd_dispatch_label(), n_layers, n_prompt, n_gen, (unsigned long long)seed, t1 - t0, t2 - t1,
+           load_path ? "gguf" : "built", simd_dispatch_label(), n_layers, n_prompt, n_gen, (unsigned long long)seed, t1 - t0, t2 - t1,
            n_prompt / (t1 - t0), n_gen / (t2 - t1), distinct, (long long)nonfinite, lmin, lmax, lsum / nv,
            sqrt(lsq / nv - (lsum / nv) * (lsum / nv)));
     for (int32_t i = 0; i < n_gen; i++) printf("%s%d", i ? ", " : "", toks[i]);

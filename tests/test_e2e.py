@@ -53,3 +53,103 @@ def test_e2e_greedy_tokens_identical(prompt, gen):
     assert gpu["tokens"] == cpu["tokens"]
     assert gpu["last_logits"] == cpu["last_logits"]
     assert cpu["distinct_tokens"] >= gen // 4
+
+
+# ---- GGUF round trip ------------------------------------------------------------
+# qwen_e2e --write-gguf writes the random model as GGUF v3 (host/gguf_write.c);
+# --gguf loads a file through the reference's own slm_model_load. The token
+# stream from the loaded file must equal the built model's, and the file
+# must parse under an independent reader of the GGUF v3 layout.
+
+def read_gguf(path):
+    """Minimal GGUF v3 reader for the test: header, key/values, tensor infos."""
+    import struct
+    with open(path, "rb") as f:
+        buf = f.read(1 << 24)                       # header sections only
+        size = os.fstat(f.fileno()).st_size
+    pos = 0
+
+    def take(fmt):
+        nonlocal pos
+        v = struct.unpack_from("<" + fmt, buf, pos)
+        pos += struct.calcsize("<" + fmt)
+        return v[0] if len(v) == 1 else v
+
+    def string():
+        nonlocal pos
+        n = take("Q")
+        s = buf[pos:pos + n].decode()
+        pos += n
+        return s
+
+    def value(t):
+        if t == 4:
+            return take("I")
+        if t == 5:
+            return take("i")
+        if t == 6:
+            return take("f")
+        if t == 8:
+            return string()
+        if t == 9:
+            et, n = take("I"), take("Q")
+            return [value(et) for _ in range(n)]
+        raise AssertionError(f"unexpected value type {t}")
+
+    assert take("I") == 0x46554747 and take("I") == 3
+    n_t, n_kv = take("Q"), take("Q")
+    kv = {}
+    for _ in range(n_kv):
+        k = string()
+        kv[k] = value(take("I"))
+    tensors = {}
+    for _ in range(n_t):
+        name = string()
+        nd = take("I")
+        shape = [take("Q") for _ in range(nd)]
+        tensors[name] = (shape, take("I"), take("Q"))
+    align = kv.get("general.alignment", 32)
+    data_start = (pos + align - 1) // align * align
+    return kv, tensors, data_start, size
+
+
+BLOCK = {0: (1, 4), 8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
+
+
+def test_gguf_roundtrip_cpu(tmp_path):
+    path = str(tmp_path / "e2e.gguf")
+    built = run(E2E_CPU, 120, prompt=12, gen=6, layers=4, seed=5, **{"write-gguf": path})
+    kv, tensors, data_start, size = read_gguf(path)
+    assert kv["general.architecture"] == "qwen35"
+    assert kv["qwen35.block_count"] == 4 and kv["qwen35.embedding_length"] == 1024
+    assert kv["qwen35.rope.dimension_sections"] == [11, 11, 10, 0]
+    assert len(kv["tokenizer.ggml.tokens"]) == 248320
+    # token_embd and output_norm, 14 tensors per DeltaNet layer (layers
+    # 0-2) and 11 per attention layer (layer 3)
+    assert len(tensors) == 2 + 3 * 14 + 11
+    end = 0
+    for name, (shape, ttype, off) in tensors.items():
+        elems, bb = BLOCK[ttype]
+        n = 1
+        for d in shape:
+            n *= d
+        assert n % elems == 0, name
+        assert off % kv["general.alignment"] == 0, name
+        end = max(end, data_start + off + n // elems * bb)
+    assert tensors["token_embd.weight"][:2] == ([1024, 248320], 14)
+    assert tensors["blk.0.ssm_alpha.weight"][:2] == ([1024, 16], 8)
+    assert end == size
+    loaded = run(E2E_CPU, 120, prompt=12, gen=6, layers=4, seed=5, gguf=path)
+    assert loaded["source"] == "gguf" and built["source"] == "built"
+    assert loaded["tokens"] == built["tokens"]
+    assert loaded["last_logits"] == built["last_logits"]
+
+
+@pytest.mark.gpu
+def test_gguf_gpu_tokens_identical(tmp_path):
+    path = str(tmp_path / "e2e.gguf")
+    cpu = run(E2E_CPU, 120, prompt=24, gen=8, layers=4, seed=6, **{"write-gguf": path})
+    gpu = run(E2E_GPU, 120, prompt=24, gen=8, layers=4, seed=6, gguf=path)
+    assert gpu["source"] == "gguf"
+    assert gpu["tokens"] == cpu["tokens"]
+    assert gpu["last_logits"] == cpu["last_logits"]
