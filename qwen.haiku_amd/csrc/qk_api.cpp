@@ -44,6 +44,9 @@ struct State {
     void *dxq = nullptr;  size_t dxq_cap = 0;
     void *dy = nullptr;   size_t dy_cap = 0;
     void *dsel = nullptr; size_t dsel_cap = 0;
+    // pinned host staging of the host seam: x goes in, y comes out
+    void *hx = nullptr;   size_t hx_cap = 0;
+    void *hy = nullptr;   size_t hy_cap = 0;
     int cu_count = 256;
 };
 
@@ -138,6 +141,18 @@ int check_mat(int type, const void *w, int64_t n, int64_t k, const void *xq, con
     return QK_OK;
 }
 
+// Pinned host buffer of at least `need` bytes (contents not kept).
+int grow_host(void **p, size_t *cap, size_t need) {
+    if (*cap >= need) return QK_OK;
+    if (*p) (void)hipHostFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    const size_t n = need < 65536 ? 65536 : need + need / 4;
+    HIP_OK(hipHostMalloc(p, n, hipHostMallocDefault), "hipHostMalloc");
+    *cap = n;
+    return QK_OK;
+}
+
 int grow(void **p, size_t *cap, size_t need) {
     if (*cap >= need) return QK_OK;
     if (*p) (void)hipFree(*p);
@@ -217,6 +232,12 @@ void hip_qk_shutdown(void) {
         *b = nullptr;
     }
     s.dx_cap = s.dxq_cap = s.dy_cap = s.dsel_cap = 0;
+    void **hbufs[] = {&s.hx, &s.hy};
+    for (void **b : hbufs) {
+        if (*b) (void)hipHostFree(*b);
+        *b = nullptr;
+    }
+    s.hx_cap = s.hy_cap = 0;
     (void)hipStreamDestroy(s.stream);
     s.stream = nullptr;
     s.init = false;
@@ -421,10 +442,19 @@ int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f, int64_t k, c
     const size_t qb = (size_t)(n_tok * act_bytes(type, k));
     const size_t yb = (size_t)(n_tok * out_f) * sizeof(float);
     if ((rc = grow(&s.dx, &s.dx_cap, xb)) || (rc = grow(&s.dxq, &s.dxq_cap, qb)) ||
-        (rc = grow(&s.dy, &s.dy_cap, yb)))
+        (rc = grow(&s.dy, &s.dy_cap, yb)) || (rc = grow_host(&s.hx, &s.hx_cap, xb)) ||
+        (rc = grow_host(&s.hy, &s.hy_cap, yb)))
         return rc;
-    HIP_OK(hipMemcpyAsync(s.dx, x, xb, hipMemcpyHostToDevice, s.stream), "hipMemcpyAsync(x)");
-    const float *dx = static_cast<const float *>(s.dx);
+    // x through pinned memory: a decode row (<= 16 KB) is read by the
+    // quantizer straight from host memory; a prefill chunk goes by DMA.
+    std::memcpy(s.hx, x, xb);
+    void *hx_dev = nullptr;
+    HIP_OK(hipHostGetDevicePointer(&hx_dev, s.hx, 0), "hipHostGetDevicePointer");
+    const float *dx = static_cast<const float *>(hx_dev);
+    if (xb > 16384) {
+        HIP_OK(hipMemcpyAsync(s.dx, s.hx, xb, hipMemcpyHostToDevice, s.stream), "hipMemcpyAsync(x)");
+        dx = static_cast<const float *>(s.dx);
+    }
     uint8_t *dxq = static_cast<uint8_t *>(s.dxq);
     float *dy = static_cast<float *>(s.dy);
     if (type == QK_TYPE_Q8_0) {
@@ -465,8 +495,9 @@ int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f, int64_t k, c
                    "gemm launch");
         }
     }
-    HIP_OK(hipMemcpyAsync(out, dy, yb, hipMemcpyDeviceToHost, s.stream), "hipMemcpyAsync(out)");
+    HIP_OK(hipMemcpyAsync(s.hy, dy, yb, hipMemcpyDeviceToHost, s.stream), "hipMemcpyAsync(out)");
     HIP_OK(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+    std::memcpy(out, s.hy, yb);
     return QK_OK;
 }
 
