@@ -886,7 +886,7 @@ __global__ __launch_bounds__(256, 5) void k_gemv(uint32_t t0, uint32_t t1, uint3
             v = o > v ? o : v;
         }
         if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = v;
-        __syncthreads();
+        lds_barrier();                                 // the logit stores need not complete first
         if (threadIdx.x == 0) {
             uint64_t m = wbest[0];
             for (int i = 1; i < 4; i++) m = wbest[i] > m ? wbest[i] : m;
@@ -988,24 +988,59 @@ hipError_t launch_gemv(GemvArgs &a, int max_grid, hipStream_t s) {
 // The GEMV leaves one key per workgroup: the maximum (value, -row) key of
 // the rows it wrote. argmax = max over those keys.
 //
-// Top-k (keys compare by value, then lower row): the k-th largest of the
-// workgroup maxima is a lower bound T on the k-th largest logit (the k
-// largest maxima are k distinct logits >= T), so every top-k logit has a
-// value key >= T. k_topk_filter finds T (radix select over the maxima)
-// and collects the logits >= T; k_topk_final ranks those candidates (by
-// counting when they fit one block, else after a radix select of the k
-// best). If more than TOPK_CAND logits pass the filter (a pathological
-// flat distribution), k_topk_final falls back to k exact passes over all
-// logits.
+// Top-k (keys compare by value, then lower row). The smallest of any k
+// distinct logits is a lower bound on the k-th largest logit. The
+// workgroup maxima are distinct logits, and so are the maxima of disjoint
+// groups of G workgroups. k_topk_filter takes as its bound T the k-th
+// largest group maximum, searched on the top 16 bits of the value key
+// (low bits zero, so T stays a lower bound), and collects every logit
+// whose value key is >= T: all of the top k are among them. k_topk_final
+// ranks the candidates. If more than TOPK_CAND logits pass (a
+// pathological flat distribution), k_topk_final falls back to k exact
+// passes over all logits.
 #define TOPK_CAND 4096
-#define LMHEAD_MAX_WG 4096                             // argmax partials (one per workgroup)
 #define LMHEAD_WG 1024                                 // workgroups of the LM-head GEMV (grid-stride
-                                                       // over tiles): fewer maxima for the top-k bound
+                                                       // over tiles), one maximum each
 
 __device__ __forceinline__ uint32_t valkey(float v) {
     uint32_t b = __float_as_uint(v);
     if (v == 0.0f) b = 0;
     return (v != v) ? 0u : ((b & 0x80000000u) ? ~b : (b | 0x80000000u));
+}
+
+__device__ __forceinline__ uint32_t dpp_mirror(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, true);   // row_mirror
+}
+
+// Largest T with zero low 16 bits such that at least k of the wave's keys
+// are >= T (R keys per lane, read from keys[R * lane ...]): a bit-by-bit
+// search from the top, one ballot per key and bit. T is wave-uniform.
+template <int R>
+__device__ uint32_t wave_bound(const uint32_t *keys, int k) {
+    const int lane = threadIdx.x & 63;
+    uint32_t x[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) x[r] = keys[R * lane + r];
+    uint32_t T = 0;
+#pragma unroll
+    for (int b = 31; b >= 16; b--) {
+        const uint32_t c = T | (1u << b);
+        int cnt = 0;
+#pragma unroll
+        for (int r = 0; r < R; r++) cnt += __popcll(__ballot(x[r] >= c));
+        T = cnt >= k ? c : T;
+    }
+    return T;
+}
+
+// Sum of v over aligned groups of P lanes (P = 1, 2, 4, 8, 16), left in
+// every lane of the group. All lanes must be active.
+__device__ __forceinline__ int group_sum(int v, int P) {
+    if (P >= 2) v += dpp_xor1(v);
+    if (P >= 4) v += dpp_xor2(v);
+    if (P >= 8) v += dpp_hmirror(v);
+    if (P >= 16) v += (int)dpp_mirror((uint32_t)v);
+    return v;
 }
 
 // Exact k-th largest of the keys held by a 1024-thread block (R keys per
@@ -1021,8 +1056,25 @@ __device__ K block_kth_largest(const K (&key)[R], const bool (&have)[R], int k, 
         if (threadIdx.x < 256) hist[threadIdx.x] = 0;
         __syncthreads();
 #pragma unroll
-        for (int r = 0; r < R; r++)
-            if (have[r] && (key[r] & mask) == prefix) atomicAdd(&hist[(uint32_t)(key[r] >> shift) & 255u], 1u);
+        for (int r = 0; r < R; r++) {
+            // Lanes holding the same digit add together, one LDS atomic
+            // per distinct digit of the wave: keys of similar logits share
+            // their top digits, and same-address atomics serialize lane by
+            // lane. After 4 rounds the rest add one by one.
+            bool act = have[r] && (key[r] & mask) == prefix;
+            const uint32_t dig = (uint32_t)(key[r] >> shift) & 255u;
+            for (int it = 0; it < 4; it++) {
+                const uint64_t pend = __ballot(act);
+                if (pend == 0) break;
+                const int leader = __builtin_ctzll(pend);
+                const uint32_t d0 = (uint32_t)__builtin_amdgcn_readlane((int)dig, leader);
+                const bool same = act && dig == d0;
+                const uint64_t m = __ballot(same);
+                if (lane == leader) atomicAdd(&hist[d0], (uint32_t)__builtin_popcountll(m));
+                act = act && !same;
+            }
+            if (act) atomicAdd(&hist[dig], 1u);
+        }
         __syncthreads();
         if (threadIdx.x < 64) {
             // lane l owns digits 255-4l .. 252-4l (descending); suffix scan
@@ -1053,34 +1105,74 @@ __device__ K block_kth_largest(const K (&key)[R], const bool (&have)[R], int k, 
     return prefix;
 }
 
-// Grid: ceil(n / 4096) blocks of 1024. Every block finds the same T from
-// the nparts (<= LMHEAD_MAX_WG) workgroup maxima, then filters its 4096
-// logits.
+// Grid: ceil(n / 4096) blocks of 1024 when topk > 0, else one block.
+// Block 0 writes the argmax. With topk > 0 every block finds the same
+// bound T from the nparts (<= LMHEAD_WG) workgroup maxima, then collects
+// its 4096 logits that reach it.
 __global__ __launch_bounds__(1024) void k_topk_filter(const float *__restrict__ logits, int64_t n,
                                                       const uint64_t *__restrict__ partial, int nparts,
                                                       int topk, uint64_t *__restrict__ cand,
-                                                      uint32_t *__restrict__ ctr) {
-    __shared__ uint32_t hist[258];
-    uint32_t key[4];
-    bool have[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int i = threadIdx.x + 1024 * r;
-        have[r] = i < nparts;
-        key[r] = have[r] ? (uint32_t)(partial[i] >> 32) : 0u;
-    }
+                                                      uint32_t *__restrict__ ctr, int32_t *__restrict__ argmax) {
+    __shared__ uint32_t gkey[1024];                    // group maxima (value keys)
+    __shared__ uint64_t red[16];
+    __shared__ uint32_t tsh;
+    const int t = threadIdx.x, lane = t & 63;
+    const uint64_t pk = t < nparts ? partial[t] : 0;
     const int64_t base = (int64_t)blockIdx.x * 4096;
     float v[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        const int64_t i = base + threadIdx.x + 1024 * r;
-        v[r] = i < n ? logits[i] : 0.0f;
+        const int64_t i = base + t + 1024 * r;
+        v[r] = (topk > 0 && i < n) ? logits[i] : 0.0f;
     }
-    // Fewer maxima than k (a tiny vocabulary): no bound, every logit passes.
-    const uint32_t T = (nparts >= topk) ? block_kth_largest<4, 32, uint32_t>(key, have, topk, hist) : 0u;
+    float l0 = 0.0f;
+    if (blockIdx.x == 0 && t == 64) l0 = logits[0];
+    // Group size: the largest of 16, 4, 1 that leaves at least k groups;
+    // G = 0: fewer maxima than k (a tiny vocabulary), every logit passes.
+    const int G = (nparts + 15) / 16 >= topk ? 16 : (nparts + 3) / 4 >= topk ? 4 : nparts >= topk ? 1 : 0;
+    if (topk > 0 && G > 0) {
+        uint32_t m = (uint32_t)(pk >> 32);
+        if (G >= 4) {
+            m = max(m, (uint32_t)dpp_xor1((int)m));
+            m = max(m, (uint32_t)dpp_xor2((int)m));
+        }
+        if (G >= 16) {
+            m = max(m, (uint32_t)dpp_hmirror((int)m));
+            m = max(m, dpp_mirror(m));
+        }
+        if ((lane & (G - 1)) == 0) gkey[t / G] = m;
+    }
+    if (blockIdx.x == 0) {
+        uint64_t m = pk;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const uint32_t lo = __shfl_xor((uint32_t)m, off), hi = __shfl_xor((uint32_t)(m >> 32), off);
+            const uint64_t o = ((uint64_t)hi << 32) | lo;
+            m = o > m ? o : m;
+        }
+        if (lane == 0) red[t >> 6] = m;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0 && t == 64) {                  // wave 1; wave 0 searches T
+        uint64_t b = red[0];
+        for (int i = 1; i < 16; i++) b = red[i] > b ? red[i] : b;
+        int32_t best = (int32_t)(0xffffffffu - (uint32_t)(b & 0xffffffffu));
+        if (l0 != l0) best = 0;                        // sample_argmax: v[0] = NaN never loses
+        *argmax = best;
+    }
+    if (topk <= 0) return;                             // uniform
+    if (t < 64) {
+        uint32_t T = 0;
+        if (G == 16) T = wave_bound<1>(gkey, topk);
+        else if (G == 4) T = wave_bound<4>(gkey, topk);
+        else if (G == 1) T = wave_bound<16>(gkey, topk);
+        if (t == 0) tsh = T;
+    }
+    __syncthreads();
+    const uint32_t T = tsh;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        const int64_t i = base + threadIdx.x + 1024 * r;
+        const int64_t i = base + t + 1024 * r;
         if (i < n && valkey(v[r]) >= T) {
             const uint32_t slot = atomicAdd(ctr, 1u);
             if (slot < TOPK_CAND) cand[slot] = ((uint64_t)valkey(v[r]) << 32) | (0xffffffffu - (uint32_t)i);
@@ -1088,54 +1180,34 @@ __global__ __launch_bounds__(1024) void k_topk_filter(const float *__restrict__ 
     }
 }
 
-// One block of 1024: argmax from the per-workgroup maxima; the exact top-k
-// of the filtered candidates, ranked value-descending / row-ascending.
+// One block of 1024: the exact top-k of the filtered candidates, ranked
+// value-descending / row-ascending.
 __global__ __launch_bounds__(1024) void k_topk_final(const float *__restrict__ logits, int64_t n,
-                                                     const uint64_t *__restrict__ partial, int nparts,
                                                      const uint64_t *__restrict__ cand,
                                                      const uint32_t *__restrict__ ctr, int topk,
-                                                     int32_t *__restrict__ argmax,
                                                      int32_t *__restrict__ topk_idx,
                                                      float *__restrict__ topk_val) {
     __shared__ uint32_t hist[258];
     __shared__ uint64_t win[1024];                     // candidates (ranking) or winners
     __shared__ uint64_t red[16];
     __shared__ uint32_t nwin;
-    // argmax: max of the partial keys
-    uint64_t m = 0;
-    for (int i = threadIdx.x; i < nparts; i += 1024) m = partial[i] > m ? partial[i] : m;
-    const uint32_t c = topk > 0 ? *ctr : 0u;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t lo = __shfl_xor((uint32_t)m, off), hi = __shfl_xor((uint32_t)(m >> 32), off);
-        const uint64_t o = ((uint64_t)hi << 32) | lo;
-        m = o > m ? o : m;
-    }
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-    if (threadIdx.x == 0) nwin = 0;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint64_t b = red[0];
-        for (int i = 1; i < 16; i++) b = red[i] > b ? red[i] : b;
-        int32_t best = (int32_t)(0xffffffffu - (uint32_t)(b & 0xffffffffu));
-        const float l0 = logits[0];
-        if (l0 != l0) best = 0;                        // sample_argmax: v[0] = NaN never loses
-        *argmax = best;
-    }
-    if (topk <= 0) return;                             // uniform
+    const int t = threadIdx.x;
+    const uint32_t c = *ctr;
+    const uint64_t mine = cand[t];                     // t < 1024 <= TOPK_CAND; used when t < c
+    if (t == 0) nwin = 0;
     int nw;                                            // keys in win[] to rank
     if (c <= 1024) {
         // Few candidates: rank every one of them directly.
-        if (threadIdx.x < c) win[threadIdx.x] = cand[threadIdx.x];
+        if (t < (int)c) win[t] = mine;
         nw = (int)c;
     } else if (c <= TOPK_CAND) {
         uint64_t key[4];
         bool have[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const uint32_t i = threadIdx.x + 1024 * r;
+            const uint32_t i = t + 1024 * r;
             have[r] = i < c;
-            key[r] = have[r] ? cand[i] : 0;
+            key[r] = r == 0 ? mine : have[r] ? cand[i] : 0;
         }
         const uint64_t T = block_kth_largest<4, 64, uint64_t>(key, have, topk, hist);
 #pragma unroll
@@ -1148,7 +1220,7 @@ __global__ __launch_bounds__(1024) void k_topk_final(const float *__restrict__ l
         uint64_t prev = ~(uint64_t)0;
         for (int r = 0; r < topk; r++) {
             uint64_t b = 0;
-            for (int64_t i = threadIdx.x; i < n; i += 1024) {
+            for (int64_t i = t; i < n; i += 1024) {
                 const uint64_t kk = ((uint64_t)valkey(logits[i]) << 32) | (0xffffffffu - (uint32_t)i);
                 if (kk < prev && kk > b) b = kk;
             }
@@ -1159,34 +1231,41 @@ __global__ __launch_bounds__(1024) void k_topk_final(const float *__restrict__ l
                 b = o > b ? o : b;
             }
             __syncthreads();
-            if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = b;
+            if ((t & 63) == 0) red[t >> 6] = b;
             __syncthreads();
             uint64_t bb = red[0];
             for (int i = 1; i < 16; i++) bb = red[i] > bb ? red[i] : bb;
-            if (threadIdx.x == 0) win[r] = bb;
+            if (t == 0) win[r] = bb;
             prev = bb;
         }
         nw = topk;
     }
     __syncthreads();
-    // Rank the keys (all distinct) and write the topk best in order.
-    if ((int)threadIdx.x < nw) {
-        const uint64_t me = win[threadIdx.x];
-        int rank = 0;
-        for (int i = 0; i < nw; i++) rank += win[i] > me;
-        if (rank < topk) {
-            const int32_t idx = (int32_t)(0xffffffffu - (uint32_t)(me & 0xffffffffu));
-            topk_idx[rank] = idx;
-            topk_val[rank] = logits[idx];
-        }
+    // Rank the keys (all distinct): P lanes per key, lane j of a group
+    // counts the keys j, j + P, ... above its key; the group's lane 0
+    // writes the key at its rank when that is below k.
+    const int P = nw <= 64 ? 16 : nw <= 128 ? 8 : nw <= 256 ? 4 : nw <= 512 ? 2 : 1;
+    const int i = t / P, j = t % P;
+    const bool live = i < nw;
+    const uint64_t me = live ? win[i] : 0;
+    const int32_t idx = (int32_t)(0xffffffffu - (uint32_t)(me & 0xffffffffu));
+    float val = 0.0f;
+    if (live && j == 0) val = logits[idx];             // in flight during the count
+    int cnt = 0;
+    if (live)
+        for (int q = j; q < nw; q += P) cnt += win[q] > me;
+    cnt = group_sum(cnt, P);
+    if (live && j == 0 && cnt < topk) {
+        topk_idx[cnt] = idx;
+        topk_val[cnt] = val;
     }
 }
 
 static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 size_t lmhead_cand_bytes(int64_t, int) {
-    // argmax partials (<= 4096 workgroups) | candidate keys | counter
-    return (size_t)(LMHEAD_MAX_WG + TOPK_CAND) * sizeof(uint64_t) + 64;
+    // argmax partials (<= LMHEAD_WG workgroups) | candidate keys | counter
+    return (size_t)(LMHEAD_WG + TOPK_CAND) * sizeof(uint64_t) + 64;
 }
 
 hipError_t launch_lmhead(const uint8_t *w, int64_t n, int64_t k, const uint8_t *xq, int topk,
@@ -1203,19 +1282,20 @@ hipError_t launch_lmhead(const uint8_t *w, int64_t n, int64_t k, const uint8_t *
     a.d[0].y = logits;
     gemv_plan(a.d[0]);
     uint64_t *partial = reinterpret_cast<uint64_t *>(scratch);
-    uint64_t *cand = partial + LMHEAD_MAX_WG;
+    uint64_t *cand = partial + LMHEAD_WG;
     uint32_t *ctr = reinterpret_cast<uint32_t *>(cand + TOPK_CAND);
     int grid = 0;
     hipError_t e = launch_gemv_impl(a, LMHEAD_WG, partial, ctr, &grid, s);
     if (e != hipSuccess) return e;
-    if (grid > LMHEAD_MAX_WG) return hipErrorInvalidValue;
+    if (grid > LMHEAD_WG) return hipErrorInvalidValue;
+    const unsigned fgrid = topk > 0 ? (unsigned)cdiv(n, 4096) : 1u;
+    hipLaunchKernelGGL(k_topk_filter, dim3(fgrid), dim3(1024), 0, s, logits, n, partial, grid, topk, cand, ctr,
+                       argmax);
     if (topk > 0) {
-        hipLaunchKernelGGL(k_topk_filter, dim3((unsigned)cdiv(n, 4096)), dim3(1024), 0, s, logits, n, partial,
-                           grid, topk, cand, ctr);
         if ((e = hipGetLastError()) != hipSuccess) return e;
+        hipLaunchKernelGGL(k_topk_final, dim3(1), dim3(1024), 0, s, logits, n, cand, ctr, topk, topk_idx,
+                           topk_val);
     }
-    hipLaunchKernelGGL(k_topk_final, dim3(1), dim3(1024), 0, s, logits, n, partial, grid, cand, ctr, topk,
-                       argmax, topk_idx, topk_val);
     return hipGetLastError();
 }
 

@@ -162,7 +162,11 @@ def test_matmul_gemm_m2048(lib, orc):
 
 # ---- LM head ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("n,k,topk", [(248320, 1024, 40), (31040, 1024, 40), (5000, 512, 256), (77, 256, 1), (300, 256, 200), (9000, 256, 64)])
+# Group sizes of the top-k bound (maxima of 1, 4 or 16 GEMV workgroups):
+# k <= 64 of 1024 maxima uses 16, (248320, 256) and (31040, 100) use 4,
+# (5000, 256) uses 1, (300, 200) has fewer maxima than k (no bound).
+@pytest.mark.parametrize("n,k,topk", [(248320, 1024, 40), (31040, 1024, 40), (5000, 512, 256), (77, 256, 1),
+                                      (300, 256, 200), (9000, 256, 64), (248320, 1024, 256), (31040, 1024, 100)])
 def test_lmhead_argmax_topk(lib, orc, n, k, topk):
     step(f"lmhead n={n} k={k} topk={topk}")
     w = synth.blocks(14, n, k, seed=2)
@@ -251,6 +255,38 @@ def test_rejects_bad_shapes(lib):
     assert "k=" in lib.last_error() or "m=" in lib.last_error()
     with pytest.raises(ValueError):                                   # binding's size guard
         lib.matvec(12, w, 8, 256, xq, y)
+
+
+def _valkey(v):
+    """Order-preserving uint32 key of a float32 (value order; NaN lowest)."""
+    b = np.asarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    b = np.where(np.asarray(v) == 0, 0, b)
+    key = np.where(b & 0x80000000, ~b & 0xffffffff, b | 0x80000000)
+    return np.where(np.isnan(v), 0, key).astype(np.uint64)
+
+
+def test_lmhead_topk_many_ties_ranked(lib, orc):
+    # 20 distinct rows repeated 1100 times: the maximum ties at 1100 rows,
+    # so more candidates pass the filter than one block ranks directly
+    # (1024) but fewer than the candidate buffer holds (4096); the k-th
+    # largest of them is selected first, then ranked. Ties go to low rows.
+    step("lmhead top-k selected candidates")
+    period, reps, k, topk = 20, 1100, 256, 10
+    w = np.tile(synth.blocks(14, period, k, seed=8), (reps, 1))
+    n = period * reps
+    xq = orc.quantize_q8k(synth.activations(1, k, seed=8))
+    want = orc.matmul_xq(14, w, n, k, xq, 1, oracle.TIER_EPI[lib.tier()])[0]
+    top = orc.argmax(want)
+    # every logit whose key shares the maximum's top 16 bits passes
+    passing = int((_valkey(want) >= (int(_valkey(want[top])) & 0xffff0000)).sum())
+    assert 1024 < passing <= 4096, passing
+    logits, am, ti, tv = lib.lmhead(dev(w), n, k, dev(xq[0]), topk=topk)
+    assert_bits_equal(host(logits), want, "logits")
+    assert int(host(am)[0]) == top
+    np.testing.assert_array_equal(host(ti), top + period * np.arange(topk))
+    assert_bits_equal(host(tv), want[host(ti)], "topk values")
+    ri, _ = orc.topk_collect(want, topk)
+    assert set(ri.tolist()) == set((top + period * np.arange(topk)).tolist())
 
 
 def test_lmhead_topk_flat_logits_fallback(lib, orc):
