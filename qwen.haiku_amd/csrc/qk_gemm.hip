@@ -14,18 +14,21 @@
 //    fp32 sum in super-block order, exactly like the reference's
 //    sequential `sum += term`.
 //
-// Work decomposition: a 256-thread workgroup owns a 64-token x 64-row
+// Work decomposition: a 512-thread workgroup owns a 64-token x 64-row
 // output tile and walks the super-blocks of K in order. For each one it
-// stages the 64 activation rows (int8 Q8_K quants, scale, bsum pairs)
-// and the 64 weight rows, dequantised to int8 with their sub-block
-// scales, into LDS (the next super-block's raw bytes are loaded into
-// registers meanwhile); each of the 4 waves then computes a 32x32
-// sub-tile:
+// stages the 64 activation rows (int8 Q8_K quants, scale, bsum pairs;
+// threads 0-255) and the 64 weight rows, dequantised to int8 with their
+// sub-block scales (threads 256-511), into LDS; the next super-block's
+// raw bytes are loaded into registers meanwhile. Each of the 8 waves then
+// computes one 32x32 sub-tile over one half of the super-block's k range
+// (integer sums: exact in any order); the two waves of a sub-tile swap
+// halves of their int32 results through LDS and each finishes 8 of the
+// 16 outputs per lane:
 //
 //  * Q4_K / Q5_K: the 6-bit sub-block scales are split into two 3-bit
 //    digits and baked into int8 weight planes (plus a 5th-bit plane for
 //    Q5_K), so one chain of v_mfma_i32_32x32x32_i8 per plane accumulates
-//    the whole super-block and isum = acc0 + 8*acc1 (+ 16*acc2); mins
+//    the wave's half super-block and isum = acc0 + 8*acc1 (+ 16*acc2); mins
 //    from the Q8_K bsums (simd/quants.h:283-304, 324-349);
 //  * Q6_K: one v_mfma_i32_32x32x16_i8 per 16-element sub-block, weights
 //    staged as u6 - 32 in [-32, 31] so the reference's
@@ -37,6 +40,8 @@
 // activation whatever that order is.
 #include "qk_dev.h"
 #include "qk_kernels.h"
+
+#include <type_traits>
 
 namespace qk {
 
@@ -342,117 +347,149 @@ template <> struct WRawOf<14> { typedef WRaw14 T; };
 __device__ __forceinline__ int tok_of(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
 
 template <int TYPE, bool FUSED>
-__global__ __launch_bounds__(256) void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb,
-                                              const uint8_t *__restrict__ xq, int64_t m, float *__restrict__ y) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb,
+                                                 const uint8_t *__restrict__ xq, int64_t m, float *__restrict__ y) {
     constexpr int BB = TYPE == 12 ? Q4K_BYTES : (TYPE == 13 ? Q5K_BYTES : Q6K_BYTES);
+    constexpr bool ALIAS = TYPE == 13;                       // Q5_K: exchange through the activation tile
     __shared__ GemmLds<Planes<TYPE>::n> s;
+    __shared__ int32_t xch_mem[ALIAS ? 1 : 4 * 2 * 8 * 64];
+    int32_t *xch = ALIAS ? reinterpret_cast<int32_t *>(&s.a[0][0]) : xch_mem;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 31, h = lane >> 5;
-    const int tm = 32 * (wave >> 1), tn = 32 * (wave & 1);   // wave sub-tile in the workgroup tile
+    const int sub = wave & 3, g = wave >> 2;                 // 32x32 sub-tile, half of the super-block's k
+    const int tm = 32 * (sub >> 1), tn = 32 * (sub & 1);
     const int64_t r0 = (int64_t)blockIdx.x * GM_BN, t0 = (int64_t)blockIdx.y * GM_BM;
-    // staging roles: token / weight row st of the tile, quarter sq
-    const int st = threadIdx.x >> 2, sq = threadIdx.x & 3;
-    const uint8_t *xrow = (t0 + st < m) ? xq + (t0 + st) * nb * Q8K_BYTES + 4 * sq : nullptr;
-    const uint8_t *wrow = (r0 + st < n) ? w + (r0 + st) * nb * BB : nullptr;
+    // staging roles: threads 0..255 stage activation rows, 256..511 weight
+    // rows; row st of the tile, quarter sq
+    const bool stage_w = threadIdx.x >= 256;
+    const int st = (threadIdx.x & 255) >> 2, sq = threadIdx.x & 3;
+    const uint8_t *xrow = (!stage_w && t0 + st < m) ? xq + (t0 + st) * nb * Q8K_BYTES + 4 * sq : nullptr;
+    const uint8_t *wrow = (stage_w && r0 + st < n) ? w + (r0 + st) * nb * BB : nullptr;
 
-    float sum[16];
-#pragma unroll
-    for (int v = 0; v < 16; v++) sum[v] = 0.0f;
-    ActRaw ar;
-    typename WRawOf<TYPE>::T wr;
-    load_act(ar, xrow, sq, 0);
-    load_w(wr, wrow, sq, 0);
     const int8_t *arow = &s.a[tm + col][0];
     const v16i zero = {0};
+    // The loop runs in one of two copies, one per staging role, so that a
+    // thread holds registers for its own raw bytes only.
+    auto body = [&](auto &raw, auto role) {
+        constexpr bool SW = decltype(role)::value;
+        float sum[8];
+#pragma unroll
+        for (int v = 0; v < 8; v++) sum[v] = 0.0f;
+        if constexpr (SW) load_w(raw, wrow, sq, 0);
+        else load_act(raw, xrow, sq, 0);
 
-    for (int i = 0; i < nb; i++) {
-        lds_barrier();                                       // previous super-block's reads done
-        store_act(s, ar, st, sq);
-        store_w(s, wr, st, sq);
-        if (i + 1 < nb) {                                    // next super-block in flight during compute
-            load_act(ar, xrow, sq, i + 1);
-            load_w(wr, wrow, sq, i + 1);
-        }
-        lds_barrier();
-
-        int32_t isum[16];
-        if (TYPE == 14) {
-            // per 16-element sub-block: MFMA, then times its int8 scale
-            const int8_t *brow = &s.b[0][tn + col][0];
-#pragma unroll
-            for (int v = 0; v < 16; v++) isum[v] = 0;
-            const uint4 scp = *(const QK_LDS uint4 *)&s.sc[tn + col][0];
-            const uint32_t scw[4] = {scp.x, scp.y, scp.z, scp.w};
-#pragma unroll
-            for (int sb = 0; sb < 16; sb++) {
-                const long av = *(const QK_LDS long *)(arow + 16 * sb + 8 * h);
-                const long bv = *(const QK_LDS long *)(brow + 16 * sb + 8 * h);
-                const v16i d = __builtin_amdgcn_mfma_i32_32x32x16_i8(av, bv, zero, 0, 0, 0);
-                const int32_t scv = (int32_t)(int8_t)(scw[sb >> 2] >> (8 * (sb & 3)));
-#pragma unroll
-                for (int v = 0; v < 16; v++) isum[v] += __mul24(scv, d[v]);
+        for (int i = 0; i < nb; i++) {
+            lds_barrier();                                       // previous super-block's reads done
+            if constexpr (SW) store_w(s, raw, st, sq);
+            else store_act(s, raw, st, sq);
+            if (i + 1 < nb) {                                    // next super-block in flight during compute
+                if constexpr (SW) load_w(raw, wrow, sq, i + 1);
+                else load_act(raw, xrow, sq, i + 1);
             }
-        } else {
-            // one accumulation chain per digit plane over the whole super-block
-            constexpr int NP = Planes<TYPE>::n;
-            v16i acc[NP];
+            lds_barrier();
+
+            // this wave's half of the super-block's k range
+            int32_t isum[16];
+            if constexpr (TYPE == 14) {
+                // per 16-element sub-block: MFMA, then times its int8 scale
+                const int8_t *brow = &s.b[0][tn + col][0];
 #pragma unroll
-            for (int pl = 0; pl < NP; pl++) acc[pl] = zero;
+                for (int v = 0; v < 16; v++) isum[v] = 0;
+                const uint2 scp = *(const QK_LDS uint2 *)&s.sc[tn + col][8 * g];
+                const uint32_t scw[2] = {scp.x, scp.y};
 #pragma unroll
-            for (int c = 0; c < 8; c++) {
-                const v4i av = *(const QK_LDS v4i *)(arow + 32 * c + 16 * h);
+                for (int j = 0; j < 8; j++) {
+                    const int sb = 8 * g + j;
+                    const long av = *(const QK_LDS long *)(arow + 16 * sb + 8 * h);
+                    const long bv = *(const QK_LDS long *)(brow + 16 * sb + 8 * h);
+                    const v16i d = __builtin_amdgcn_mfma_i32_32x32x16_i8(av, bv, zero, 0, 0, 0);
+                    const int32_t scv = (int32_t)(int8_t)(scw[j >> 2] >> (8 * (j & 3)));
 #pragma unroll
-                for (int pl = 0; pl < NP; pl++) {
-                    const v4i bv = *(const QK_LDS v4i *)(&s.b[pl][tn + col][32 * c + 16 * h]);
-                    acc[pl] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, acc[pl], 0, 0, 0);
+                    for (int v = 0; v < 16; v++) isum[v] += __mul24(scv, d[v]);
+                }
+            } else {
+                // one accumulation chain per digit plane over the half
+                constexpr int NP = Planes<TYPE>::n;
+                v16i acc[NP];
+#pragma unroll
+                for (int pl = 0; pl < NP; pl++) acc[pl] = zero;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int c = 4 * g + j;
+                    const v4i av = *(const QK_LDS v4i *)(arow + 32 * c + 16 * h);
+#pragma unroll
+                    for (int pl = 0; pl < NP; pl++) {
+                        const v4i bv = *(const QK_LDS v4i *)(&s.b[pl][tn + col][32 * c + 16 * h]);
+                        acc[pl] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, acc[pl], 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    int32_t t = acc[0][v] + 8 * acc[1][v];
+                    if constexpr (NP == 3) t += 16 * acc[2][v];
+                    isum[v] = t;
                 }
             }
+            // The two waves of a sub-tile swap halves: this wave finishes
+            // outputs v = 8g .. 8g+7 and hands the other eight to its partner.
+            // Integer sums: exact in any order.
+            if (ALIAS) lds_barrier();                            // every wave is done reading s.a
+            int32_t *xo = xch + ((sub * 2 + (1 - g)) * 8) * 64 + lane;
+            const int32_t *xi = xch + ((sub * 2 + g) * 8) * 64 + lane;
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                int32_t t = acc[0][v] + 8 * acc[1][v];
-                if constexpr (NP == 3) t += 16 * acc[2][v];
-                isum[v] = t;
+            for (int v = 0; v < 8; v++) xo[64 * v] = g ? isum[v] : isum[8 + v];
+            lds_barrier();
+            int32_t mine[8];
+#pragma unroll
+            for (int v = 0; v < 8; v++) mine[v] = (g ? isum[8 + v] : isum[v]) + xi[64 * v];
+
+            const float wd = s.wd[tn + col];
+            if constexpr (TYPE == 14) {
+#pragma unroll
+                for (int v = 0; v < 8; v++) {
+                    const float yd = s.yd[tm + tok_of(8 * g + v, h)];
+                    sum[v] = __fadd_rn(sum[v], __fmul_rn(__fmul_rn(wd, yd), (float)mine[v]));
+                }
+            } else {
+                // isum_mins = sum_j m_j * (bsums[2j] + bsums[2j+1]) as two small
+                // MFMAs: the bsum pairs enter as int8 digits (lo | hi), the mins
+                // sit against the lo half for one product and the hi half for
+                // the other, so mins = lo_product + 128 * hi_product exactly.
+                const long amv = *(const QK_LDS long *)&s.am[tm + col][8 * h];
+                const long mnv = *(const QK_LDS long *)&s.mn[tn + col][0];
+                const v16i dl = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 0 ? mnv : 0L, zero, 0, 0, 0);
+                const v16i dh = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 1 ? mnv : 0L, zero, 0, 0, 0);
+                const float wdm = s.wdm[tn + col];
+#pragma unroll
+                for (int v = 0; v < 8; v++) {
+                    const int vv = 8 * g + v;
+                    const int32_t mins = (g ? dl[8 + v] : dl[v]) + (g ? dh[8 + v] : dh[v]) * 128;
+                    const float yd = s.yd[tm + tok_of(vv, h)];
+                    const float d = __fmul_rn(yd, wd);
+                    const float dmin = __fmul_rn(yd, wdm);
+                    const float pm = __fmul_rn(dmin, (float)mins);
+                    const float term = FUSED ? __builtin_fmaf(d, (float)mine[v], -pm)
+                                             : __fsub_rn(__fmul_rn(d, (float)mine[v]), pm);
+                    sum[v] = __fadd_rn(sum[v], term);
+                }
             }
         }
 
-        const float wd = s.wd[tn + col];
-        if (TYPE == 14) {
+        const int64_t row = r0 + tn + col;
+        if (row < n) {
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const float yd = s.yd[tm + tok_of(v, h)];
-                sum[v] = __fadd_rn(sum[v], __fmul_rn(__fmul_rn(wd, yd), (float)isum[v]));
-            }
-        } else {
-            // isum_mins = sum_j m_j * (bsums[2j] + bsums[2j+1]) as two small
-            // MFMAs: the bsum pairs enter as int8 digits (lo | hi), the mins
-            // sit against the lo half for one product and the hi half for
-            // the other, so mins = lo_product + 128 * hi_product exactly.
-            const long amv = *(const QK_LDS long *)&s.am[tm + col][8 * h];
-            const long mnv = *(const QK_LDS long *)&s.mn[tn + col][0];
-            const v16i dl = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 0 ? mnv : 0L, zero, 0, 0, 0);
-            const v16i dh = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 1 ? mnv : 0L, zero, 0, 0, 0);
-            const float wdm = s.wdm[tn + col];
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int32_t mins = dl[v] + dh[v] * 128;
-                const float yd = s.yd[tm + tok_of(v, h)];
-                const float d = __fmul_rn(yd, wd);
-                const float dmin = __fmul_rn(yd, wdm);
-                const float pm = __fmul_rn(dmin, (float)mins);
-                const float term = FUSED ? __builtin_fmaf(d, (float)isum[v], -pm)
-                                         : __fsub_rn(__fmul_rn(d, (float)isum[v]), pm);
-                sum[v] = __fadd_rn(sum[v], term);
+            for (int v = 0; v < 8; v++) {
+                const int64_t t = t0 + tm + tok_of(8 * g + v, h);
+                if (t < m) y[t * n + row] = FUSED ? bcast8(sum[v]) : sum[v];
             }
         }
-    }
-
-    const int64_t row = r0 + tn + col;
-    if (row < n) {
-#pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const int64_t t = t0 + tm + tok_of(v, h);
-            if (t < m) y[t * n + row] = FUSED ? bcast8(sum[v]) : sum[v];
-        }
+    };
+    if (stage_w) {
+        typename WRawOf<TYPE>::T wr;
+        body(wr, std::true_type{});
+    } else {
+        ActRaw ar;
+        body(ar, std::false_type{});
     }
 }
 
@@ -462,8 +499,8 @@ hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, const u
     const dim3 grid((unsigned)((n + GM_BN - 1) / GM_BN), (unsigned)((m + GM_BM - 1) / GM_BM));
 #define QK_GEMM_LAUNCH(T)                                                                            \
     do {                                                                                             \
-        if (fused) hipLaunchKernelGGL((k_gemm<T, true>), grid, dim3(256), 0, s, w, n, nb, xq, m, y); \
-        else hipLaunchKernelGGL((k_gemm<T, false>), grid, dim3(256), 0, s, w, n, nb, xq, m, y);      \
+        if (fused) hipLaunchKernelGGL((k_gemm<T, true>), grid, dim3(512), 0, s, w, n, nb, xq, m, y); \
+        else hipLaunchKernelGGL((k_gemm<T, false>), grid, dim3(512), 0, s, w, n, nb, xq, m, y);      \
     } while (0)
     switch (type) {
         case 12: QK_GEMM_LAUNCH(12); break;
