@@ -14,22 +14,24 @@
 //    fp32 sum in super-block order, exactly like the reference's
 //    sequential `sum += term`.
 //
-// Work decomposition: a 512-thread workgroup owns a 64-token x 64-row
-// output tile and walks the super-blocks of K in order. For each one it
-// stages the 64 activation rows (int8 Q8_K quants, scale, bsum pairs;
-// threads 0-255) and the 64 weight rows, dequantised to int8 with their
-// sub-block scales (threads 256-511), into LDS; the next super-block's
-// raw bytes are loaded into registers meanwhile. Each of the 8 waves then
-// computes one 32x32 sub-tile over one half of the super-block's k range
-// (integer sums: exact in any order); the two waves of a sub-tile swap
-// halves of their int32 results through LDS and each finishes 8 of the
+// Work decomposition: a 512-thread workgroup owns a 64-token x BN-row
+// output tile (BN = 64, or 32 when 64-row tiles would leave CUs idle) and
+// walks the super-blocks of K in order. For each one it stages the 64
+// activation rows (int8 Q8_K quants, scale, bsum pairs; threads 0-255)
+// and the BN weight rows, dequantised to int8 with their sub-block
+// scales (the next 4*BN threads), into LDS; the next super-block's raw
+// bytes are loaded into registers meanwhile. Each 32x32 sub-tile is
+// computed by KS = 128 / BN waves, each over 1/KS of the super-block's k
+// range (integer sums: exact in any order); the waves of a sub-tile
+// exchange their int32 parts through LDS and each finishes 16/KS of the
 // 16 outputs per lane:
 //
 //  * Q4_K / Q5_K: the 6-bit sub-block scales are split into two 3-bit
 //    digits and baked into int8 weight planes (plus a 5th-bit plane for
 //    Q5_K), so one chain of v_mfma_i32_32x32x32_i8 per plane accumulates
-//    the wave's half super-block and isum = acc0 + 8*acc1 (+ 16*acc2); mins
-//    from the Q8_K bsums (simd/quants.h:283-304, 324-349);
+//    the wave's part of the super-block and
+//    isum = acc0 + 8*acc1 (+ 16*acc2); mins from the Q8_K bsums
+//    (simd/quants.h:283-304, 324-349);
 //  * Q6_K: one v_mfma_i32_32x32x16_i8 per 16-element sub-block, weights
 //    staged as u6 - 32 in [-32, 31] so the reference's
 //    isum - 32*isum_mins (simd/quants.h:359-399) is one exact int32 sum.
@@ -49,7 +51,6 @@ typedef int32_t v4i __attribute__((ext_vector_type(4)));
 typedef int32_t v16i __attribute__((ext_vector_type(16)));
 
 #define GM_BM 64                      // tokens per workgroup tile
-#define GM_BN 64                      // weight rows per workgroup tile
 #define GM_LD 272                     // LDS row stride of the int8 tiles (256 + 16)
 
 // Dequantised weight planes per super-block. Q4_K / Q5_K: the 6-bit
@@ -63,16 +64,16 @@ typedef int32_t v16i __attribute__((ext_vector_type(16)));
 // MFMA.
 template <int TYPE> struct Planes { static constexpr int n = TYPE == 12 ? 2 : (TYPE == 13 ? 3 : 1); };
 
-template <int NP>
+template <int NP, int BN>
 struct __attribute__((aligned(16))) GemmLds {
     int8_t a[GM_BM][GM_LD];           // activation quants of the super-block
-    int8_t b[NP][GM_BN][GM_LD];       // dequantised int8 weight planes
+    int8_t b[NP][BN][GM_LD];          // dequantised int8 weight planes
     int8_t am[GM_BM][16];             // bsum pairs p = 128*hi + lo: lo[8] (0..127) | hi[8] (-64..63)
     float yd[GM_BM];                  // Q8_K d per token
-    int8_t sc[GM_BN][16];             // Q6_K sub-block scales per weight row
-    uint8_t mn[GM_BN][8];             // 6-bit mins (Q4_K / Q5_K)
-    float wd[GM_BN];                  // fp16 d, widened
-    float wdm[GM_BN];                 // fp16 dmin, widened
+    int8_t sc[BN][16];                // Q6_K sub-block scales per weight row
+    uint8_t mn[BN][8];                // 6-bit mins (Q4_K / Q5_K)
+    float wd[BN];                     // fp16 d, widened
+    float wdm[BN];                    // fp16 dmin, widened
 };
 
 __device__ __forceinline__ void lds_st16(void *p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
@@ -346,60 +347,74 @@ template <> struct WRawOf<14> { typedef WRaw14 T; };
 // row) = lane % 32, row (token) = 8*(v/4) + 4*(lane/32) + v%4.
 __device__ __forceinline__ int tok_of(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
 
-template <int TYPE, bool FUSED>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb,
-                                                 const uint8_t *__restrict__ xq, int64_t m, float *__restrict__ y) {
+struct NoRaw {};
+
+// BN = 64: four 32x32 sub-tiles, two waves each (halves of the super-
+// block's k); BN = 32: two sub-tiles, four waves each (quarters). Either
+// way 8 waves; each wave finishes VPW = 16 / KS of its sub-tile's 16
+// outputs per lane after the exchange.
+template <int TYPE, bool FUSED, int BN>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
+void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb, const uint8_t *__restrict__ xq, int64_t m,
+            float *__restrict__ y) {
     constexpr int BB = TYPE == 12 ? Q4K_BYTES : (TYPE == 13 ? Q5K_BYTES : Q6K_BYTES);
-    constexpr bool ALIAS = TYPE == 13;                       // Q5_K: exchange through the activation tile
-    __shared__ GemmLds<Planes<TYPE>::n> s;
-    __shared__ int32_t xch_mem[ALIAS ? 1 : 4 * 2 * 8 * 64];
+    constexpr int NT = BN / 32;                              // sub-tile columns
+    constexpr int NSUB = 2 * NT;                             // sub-tiles
+    constexpr int KS = 8 / NSUB;                             // waves per sub-tile
+    constexpr int VPW = 16 / KS;                             // outputs per lane a wave finishes
+    constexpr bool ALIAS = TYPE == 13 && BN == 64;           // Q5_K: exchange through the activation tile
+    constexpr int XCH = NSUB * KS * (KS - 1) * VPW * 64;     // exchange words
+    __shared__ GemmLds<Planes<TYPE>::n, BN> s;
+    __shared__ int32_t xch_mem[ALIAS ? 1 : XCH];
     int32_t *xch = ALIAS ? reinterpret_cast<int32_t *>(&s.a[0][0]) : xch_mem;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 31, h = lane >> 5;
-    const int sub = wave & 3, g = wave >> 2;                 // 32x32 sub-tile, half of the super-block's k
-    const int tm = 32 * (sub >> 1), tn = 32 * (sub & 1);
-    const int64_t r0 = (int64_t)blockIdx.x * GM_BN, t0 = (int64_t)blockIdx.y * GM_BM;
-    // staging roles: threads 0..255 stage activation rows, 256..511 weight
-    // rows; row st of the tile, quarter sq
-    const bool stage_w = threadIdx.x >= 256;
+    const int sub = wave % NSUB, g = wave / NSUB;            // sub-tile, part of the super-block's k
+    const int tm = 32 * (sub / NT), tn = 32 * (sub % NT);
+    const int64_t r0 = (int64_t)blockIdx.x * BN, t0 = (int64_t)blockIdx.y * GM_BM;
+    // staging roles: threads 0..255 stage activation rows, the next 4*BN
+    // weight rows, the rest (BN = 32) nothing; row st of the tile, quarter sq
+    const int role = threadIdx.x < 256 ? 0 : (threadIdx.x < 256 + 4 * BN ? 1 : 2);
     const int st = (threadIdx.x & 255) >> 2, sq = threadIdx.x & 3;
-    const uint8_t *xrow = (!stage_w && t0 + st < m) ? xq + (t0 + st) * nb * Q8K_BYTES + 4 * sq : nullptr;
-    const uint8_t *wrow = (stage_w && r0 + st < n) ? w + (r0 + st) * nb * BB : nullptr;
+    const uint8_t *xrow = (role == 0 && t0 + st < m) ? xq + (t0 + st) * nb * Q8K_BYTES + 4 * sq : nullptr;
+    const uint8_t *wrow = (role == 1 && r0 + st < n) ? w + (r0 + st) * nb * BB : nullptr;
 
     const int8_t *arow = &s.a[tm + col][0];
     const v16i zero = {0};
-    // The loop runs in one of two copies, one per staging role, so that a
-    // thread holds registers for its own raw bytes only.
-    auto body = [&](auto &raw, auto role) {
-        constexpr bool SW = decltype(role)::value;
-        float sum[8];
+    // The loop runs in one copy per staging role, so that a thread holds
+    // registers for its own raw bytes only.
+    auto body = [&](auto &raw, auto role_c) {
+        constexpr int R = decltype(role_c)::value;
+        float sum[VPW];
 #pragma unroll
-        for (int v = 0; v < 8; v++) sum[v] = 0.0f;
-        if constexpr (SW) load_w(raw, wrow, sq, 0);
-        else load_act(raw, xrow, sq, 0);
+        for (int v = 0; v < VPW; v++) sum[v] = 0.0f;
+        if constexpr (R == 1) load_w(raw, wrow, sq, 0);
+        if constexpr (R == 0) load_act(raw, xrow, sq, 0);
 
         for (int i = 0; i < nb; i++) {
             lds_barrier();                                       // previous super-block's reads done
-            if constexpr (SW) store_w(s, raw, st, sq);
-            else store_act(s, raw, st, sq);
+            if constexpr (R == 1) store_w(s, raw, st, sq);
+            if constexpr (R == 0) store_act(s, raw, st, sq);
             if (i + 1 < nb) {                                    // next super-block in flight during compute
-                if constexpr (SW) load_w(raw, wrow, sq, i + 1);
-                else load_act(raw, xrow, sq, i + 1);
+                if constexpr (R == 1) load_w(raw, wrow, sq, i + 1);
+                if constexpr (R == 0) load_act(raw, xrow, sq, i + 1);
             }
             lds_barrier();
 
-            // this wave's half of the super-block's k range
+            // this wave's part of the super-block's k range
             int32_t isum[16];
             if constexpr (TYPE == 14) {
                 // per 16-element sub-block: MFMA, then times its int8 scale
+                constexpr int SPW = 16 / KS;
                 const int8_t *brow = &s.b[0][tn + col][0];
 #pragma unroll
                 for (int v = 0; v < 16; v++) isum[v] = 0;
-                const uint2 scp = *(const QK_LDS uint2 *)&s.sc[tn + col][8 * g];
-                const uint32_t scw[2] = {scp.x, scp.y};
+                uint32_t scw[SPW / 4];
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const int sb = 8 * g + j;
+                for (int q = 0; q < SPW / 4; q++) scw[q] = *(const QK_LDS uint32_t *)&s.sc[tn + col][SPW * g + 4 * q];
+#pragma unroll
+                for (int j = 0; j < SPW; j++) {
+                    const int sb = SPW * g + j;
                     const long av = *(const QK_LDS long *)(arow + 16 * sb + 8 * h);
                     const long bv = *(const QK_LDS long *)(brow + 16 * sb + 8 * h);
                     const v16i d = __builtin_amdgcn_mfma_i32_32x32x16_i8(av, bv, zero, 0, 0, 0);
@@ -408,14 +423,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
                     for (int v = 0; v < 16; v++) isum[v] += __mul24(scv, d[v]);
                 }
             } else {
-                // one accumulation chain per digit plane over the half
+                // one accumulation chain per digit plane over the part
                 constexpr int NP = Planes<TYPE>::n;
+                constexpr int CPW = 8 / KS;
                 v16i acc[NP];
 #pragma unroll
                 for (int pl = 0; pl < NP; pl++) acc[pl] = zero;
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int c = 4 * g + j;
+                for (int j = 0; j < CPW; j++) {
+                    const int c = CPW * g + j;
                     const v4i av = *(const QK_LDS v4i *)(arow + 32 * c + 16 * h);
 #pragma unroll
                     for (int pl = 0; pl < NP; pl++) {
@@ -430,24 +446,39 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
                     isum[v] = t;
                 }
             }
-            // The two waves of a sub-tile swap halves: this wave finishes
-            // outputs v = 8g .. 8g+7 and hands the other eight to its partner.
-            // Integer sums: exact in any order.
+            // The KS waves of a sub-tile exchange parts: wave g finishes
+            // outputs v = VPW*g .. VPW*g + VPW-1 and hands the others to
+            // their owners. Integer sums: exact in any order.
             if (ALIAS) lds_barrier();                            // every wave is done reading s.a
-            int32_t *xo = xch + ((sub * 2 + (1 - g)) * 8) * 64 + lane;
-            const int32_t *xi = xch + ((sub * 2 + g) * 8) * 64 + lane;
 #pragma unroll
-            for (int v = 0; v < 8; v++) xo[64 * v] = g ? isum[v] : isum[8 + v];
+            for (int o = 0; o < KS; o++) {
+                if (o == g) continue;
+                const int slot = (g - o - 1 + KS) % KS;
+                int32_t *xo = xch + (((sub * KS + o) * (KS - 1) + slot) * VPW) * 64 + lane;
+#pragma unroll
+                for (int v = 0; v < VPW; v++) xo[64 * v] = isum[VPW * o + v];
+            }
             lds_barrier();
-            int32_t mine[8];
+            // own part (g is wave-uniform; selects keep every index static)
+            int32_t mine[VPW];
 #pragma unroll
-            for (int v = 0; v < 8; v++) mine[v] = (g ? isum[8 + v] : isum[v]) + xi[64 * v];
+            for (int v = 0; v < VPW; v++) {
+                mine[v] = isum[v];
+#pragma unroll
+                for (int q = 1; q < KS; q++) mine[v] = g == q ? isum[VPW * q + v] : mine[v];
+            }
+#pragma unroll
+            for (int sl = 0; sl < KS - 1; sl++) {
+                const int32_t *xi = xch + (((sub * KS + g) * (KS - 1) + sl) * VPW) * 64 + lane;
+#pragma unroll
+                for (int v = 0; v < VPW; v++) mine[v] += xi[64 * v];
+            }
 
             const float wd = s.wd[tn + col];
             if constexpr (TYPE == 14) {
 #pragma unroll
-                for (int v = 0; v < 8; v++) {
-                    const float yd = s.yd[tm + tok_of(8 * g + v, h)];
+                for (int v = 0; v < VPW; v++) {
+                    const float yd = s.yd[tm + tok_of(VPW * g + v, h)];
                     sum[v] = __fadd_rn(sum[v], __fmul_rn(__fmul_rn(wd, yd), (float)mine[v]));
                 }
             } else {
@@ -461,9 +492,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
                 const v16i dh = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 1 ? mnv : 0L, zero, 0, 0, 0);
                 const float wdm = s.wdm[tn + col];
 #pragma unroll
-                for (int v = 0; v < 8; v++) {
-                    const int vv = 8 * g + v;
-                    const int32_t mins = (g ? dl[8 + v] : dl[v]) + (g ? dh[8 + v] : dh[v]) * 128;
+                for (int v = 0; v < VPW; v++) {
+                    const int vv = VPW * g + v;
+                    int32_t ml = dl[v], mh = dh[v];
+#pragma unroll
+                    for (int q = 1; q < KS; q++) {
+                        ml = g == q ? dl[VPW * q + v] : ml;
+                        mh = g == q ? dh[VPW * q + v] : mh;
+                    }
+                    const int32_t mins = ml + mh * 128;
                     const float yd = s.yd[tm + tok_of(vv, h)];
                     const float d = __fmul_rn(yd, wd);
                     const float dmin = __fmul_rn(yd, wdm);
@@ -478,29 +515,41 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
         const int64_t row = r0 + tn + col;
         if (row < n) {
 #pragma unroll
-            for (int v = 0; v < 8; v++) {
-                const int64_t t = t0 + tm + tok_of(8 * g + v, h);
+            for (int v = 0; v < VPW; v++) {
+                const int64_t t = t0 + tm + tok_of(VPW * g + v, h);
                 if (t < m) y[t * n + row] = FUSED ? bcast8(sum[v]) : sum[v];
             }
         }
     };
-    if (stage_w) {
+    if (role == 1) {
         typename WRawOf<TYPE>::T wr;
-        body(wr, std::true_type{});
-    } else {
+        body(wr, std::integral_constant<int, 1>{});
+    } else if (role == 0) {
         ActRaw ar;
-        body(ar, std::false_type{});
+        body(ar, std::integral_constant<int, 0>{});
+    } else {
+        NoRaw nr;
+        body(nr, std::integral_constant<int, 2>{});
     }
 }
 
 hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, const uint8_t *xq, int64_t m,
                        float *y, int fused, hipStream_t s) {
     const int nb = (int)(k / QK_K);
-    const dim3 grid((unsigned)((n + GM_BN - 1) / GM_BN), (unsigned)((m + GM_BM - 1) / GM_BM));
-#define QK_GEMM_LAUNCH(T)                                                                            \
-    do {                                                                                             \
-        if (fused) hipLaunchKernelGGL((k_gemm<T, true>), grid, dim3(512), 0, s, w, n, nb, xq, m, y); \
-        else hipLaunchKernelGGL((k_gemm<T, false>), grid, dim3(512), 0, s, w, n, nb, xq, m, y);      \
+    const unsigned mt = (unsigned)((m + GM_BM - 1) / GM_BM);
+    // 64-row tiles when they alone give every CU a workgroup, else 32-row
+    // tiles (twice the workgroups, k split four ways)
+    const bool narrow = (uint64_t)((n + 63) / 64) * mt < 256;
+    const dim3 grid64((unsigned)((n + 63) / 64), mt), grid32((unsigned)((n + 31) / 32), mt);
+#define QK_GEMM_LAUNCH(T)                                                                                   \
+    do {                                                                                                    \
+        if (narrow) {                                                                                       \
+            if (fused) hipLaunchKernelGGL((k_gemm<T, true, 32>), grid32, dim3(512), 0, s, w, n, nb, xq, m, y); \
+            else hipLaunchKernelGGL((k_gemm<T, false, 32>), grid32, dim3(512), 0, s, w, n, nb, xq, m, y);      \
+        } else {                                                                                            \
+            if (fused) hipLaunchKernelGGL((k_gemm<T, true, 64>), grid64, dim3(512), 0, s, w, n, nb, xq, m, y); \
+            else hipLaunchKernelGGL((k_gemm<T, false, 64>), grid64, dim3(512), 0, s, w, n, nb, xq, m, y);      \
+        }                                                                                                   \
     } while (0)
     switch (type) {
         case 12: QK_GEMM_LAUNCH(12); break;
