@@ -398,8 +398,26 @@ __device__ __forceinline__ uint64_t argkey(float v, int64_t row) {
 // issued before item i is reduced, and the first item's loads go out
 // before the activation row is staged. Item offsets are 32-bit: the API
 // limits a matrix to 4 GB.
+// The P super-block terms of a row, from the first lane of each of its P
+// four-lane groups, into the row's first lane (the only lane that adds
+// and stores them, in order). P = 4: the groups sit 4 lanes apart in one
+// 16-lane row, so DPP row_shl moves them; wider rows cross DPP rows and
+// use ds_bpermute.
+template <int P>
+__device__ __forceinline__ void gather_terms(float (&tg)[P], float t, int src0) {
+    if constexpr (P == 4) {
+        tg[0] = t;
+        tg[1] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x104, 0xF, 0xF, true));
+        tg[2] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x108, 0xF, 0xF, true));
+        tg[3] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x10C, 0xF, 0xF, true));
+    } else {
+#pragma unroll
+        for (int g2 = 0; g2 < P; g2++) tg[g2] = __shfl(t, src0 + 4 * g2);
+    }
+}
+
 template <int TYPE, int LP, bool FUSED>
-__device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best) {
+__device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best, bool keys) {
     constexpr int BB = TYPE == 12 ? Q4K_BYTES : (TYPE == 13 ? Q5K_BYTES : Q6K_BYTES);
     constexpr int P = 1 << LP;
     constexpr int RPW = 16 >> LP;                      // rows per wave item
@@ -460,8 +478,7 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
         read_sb(r, wb, sp.ofs + lofs, j);
         const float t = term_sb<FUSED>(r, it * P + g, j, lds, nb);
         float tg[P];
-#pragma unroll
-        for (int g2 = 0; g2 < P; g2++) tg[g2] = __shfl(t, src0 + 4 * g2);
+        gather_terms<P>(tg, t, src0);
         const int lim = (nb - it * P < P) ? nb - it * P : P;
 #pragma unroll
         for (int g2 = 0; g2 < P; g2++)
@@ -471,8 +488,10 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
             if (FUSED) sum = bcast8(sum);
             if (row < n && g == 0 && j == 0) {
                 *(QK_GLOBAL float *)(y + row) = sum;
-                const uint64_t k = argkey(sum, row);
-                best = k > best ? k : best;
+                if (keys) {
+                    const uint64_t k = argkey(sum, row);
+                    best = k > best ? k : best;
+                }
             }
             sum = 0.0f;
         }
@@ -508,7 +527,7 @@ __device__ __forceinline__ void load_direct(Raw<13> &r, __amdgpu_buffer_rsrc_t r
     r.q1 = bl128(rs, off + 64 + 32 * j);
 }
 template <int TYPE, int LP, bool FUSED>
-__device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best) {
+__device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best, bool keys) {
     constexpr int BB = TYPE == 12 ? Q4K_BYTES : Q5K_BYTES;
     constexpr int P = 1 << LP;
     constexpr int RPW = 16 >> LP;
@@ -553,8 +572,7 @@ __device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t
         load_direct(nxt, rsrc(ntile, nit), lofs, j);
         const float t = term_sb<FUSED>(cur, it * P + g, j, lds, nb);
         float tg[P];
-#pragma unroll
-        for (int g2 = 0; g2 < P; g2++) tg[g2] = __shfl(t, src0 + 4 * g2);
+        gather_terms<P>(tg, t, src0);
         const int lim = (nb - it * P < P) ? nb - it * P : P;
 #pragma unroll
         for (int g2 = 0; g2 < P; g2++)
@@ -564,8 +582,10 @@ __device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t
             if (FUSED) sum = bcast8(sum);
             if (row < n && g == 0 && j == 0) {
                 *(QK_GLOBAL float *)(y + row) = sum;
-                const uint64_t k = argkey(sum, row);
-                best = k > best ? k : best;
+                if (keys) {
+                    const uint64_t k = argkey(sum, row);
+                    best = k > best ? k : best;
+                }
             }
             sum = 0.0f;
         }
@@ -589,7 +609,7 @@ __device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t
 //        ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7));
 //  separate (scalar/AVX1): sum = sum + (float)(sum_s p_s) * s_b.
 template <bool FUSED>
-__device__ __forceinline__ void run_q80(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best) {
+__device__ __forceinline__ void run_q80(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best, bool keys) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int s = lane & 7, ph = lane >> 3;
@@ -692,8 +712,10 @@ __device__ __forceinline__ void run_q80(const KDesc &D, int lw, int nwg, uint8_t
                 }
                 if (lane == 0) {
                     *(QK_GLOBAL float *)(y + row) = r;
-                    const uint64_t k = argkey(r, row);
-                    best = k > best ? k : best;
+                    if (keys) {
+                        const uint64_t k = argkey(r, row);
+                        best = k > best ? k : best;
+                    }
                 }
                 acc = 0.0f;
             }
@@ -723,7 +745,7 @@ __device__ __forceinline__ int32_t dpp_shl8(int32_t v) {
 }
 
 template <int NB, bool FUSED>
-__device__ __forceinline__ void run_q80r(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best) {
+__device__ __forceinline__ void run_q80r(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best, bool keys) {
     constexpr int ROWB = NB * Q80_BYTES;               // 544 or 1088
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -808,8 +830,10 @@ __device__ __forceinline__ void run_q80r(const KDesc &D, int lw, int nwg, uint8_
         const int row = tile * 16 + wave * 4 + r;
         if (r < nr && h == 0 && s == 0) {
             *(QK_GLOBAL float *)(y + row) = acc;
-            const uint64_t k = argkey(acc, row);
-            best = k > best ? k : best;
+            if (keys) {
+                const uint64_t k = argkey(acc, row);
+                best = k > best ? k : best;
+            }
         }
         wave_sync();                                   // window reads done before the next store
         cur = nxt;
@@ -852,26 +876,27 @@ __global__ __launch_bounds__(256, 5) void k_gemv(uint32_t t0, uint32_t t1, uint3
     __builtin_memcpy(&D, &raw, sizeof(KDesc));
     const int lw = (int)blockIdx.x - D.wg0;
     uint64_t best = 0;
+    const bool keys = amax_partial != nullptr;        // argmax keys (LM head) wanted
     switch (D.type) {
         case 12:
-            if (D.p == 4) run_kqd<12, 2, FUSED>(D, lw, D.nwg, lds, best);
-            else if (D.p == 8) run_kqd<12, 3, FUSED>(D, lw, D.nwg, lds, best);
-            else run_kqd<12, 4, FUSED>(D, lw, D.nwg, lds, best);
+            if (D.p == 4) run_kqd<12, 2, FUSED>(D, lw, D.nwg, lds, best, keys);
+            else if (D.p == 8) run_kqd<12, 3, FUSED>(D, lw, D.nwg, lds, best, keys);
+            else run_kqd<12, 4, FUSED>(D, lw, D.nwg, lds, best, keys);
             break;
         case 13:
-            if (D.p == 4) run_kqd<13, 2, FUSED>(D, lw, D.nwg, lds, best);
-            else if (D.p == 8) run_kqd<13, 3, FUSED>(D, lw, D.nwg, lds, best);
-            else run_kqd<13, 4, FUSED>(D, lw, D.nwg, lds, best);
+            if (D.p == 4) run_kqd<13, 2, FUSED>(D, lw, D.nwg, lds, best, keys);
+            else if (D.p == 8) run_kqd<13, 3, FUSED>(D, lw, D.nwg, lds, best, keys);
+            else run_kqd<13, 4, FUSED>(D, lw, D.nwg, lds, best, keys);
             break;
         case 14:
-            if (D.p == 4) run_kq<14, 2, FUSED>(D, lw, D.nwg, lds, best);
-            else if (D.p == 8) run_kq<14, 3, FUSED>(D, lw, D.nwg, lds, best);
-            else run_kq<14, 4, FUSED>(D, lw, D.nwg, lds, best);
+            if (D.p == 4) run_kq<14, 2, FUSED>(D, lw, D.nwg, lds, best, keys);
+            else if (D.p == 8) run_kq<14, 3, FUSED>(D, lw, D.nwg, lds, best, keys);
+            else run_kq<14, 4, FUSED>(D, lw, D.nwg, lds, best, keys);
             break;
         default:
-            if (D.p == 4 && D.nb == 32) run_q80r<32, FUSED>(D, lw, D.nwg, lds, best);
-            else if (D.p == 4) run_q80r<16, FUSED>(D, lw, D.nwg, lds, best);
-            else run_q80<FUSED>(D, lw, D.nwg, lds, best);
+            if (D.p == 4 && D.nb == 32) run_q80r<32, FUSED>(D, lw, D.nwg, lds, best, keys);
+            else if (D.p == 4) run_q80r<16, FUSED>(D, lw, D.nwg, lds, best, keys);
+            else run_q80<FUSED>(D, lw, D.nwg, lds, best, keys);
             break;
     }
     if (amax_partial) {
