@@ -467,10 +467,11 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
     stage_q8k_rest(st0, ar, nb, lds, lds + D.lds_act);
     lds_barrier();
     float sum = 0.0f;
-    while (tile < ntiles) {
-        Chunk nxt;
-        chunk_load(nxt, nsp, lane);
-        chunk_store(cur, wb, sp, lane);
+    // item (tile, it) from registers c (range sp): through the window, the
+    // term, gathered into the row's first lane, which stores the row after
+    // its last item
+    auto item = [&](const Chunk &c, const Span &sp, int tile, int it) __attribute__((always_inline)) {
+        chunk_store(c, wb, sp, lane);
         wave_sync();
         // Lanes of a block past the row end or of a row past n compute a
         // term from in-range LDS bytes that is never added or stored.
@@ -496,6 +497,15 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
             sum = 0.0f;
         }
         wave_sync();                                   // window reads done before the next store
+    };
+    if (ntile >= ntiles) {                             // one item (a decode launch): no look-ahead
+        item(cur, sp, tile, it);
+        return;
+    }
+    while (tile < ntiles) {
+        Chunk nxt;
+        chunk_load(nxt, nsp, lane);
+        item(cur, sp, tile, it);
         cur = nxt;
         sp = nsp;
         tile = ntile;
@@ -567,10 +577,10 @@ __device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t
     stage_q8k_rest(st0, ar, nb, lds, lds + D.lds_act);
     lds_barrier();
     float sum = 0.0f;
-    while (tile < ntiles) {
-        Raw<TYPE> nxt;
-        load_direct(nxt, rsrc(ntile, nit), lofs, j);
-        const float t = term_sb<FUSED>(cur, it * P + g, j, lds, nb);
+    // item (tile, it) from registers c: its term, gathered into the row's
+    // first lane, which stores the row after its last item
+    auto item = [&](const Raw<TYPE> &c, int tile, int it) __attribute__((always_inline)) {
+        const float t = term_sb<FUSED>(c, it * P + g, j, lds, nb);
         float tg[P];
         gather_terms<P>(tg, t, src0);
         const int lim = (nb - it * P < P) ? nb - it * P : P;
@@ -589,6 +599,15 @@ __device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t
             }
             sum = 0.0f;
         }
+    };
+    if (ntile >= ntiles) {                             // one item (a decode launch): no look-ahead
+        item(cur, tile, it);
+        return;
+    }
+    while (tile < ntiles) {
+        Raw<TYPE> nxt;
+        load_direct(nxt, rsrc(ntile, nit), lofs, j);
+        item(cur, tile, it);
         cur = nxt;
         tile = ntile;
         it = nit;
@@ -791,12 +810,10 @@ __device__ __forceinline__ void run_q80r(const KDesc &D, int lw, int nwg, uint8_
     lds_barrier();
     const QK_LDS uint32_t *aq = (const QK_LDS uint32_t *)(lds);
     const QK_LDS float *ad = (const QK_LDS float *)(lds + NB * 32);
-    while (tile < ntiles) {
-        const int ntile = tile + nwg;
-        const Span nsp = span(ntile);
-        ChunkN<5> nxt;
-        chunk_load(nxt, nsp, lane);
-        chunk_store(cur, wb, sp, lane);
+    // item `tile` from registers c (range sp): through the window, then
+    // four rows' dots and one store per row
+    auto item = [&](const ChunkN<5> &c, const Span &sp, int tile) __attribute__((always_inline)) {
+        chunk_store(c, wb, sp, lane);
         wave_sync();
         const int nr = sp.npc / (ROWB / 16);
         const uint8_t *rowp = wb + r * ROWB;
@@ -836,6 +853,17 @@ __device__ __forceinline__ void run_q80r(const KDesc &D, int lw, int nwg, uint8_
             }
         }
         wave_sync();                                   // window reads done before the next store
+    };
+    if (tile + nwg >= ntiles) {                        // one item (a decode launch): no look-ahead
+        item(cur, sp, tile);
+        return;
+    }
+    while (tile < ntiles) {
+        const int ntile = tile + nwg;
+        const Span nsp = span(ntile);
+        ChunkN<5> nxt;
+        chunk_load(nxt, nsp, lane);
+        item(cur, sp, tile);
         cur = nxt;
         sp = nsp;
         tile = ntile;
