@@ -145,8 +145,9 @@ int hip_quantize_q8_0(const float *x, int64_t m, int64_t k, void *xq,
  * tensor_matmul_q{4k,5k,6k}_f32 / _q8_0_f32 at n_tok == 1
  * (slm/tensor.c:846-850, 912-917, 1026-1031, 974-979) and the
  * simd_q*_row_dot entry points it calls (simd/simd.c:236-250).
- * Limits: w 16-byte aligned; k <= 16384 (the activation row is staged
- * in LDS); the matrix (n rows x row bytes) below 4 GB (32-bit offsets). */
+ * Limits: w 16-byte aligned; k <= 16384 (a Q8_0 activation row is
+ * staged in LDS; the limit holds for every type); the matrix (n rows x
+ * row bytes) below 4 GB (32-bit offsets). */
 int hip_matvec_q4k (const void *w, int64_t n, int64_t k, const void *xq,
                     float *y, void *stream);
 int hip_matvec_q5k (const void *w, int64_t n, int64_t k, const void *xq,

@@ -127,7 +127,7 @@ int check_mat(int type, const void *w, int64_t n, int64_t k, const void *xq, con
     if (!w || !xq || !y) return fail(QK_ERR_ARG, "null pointer");
     if (n < 1 || k < 1) return fail(QK_ERR_ARG, "empty matrix (n=%lld, k=%lld)", (long long)n, (long long)k);
     if (k % block_elems(type)) return fail(QK_ERR_ARG, "k=%lld is not a multiple of %lld", (long long)k, (long long)block_elems(type));
-    if (k > 16384) return fail(QK_ERR_ARG, "k=%lld exceeds the 16384 limit of the LDS activation stage", (long long)k);
+    if (k > 16384) return fail(QK_ERR_ARG, "k=%lld exceeds the 16384 limit", (long long)k);
     if (n > 0x7fffffffLL) return fail(QK_ERR_ARG, "n=%lld exceeds 2^31-1 rows", (long long)n);
     // The GEMV streams the matrix with 16-byte loads from its base and
     // addresses it with 32-bit byte offsets (buffer loads).

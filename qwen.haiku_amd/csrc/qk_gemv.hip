@@ -18,70 +18,23 @@
 //
 // Arithmetic. An aligned group of 4 lanes owns one 256-element super-block:
 // each lane takes 32 quant bytes and runs v_dot4 against the activation
-// row staged in LDS, and the group sums its int32 partials with DPP. The
+// bytes they meet, which it loads straight from the Q8_K row into
+// registers (every workgroup reads the same row, so these loads hit the
+// L2 after the first); the group sums its int32 partials with DPP. The
 // super-block terms of a row are added in block order by one lane, so the
 // float sum rounds exactly as the reference's sequential `sum += term`
 // (simd/quants.h:305, simd/avx.c:467).
 //
-// Activations are staged once per workgroup into LDS with 16-byte
-// aligned quant rows (Q8_K: qs[nb][256] | bsums[nb][16] | d[nb]).
+// Q8_0 activation rows are staged once per workgroup into LDS
+// (qs[nb][32] | d[nb]).
 #include "qk_dev.h"
 #include "qk_kernels.h"
 
 namespace qk {
 
-// ---- activation staging ----------------------------------------------------
-// Dword i of the raw Q8_K row goes to its place in the LDS layout, in
-// rounds of 1024 dwords (4 per thread). Loads past the row return zeros
-// (buffer range check) and their stores land in `junk`, a spot that is
-// overwritten after the barrier that ends staging. The first round is
-// split: its loads go out before the weight loads (stage_q8k_first), its
-// stores after them (stage_q8k_rest), so the stores wait only for the
-// activations.
-struct Stage {
-    uint32_t v[4];
-};
-
+// Range-checked view of an activation row: loads past `bytes` read zeros.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t act_rsrc(const uint8_t *xq, int bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(xq), 0, bytes, 0x00020000);
-}
-
-__device__ __forceinline__ void stage_q8k_load(Stage &st, __amdgpu_buffer_rsrc_t r, int base, int tot) {
-#pragma unroll
-    for (int u = 0; u < 4; u++)
-        if (base + 256 * u < tot)
-            st.v[u] = __builtin_amdgcn_raw_buffer_load_b32(r, 4 * (base + 256 * u + (int)threadIdx.x), 0, 0);
-}
-
-__device__ __forceinline__ void stage_q8k_store(const Stage &st, int base, int tot, int nb, uint8_t *lds,
-                                                uint8_t *junk) {
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        if (base + 256 * u < tot) {
-            const int i = base + 256 * u + (int)threadIdx.x;
-            const int b = i / 73, q = i - b * 73;
-            // q == 0: d; 1..64: qs dword q-1; 65..72: bsums dword q-65
-            const int to_d = nb * 288 + 4 * b;
-            const int to_qs = b * 256 + 4 * q - 4;
-            const int to_bs = nb * 256 + b * 32 + 4 * q - 260;
-            int dst = q > 64 ? to_bs : to_qs;
-            dst = q == 0 ? to_d : dst;
-            uint8_t *p = (i < tot) ? lds + dst : junk;
-            *(QK_LDS uint32_t *)(p) = st.v[u];
-        }
-    }
-}
-
-// Rounds after the first (rows longer than 1024 dwords: k > 3584).
-__device__ __forceinline__ void stage_q8k_rest(const Stage &first, __amdgpu_buffer_rsrc_t r, int nb, uint8_t *lds,
-                                               uint8_t *junk) {
-    const int tot = nb * 73;
-    stage_q8k_store(first, 0, tot, nb, lds, junk);
-    for (int base = 1024; base < tot; base += 1024) {
-        Stage st;
-        stage_q8k_load(st, r, base, tot);
-        stage_q8k_store(st, base, tot, nb, lds, junk);
-    }
 }
 
 // Workgroup barrier that orders LDS only: it waits for the LDS stores
@@ -141,23 +94,6 @@ __device__ __forceinline__ int32_t sum4(int32_t v) {
     v += dpp_xor1(v);
     v += dpp_xor2(v);
     return v;
-}
-
-__device__ __forceinline__ int32_t dot32(const uint32_t (&w)[8], const uint8_t *a) {
-    const uint4 a0 = lds16(a), a1 = lds16(a + 16);
-    int32_t s = dot4(w[0], a0.x, 0);
-    s = dot4(w[1], a0.y, s);
-    s = dot4(w[2], a0.z, s);
-    s = dot4(w[3], a0.w, s);
-    s = dot4(w[4], a1.x, s);
-    s = dot4(w[5], a1.y, s);
-    s = dot4(w[6], a1.z, s);
-    return dot4(w[7], a1.w, s);
-}
-
-__device__ __forceinline__ int32_t bsum_pair(const uint8_t *act, int nb, int b, int s) {
-    const uint32_t v = lds32(act + nb * 256 + b * 32 + 4 * s);
-    return (int32_t)(int16_t)(v & 0xffffu) + (int32_t)(int16_t)(v >> 16);
 }
 
 // ---- wave-contiguous weight staging -------------------------------------------
@@ -255,51 +191,6 @@ template <> struct Raw<12> { uint4 hdr, q0, q1; };
 template <> struct Raw<13> { uint4 hdr, q0, q1, h0, h1; };
 template <> struct Raw<14> { uint32_t l[9], h[9], sh, sc, sc2, d; };
 
-// Q4_K (simd/quants.h:267-306): lane j holds chunk c = j, qs[32j..32j+32):
-// low nibbles pair with q8[64j..64j+32) under scale 2j, high nibbles with
-// q8[64j+32..64j+64) under scale 2j+1; mins 2j, 2j+1 meet bsum pairs 2j,
-// 2j+1.
-template <bool FUSED>
-__device__ __forceinline__ float term_sb(const Raw<12> &r, int b, int j, const uint8_t *act, int nb) {
-    const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-    uint32_t lo[8], hi[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        lo[i] = q[i] & M4;
-        hi[i] = (q[i] >> 4) & M4;
-    }
-    const uint8_t *a = act + b * 256 + 64 * j;
-    const int32_t slo = dot32(lo, a), shi = dot32(hi, a + 32);
-    int32_t sc0, m0, sc1, m1;
-    scale_min_pair(r.hdr.y, r.hdr.z, r.hdr.w, j, sc0, m0, sc1, m1);
-    const int32_t isum = sum4(__mul24(slo, sc0) + __mul24(shi, sc1));
-    const int32_t mins = sum4(__mul24(m0, bsum_pair(act, nb, b, 2 * j)) + __mul24(m1, bsum_pair(act, nb, b, 2 * j + 1)));
-    const float yd = ((const QK_LDS float *)(act + nb * 288))[b];
-    return kterm<FUSED>(yd, r.hdr.x & 0xffffu, r.hdr.x >> 16, isum, mins);
-}
-
-// Q5_K (simd/quants.h:310-351): as Q4_K plus bit 2j / 2j+1 of qh[l].
-template <bool FUSED>
-__device__ __forceinline__ float term_sb(const Raw<13> &r, int b, int j, const uint8_t *act, int nb) {
-    const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-    const uint32_t qh[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
-    const uint32_t s0 = 2 * j, s1 = 2 * j + 1;
-    uint32_t lo[8], hi[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        lo[i] = (q[i] & M4) | (((qh[i] >> s0) & 0x01010101u) << 4);
-        hi[i] = ((q[i] >> 4) & M4) | (((qh[i] >> s1) & 0x01010101u) << 4);
-    }
-    const uint8_t *a = act + b * 256 + 64 * j;
-    const int32_t slo = dot32(lo, a), shi = dot32(hi, a + 32);
-    int32_t sc0, m0, sc1, m1;
-    scale_min_pair(r.hdr.y, r.hdr.z, r.hdr.w, j, sc0, m0, sc1, m1);
-    const int32_t isum = sum4(__mul24(slo, sc0) + __mul24(shi, sc1));
-    const int32_t mins = sum4(__mul24(m0, bsum_pair(act, nb, b, 2 * j)) + __mul24(m1, bsum_pair(act, nb, b, 2 * j + 1)));
-    const float yd = ((const QK_LDS float *)(act + nb * 288))[b];
-    return kterm<FUSED>(yd, r.hdr.x & 0xffffu, r.hdr.x >> 16, isum, mins);
-}
-
 // Q6_K (simd/quants.h:356-402). Lane j = 2h + qq holds ql bytes
 // [32j, 32j+32) (positions l = 0..31 of half h, quarter qq): the low
 // nibble is element 128h + 32qq + l, the high nibble element +64; the two
@@ -325,9 +216,105 @@ __device__ __forceinline__ void read_sb(Raw<14> &r, const uint8_t *wb, int off, 
     r.d = lds_u16(wb + off + 208);
 }
 
+// ---- activation operands straight from the Q8_K row -----------------------
+// Block b of the row is 292 bytes: d (f32) | qs[256] | bsums[16] (i16).
+// Each lane loads the activation bytes its weights meet with range-checked
+// buffer loads (a lane of a super-block past the row end reads zeros and
+// its term is never added). Every workgroup reads the same row, so these
+// loads hit the L2 after the first.
+__device__ __forceinline__ uint32_t bl32(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint4 bl128a(__amdgpu_buffer_rsrc_t r, int off) {   // 4-byte aligned
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+// Q4_K / Q5_K lane j: qs[64j, 64j+64), bsums 4j..4j+3 (pairs 2j, 2j+1), d.
+struct ActK { uint4 a0, a1, a2, a3; uint32_t bs0, bs1; float d; };
+__device__ __forceinline__ void load_act(ActK &x, __amdgpu_buffer_rsrc_t r, int b, int j) {
+    const int o = b * Q8K_BYTES;
+    x.a0 = bl128a(r, o + 4 + 64 * j);
+    x.a1 = bl128a(r, o + 20 + 64 * j);
+    x.a2 = bl128a(r, o + 36 + 64 * j);
+    x.a3 = bl128a(r, o + 52 + 64 * j);
+    x.bs0 = bl32(r, o + 260 + 8 * j);
+    x.bs1 = bl32(r, o + 264 + 8 * j);
+    x.d = __uint_as_float(bl32(r, o));
+}
+// Q6_K lane j = 2h + qq, s = 8h + 2qq: qs of sub-blocks s, s+1 and s+4,
+// s+5, bsums s, s+1 and s+4, s+5, d.
+struct Act6 { uint4 a0, a1, a4, a5; uint32_t bl, bh; float d; };
+__device__ __forceinline__ void load_act(Act6 &x, __amdgpu_buffer_rsrc_t r, int b, int j) {
+    const int o = b * Q8K_BYTES, s = 8 * (j >> 1) + 2 * (j & 1);
+    x.a0 = bl128a(r, o + 4 + 16 * s);
+    x.a1 = bl128a(r, o + 20 + 16 * s);
+    x.a4 = bl128a(r, o + 68 + 16 * s);
+    x.a5 = bl128a(r, o + 84 + 16 * s);
+    x.bl = bl32(r, o + 260 + 2 * s);
+    x.bh = bl32(r, o + 268 + 2 * s);
+    x.d = __uint_as_float(bl32(r, o));
+}
+template <int T> struct ActOf { typedef ActK type; };
+template <> struct ActOf<14> { typedef Act6 type; };
+
+__device__ __forceinline__ int32_t dot32r(const uint32_t (&w)[8], const uint4 a0, const uint4 a1) {
+    int32_t s = dot4(w[0], a0.x, 0);
+    s = dot4(w[1], a0.y, s);
+    s = dot4(w[2], a0.z, s);
+    s = dot4(w[3], a0.w, s);
+    s = dot4(w[4], a1.x, s);
+    s = dot4(w[5], a1.y, s);
+    s = dot4(w[6], a1.z, s);
+    return dot4(w[7], a1.w, s);
+}
+__device__ __forceinline__ int32_t pair_of(uint32_t v) {
+    return (int32_t)(int16_t)(v & 0xffffu) + (int32_t)(int16_t)(v >> 16);
+}
+
+// Q4_K (simd/quants.h:267-306): lane j holds chunk c = j, qs[32j..32j+32):
+// low nibbles pair with q8[64j..64j+32) under scale 2j, high nibbles with
+// q8[64j+32..64j+64) under scale 2j+1; mins 2j, 2j+1 meet bsum pairs 2j,
+// 2j+1.
 template <bool FUSED>
-__device__ __forceinline__ float term_sb(const Raw<14> &r, int b, int j, const uint8_t *act, int nb) {
-    const int h = j >> 1, qq = j & 1;
+__device__ __forceinline__ float term_sb(const Raw<12> &r, const ActK &x, int j) {
+    const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        lo[i] = q[i] & M4;
+        hi[i] = (q[i] >> 4) & M4;
+    }
+    const int32_t slo = dot32r(lo, x.a0, x.a1), shi = dot32r(hi, x.a2, x.a3);
+    int32_t sc0, m0, sc1, m1;
+    scale_min_pair(r.hdr.y, r.hdr.z, r.hdr.w, j, sc0, m0, sc1, m1);
+    const int32_t isum = sum4(__mul24(slo, sc0) + __mul24(shi, sc1));
+    const int32_t mins = sum4(__mul24(m0, pair_of(x.bs0)) + __mul24(m1, pair_of(x.bs1)));
+    return kterm<FUSED>(x.d, r.hdr.x & 0xffffu, r.hdr.x >> 16, isum, mins);
+}
+// Q5_K (simd/quants.h:310-351): as Q4_K plus bit 2j / 2j+1 of qh[l].
+template <bool FUSED>
+__device__ __forceinline__ float term_sb(const Raw<13> &r, const ActK &x, int j) {
+    const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    const uint32_t qh[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+    const uint32_t s0 = 2 * j, s1 = 2 * j + 1;
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        lo[i] = (q[i] & M4) | (((qh[i] >> s0) & 0x01010101u) << 4);
+        hi[i] = ((q[i] >> 4) & M4) | (((qh[i] >> s1) & 0x01010101u) << 4);
+    }
+    const int32_t slo = dot32r(lo, x.a0, x.a1), shi = dot32r(hi, x.a2, x.a3);
+    int32_t sc0, m0, sc1, m1;
+    scale_min_pair(r.hdr.y, r.hdr.z, r.hdr.w, j, sc0, m0, sc1, m1);
+    const int32_t isum = sum4(__mul24(slo, sc0) + __mul24(shi, sc1));
+    const int32_t mins = sum4(__mul24(m0, pair_of(x.bs0)) + __mul24(m1, pair_of(x.bs1)));
+    return kterm<FUSED>(x.d, r.hdr.x & 0xffffu, r.hdr.x >> 16, isum, mins);
+}
+// Q6_K: the lane's share of isum - 32*isum_mins over sub-blocks s, s+1,
+// s+4, s+5 (see read_sb), exact in int32.
+template <bool FUSED>
+__device__ __forceinline__ float term_sb(const Raw<14> &r, const Act6 &x, int j) {
+    const int qq = j & 1;
     const uint32_t sh = r.sh, sa = 2 * qq;
     uint32_t lo[8], hi[8];
 #pragma unroll
@@ -337,23 +324,18 @@ __device__ __forceinline__ float term_sb(const Raw<14> &r, int b, int j, const u
         lo[i] = (ql & M4) | ((qh << 4) & 0x30303030u);
         hi[i] = ((ql >> 4) & M4) | (qh & 0x30303030u);
     }
-    const int s = 8 * h + 2 * qq;                      // sub-blocks s, s+1 | s+4, s+5
-    const uint8_t *a = act + b * 256 + 16 * s;
-    const int32_t d0 = dot16(lo[0], lo[1], lo[2], lo[3], lds16(a));
-    const int32_t d1 = dot16(lo[4], lo[5], lo[6], lo[7], lds16(a + 16));
-    const int32_t d4 = dot16(hi[0], hi[1], hi[2], hi[3], lds16(a + 64));
-    const int32_t d5 = dot16(hi[4], hi[5], hi[6], hi[7], lds16(a + 80));
+    const int32_t d0 = dot16(lo[0], lo[1], lo[2], lo[3], x.a0);
+    const int32_t d1 = dot16(lo[4], lo[5], lo[6], lo[7], x.a1);
+    const int32_t d4 = dot16(hi[0], hi[1], hi[2], hi[3], x.a4);
+    const int32_t d5 = dot16(hi[4], hi[5], hi[6], hi[7], x.a5);
     const int32_t sc0 = (int32_t)(int8_t)(r.sc & 0xffu), sc1 = (int32_t)(int8_t)(r.sc >> 8);
     const int32_t sc4 = (int32_t)(int8_t)(r.sc2 & 0xffu), sc5 = (int32_t)(int8_t)(r.sc2 >> 8);
-    const uint32_t bl = lds32(act + nb * 256 + b * 32 + 2 * s);
-    const uint32_t bh = lds32(act + nb * 256 + b * 32 + 2 * s + 8);
-    const int32_t b0 = (int16_t)(bl & 0xffffu), b1 = (int16_t)(bl >> 16);
-    const int32_t b4 = (int16_t)(bh & 0xffffu), b5 = (int16_t)(bh >> 16);
+    const int32_t b0 = (int16_t)(x.bl & 0xffffu), b1 = (int16_t)(x.bl >> 16);
+    const int32_t b4 = (int16_t)(x.bh & 0xffffu), b5 = (int16_t)(x.bh >> 16);
     const int32_t v = __mul24(d0, sc0) + __mul24(d1, sc1) + __mul24(d4, sc4) + __mul24(d5, sc5) -
                       32 * (__mul24(b0, sc0) + __mul24(b1, sc1) + __mul24(b4, sc4) + __mul24(b5, sc5));
     const int32_t tot = sum4(v);
-    const float yd = ((const QK_LDS float *)(act + nb * 288))[b];
-    return q6term(yd, r.d, tot);
+    return q6term(x.d, r.d, tot);
 }
 
 // Device-side descriptor: 64 bytes, fetched by one scalar load once a
@@ -452,11 +434,12 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
         sp.npc = len ? (int32_t)((s0 + len - a0 + 15) >> 4) : 0;
         return sp;
     };
-    // activation loads first, then the first item's weights; the staging
-    // stores then wait only for the activations
+    // activation operands of super-block g first (those of every item
+    // when a row is one item), then the first item's weights
     const __amdgpu_buffer_rsrc_t ar = act_rsrc(D.xq, nb * Q8K_BYTES);
-    Stage st0;
-    stage_q8k_load(st0, ar, 0, nb * 73);
+    Act6 xa;
+    load_act(xa, ar, g, j);
+    int xit = 0;
     int tile = lw, it = 0;
     Span sp = span(tile, it);
     Chunk cur;
@@ -464,8 +447,6 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
     int ntile = tile, nit = it + 1;
     if (nit == niter) { nit = 0; ntile += nwg; }
     Span nsp = span(ntile, nit);                       // computed while the loads are in flight
-    stage_q8k_rest(st0, ar, nb, lds, lds + D.lds_act);
-    lds_barrier();
     float sum = 0.0f;
     // item (tile, it) from registers c (range sp): through the window, the
     // term, gathered into the row's first lane, which stores the row after
@@ -477,7 +458,11 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
         // term from in-range LDS bytes that is never added or stored.
         Raw<TYPE> r;
         read_sb(r, wb, sp.ofs + lofs, j);
-        const float t = term_sb<FUSED>(r, it * P + g, j, lds, nb);
+        if (it != xit) {                               // rows of several items: next super-blocks
+            load_act(xa, ar, it * P + g, j);
+            xit = it;
+        }
+        const float t = term_sb<FUSED>(r, xa, j);
         float tg[P];
         gather_terms<P>(tg, t, src0);
         const int lim = (nb - it * P < P) ? nb - it * P : P;
@@ -566,21 +551,26 @@ __device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t
         const uint32_t s0 = (uint32_t)r0 * rowb + (uint32_t)(i * P * BB);
         return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w + s0), 0, (int)len, 0x00020000);
     };
+    // activation operands of super-block g first (those of every item
+    // when a row is one item), then the first item's weights
     const __amdgpu_buffer_rsrc_t ar = act_rsrc(D.xq, nb * Q8K_BYTES);
-    Stage st0;
-    stage_q8k_load(st0, ar, 0, nb * 73);
+    typename ActOf<TYPE>::type xa;
+    load_act(xa, ar, g, j);
+    int xit = 0;
     int tile = lw, it = 0;
     Raw<TYPE> cur;
     load_direct(cur, rsrc(tile, it), lofs, j);
     int ntile = tile, nit = it + 1;
     if (nit == niter) { nit = 0; ntile += nwg; }
-    stage_q8k_rest(st0, ar, nb, lds, lds + D.lds_act);
-    lds_barrier();
     float sum = 0.0f;
     // item (tile, it) from registers c: its term, gathered into the row's
     // first lane, which stores the row after its last item
     auto item = [&](const Raw<TYPE> &c, int tile, int it) __attribute__((always_inline)) {
-        const float t = term_sb<FUSED>(c, it * P + g, j, lds, nb);
+        if (it != xit) {                               // rows of several items: next super-blocks
+            load_act(xa, ar, it * P + g, j);
+            xit = it;
+        }
+        const float t = term_sb<FUSED>(c, xa, j);
         float tg[P];
         gather_terms<P>(tg, t, src0);
         const int lim = (nb - it * P < P) ? nb - it * P : P;
@@ -968,7 +958,7 @@ void gemv_plan(GemvDesc &d) {
         while (p < 16 && p < d.nb) p *= 2;
         d.p = p;
         d.rows_per_tile = 4 * (16 / p);
-        d.lds_act = (d.nb * 292 + 15) & ~15;
+        d.lds_act = 0;                                 // activations go straight to registers
     }
     d.tr = d.rows_per_tile;
     d.tile_cap = 0;

@@ -244,7 +244,7 @@ def test_rejects_bad_shapes(lib):
     L = lib.L
     assert L.hip_matvec_q4k(wp, 4, 1000, xp, yp, None) == 1          # k % 256
     assert L.hip_matvec_q4k(C.c_void_p(w.data_ptr() + 1), 1, 256, xp, yp, None) == 1   # misaligned
-    assert L.hip_matvec_q4k(wp, 1, 32768, xp, yp, None) == 1         # k above the LDS stage
+    assert L.hip_matvec_q4k(wp, 1, 32768, xp, yp, None) == 1         # k above 16384
     assert L.hip_matvec_q8_0(wp, 1, 32768, xp, yp, None) == 1
     assert L.hip_matvec_q4k(wp, 0, 256, xp, yp, None) == 1           # empty
     assert L.hip_matvec_q4k(None, 1, 256, xp, yp, None) == 1         # null
