@@ -370,16 +370,6 @@ __device__ __forceinline__ uint64_t argkey(float v, int64_t row) {
     return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)row);
 }
 
-// Q6_K rows handled by this workgroup (the LDS-window path): tiles
-// lw, lw+nwg, ... of 4 waves x 16/P rows. A row's P = 2^LP groups each take
-// one super-block of a step (P super-blocks); the P terms of a step are
-// gathered with ds_bpermute and added to the row sum in super-block order.
-// A wave item (tile, step) is one contiguous range of W: the wave's 16/P
-// whole rows when a row fits one step (nb <= P), else P super-blocks of
-// its one row (P = 16). Items are pipelined one deep: item i+1's loads are
-// issued before item i is reduced, and the first item's loads go out
-// before the activation row is staged. Item offsets are 32-bit: the API
-// limits a matrix to 4 GB.
 // The P super-block terms of a row, from the first lane of each of its P
 // four-lane groups, into the row's first lane (the only lane that adds
 // and stores them, in order). P = 4: the groups sit 4 lanes apart in one
@@ -398,6 +388,16 @@ __device__ __forceinline__ void gather_terms(float (&tg)[P], float t, int src0) 
     }
 }
 
+// Q6_K rows handled by this workgroup (the LDS-window path): tiles
+// lw, lw+nwg, ... of 4 waves x 16/P rows. A row's P = 2^LP groups each take
+// one super-block of a step (P super-blocks); the P terms of a step are
+// gathered into the row's first lane and added to the row sum in
+// super-block order. A wave item (tile, step) is one contiguous range of
+// W: the wave's 16/P whole rows when a row fits one step (nb <= P), else P
+// super-blocks of its one row (P = 16). Items are pipelined one deep: item
+// i+1's loads are issued before item i is reduced; the activation
+// operands' loads go out before the first item's. Item offsets are
+// 32-bit: the API limits a matrix to 4 GB.
 template <int TYPE, int LP, bool FUSED>
 __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best, bool keys) {
     constexpr int BB = TYPE == 12 ? Q4K_BYTES : (TYPE == 13 ? Q5K_BYTES : Q6K_BYTES);
