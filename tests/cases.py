@@ -38,3 +38,28 @@ def edge_rows(k):
     small = rng.normal(0, 1, 256).astype(np.float32) * np.float32(1e-3)
     rows.append(tile(small))
     return np.stack(rows).astype(np.float32)
+
+
+def special_rows(k):
+    """(m, k) float32 rows with NaN and infinity entries and |x| ties across
+    lanes, each 256-element block carrying the same pattern."""
+    rows = []
+    rng = np.random.default_rng(4321)
+    def tile(block):
+        return np.resize(np.asarray(block, np.float32), k)
+    t = rng.normal(0, 1, 256).astype(np.float32)
+    t[3], t[100] = np.nan, np.nan                          # NaN never chosen; quantizes to 0
+    t[200] = 7.0
+    rows.append(tile(t))
+    t = rng.normal(0, 1, 256).astype(np.float32)
+    t[10] = np.inf                                         # amax = inf: d = -inf, q = 0
+    rows.append(tile(t))
+    t = rng.normal(0, 1, 256).astype(np.float32)
+    t[20], t[200] = -4.0, 4.0                              # tie across lanes: the first wins
+    rows.append(tile(t))
+    t = rng.normal(0, 1, 256).astype(np.float32)
+    t[63], t[64] = 4.0, -4.0                               # tie across a 16-lane row boundary
+    rows.append(tile(t))
+    t = np.full(256, np.nan, np.float32)                   # all NaN: amax 0, d = 0
+    rows.append(tile(t))
+    return np.stack(rows).astype(np.float32)

@@ -7,7 +7,7 @@ Sizes: the BASELINE configurations at full size where the oracle is fast
 import numpy as np
 import pytest
 
-from cases import edge_rows
+from cases import edge_rows, special_rows
 from conftest import assert_bits_equal, oracle, qk, synth
 
 pytestmark = pytest.mark.gpu
@@ -35,7 +35,7 @@ def step(msg):
 @pytest.mark.parametrize("k", [256, 1024, 3584, 16384])
 def test_quantize_q8k_bit_exact(lib, orc, k):
     step(f"quantize_q8k k={k}")
-    x = np.concatenate([edge_rows(k), synth.activations(37, k, seed=k)])
+    x = np.concatenate([edge_rows(k), special_rows(k), synth.activations(37, k, seed=k)])
     got = host(lib.quantize_q8k(dev(x)))
     np.testing.assert_array_equal(got, orc.quantize_q8k(x))
 
@@ -43,7 +43,7 @@ def test_quantize_q8k_bit_exact(lib, orc, k):
 @pytest.mark.parametrize("k", [32, 1024, 2080])
 def test_quantize_q8_0_bit_exact(lib, orc, k):
     step(f"quantize_q8_0 k={k}")
-    x = np.concatenate([edge_rows(k), synth.activations(21, k, seed=k)])
+    x = np.concatenate([edge_rows(k), special_rows(k), synth.activations(21, k, seed=k)])
     got = host(lib.quantize_q8_0(dev(x)))
     np.testing.assert_array_equal(got, orc.quantize_q8_0(x))
 

@@ -15,7 +15,7 @@ import os
 import numpy as np
 import pytest
 
-from cases import edge_rows
+from cases import edge_rows, special_rows
 from conftest import assert_bits_equal, bits, oracle, synth
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -150,7 +150,7 @@ def test_q8_0_halves_away_from_zero(orc):
 
 
 def test_quantizers_vs_reference(orc, ref):
-    x = np.concatenate([edge_rows(2048), synth.activations(32, 2048, seed=9)])
+    x = np.concatenate([edge_rows(2048), special_rows(2048), synth.activations(32, 2048, seed=9)])
     np.testing.assert_array_equal(orc.quantize_q8k(x), ref.quantize_q8k(x))
     np.testing.assert_array_equal(orc.quantize_q8k(x), ref.quantize_q8k(x, quants_h=True))
     np.testing.assert_array_equal(orc.quantize_q8_0(x), ref.quantize_q8_0(x))
