@@ -304,3 +304,58 @@ def test_lmhead_topk_flat_logits_fallback(lib, orc):
     np.testing.assert_array_equal(host(ti), np.arange(topk))
     ri, _ = orc.topk_collect(want, topk)
     assert set(ri.tolist()) == set(range(topk))
+
+
+# ---- concurrency and streams -------------------------------------------------------------
+
+def test_host_seam_from_several_threads(lib, orc):
+    # The reference's model (and so its weights) may be shared by several
+    # contexts on several host threads (slm/slm.h:33-36); the seam's weight
+    # registry and staging buffers must hold up under concurrent calls.
+    import threading
+    step("host seam, 4 threads")
+    cases = [(12, 512, 1024, 1), (13, 256, 1024, 3), (14, 128, 1024, 1), (8, 256, 1024, 2)]
+    data = []
+    for i, (t, n, k, m) in enumerate(cases):
+        w = synth.blocks(t, n, k, seed=11, tag=i)
+        x = synth.activations(m, k, seed=11 + i)
+        data.append((t, w, n, k, x, orc.matmul(t, w, n, k, x, oracle.TIER_EPI[lib.tier()])))
+    errors = []
+
+    def worker(i):
+        try:
+            t, w, n, k, x, want = data[i]
+            for _ in range(5):
+                got = lib.matmul_host(t, w, n, k, x)
+                assert_bits_equal(got, want, f"thread {i}")
+        except Exception as e:              # reported below, on the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(data))]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(120)
+    assert not any(th.is_alive() for th in threads)
+    assert not errors, errors[0]
+    for t, w, n, k, x, want in data:
+        lib.unregister_weight(w)
+
+
+def test_matvec_on_a_side_stream(lib, orc):
+    # Entry points take the caller's stream; work queued there is ordered
+    # after the caller's own work on it and finishes before its sync.
+    import torch
+    step("matvec on a side stream")
+    t, n, k = 12, 3584, 1024
+    w = synth.blocks(t, n, k, seed=12)
+    x = synth.activations(1, k, seed=12)
+    want = orc.matmul(t, w, n, k, x, oracle.TIER_EPI[lib.tier()])[0]
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        wd = dev(w)
+        xd = torch.from_numpy(x).cuda()
+        xq = lib.quantize_q8k(xd)[0]
+        y = lib.matvec(t, wd, n, k, xq)
+    side.synchronize()
+    assert_bits_equal(host(y), want, "side stream")
