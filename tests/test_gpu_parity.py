@@ -72,6 +72,8 @@ SHAPES = [
     (14, 1024, 3584), (8, 1024, 1024),                     # config 1
     (12, 7, 256), (12, 33, 768), (12, 65, 1280), (13, 19, 512), (14, 17, 768),
     (14, 100, 2560), (12, 40, 16384), (14, 9, 16384), (8, 45, 96), (8, 3, 16384),
+    (13, 21, 8192), (8, 70, 512),                          # Q5_K rows of two items; Q8_0 512 rows path
+    (12, 40000, 256), (13, 40000, 256),                    # more tiles than workgroups: items in a loop
 ]
 
 
