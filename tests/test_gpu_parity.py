@@ -130,6 +130,9 @@ GEMM_SHAPES = [
     (13, 2048, 1024, 96), (13, 1024, 2048, 33),
     (12, 100, 768, 37), (13, 65, 256, 1), (14, 63, 512, 65), (14, 129, 1280, 7),
     (12, 64, 256, 64), (12, 1, 512, 3),
+    # 64-row tiles (at least 256 of them) for every type; the others run
+    # 32-row tiles with a four-way k split
+    (13, 4096, 1024, 512), (14, 4096, 1024, 300), (12, 4160, 512, 260),
 ]
 
 
