@@ -79,10 +79,13 @@ class Events:
         return e0.elapsed_time(e1) / 1e3            # seconds
 
 
-def bench_config1(torch, qk, synth, lib, steps, warmup):
+def bench_config1(torch, qk, synth, lib, steps, warmup, warm=False):
+    """Config 1 (the metric). warm=True: one weight copy, so the 11.5 MB
+    stay in the 256 MB MALL between steps (a labelled warm-cache figure,
+    never the metric)."""
     per_set = sum(alg_bytes(*s) for s in CONFIG1)
     wbytes = sum(alg_bytes(*s) - ((s[2] // 32) * 34 if s[0] == 8 else (s[2] // 256) * 292) - 4 * s[1] for s in CONFIG1)
-    copies = max(2, -(-MALL_DEFEAT_BYTES // wbytes))
+    copies = 1 if warm else max(2, -(-MALL_DEFEAT_BYTES // wbytes))
     base = []
     for i, (t, n, k) in enumerate(CONFIG1):
         w = torch.from_numpy(synth.blocks(t, n, k, seed=0, tag=i)).cuda()
@@ -307,6 +310,10 @@ def main():
     }
     if not a.no_extra:
         extra = {}
+        pw, cw, sw = bench_config1(torch, qk, synth, lib, a.steps, a.warmup, warm=True)
+        extra["config1_warm_mall"] = {"GB/s": round(pw * a.steps / sw / 1e9, 2),
+                                      "us_per_launch": round(sw / a.steps * 1e6, 3), "copies": cw,
+                                      "note": "one weight copy, resident in the 256 MB MALL; not HBM"}
         p0, c0, s0 = bench_config0(torch, qk, synth, lib, a.steps, a.warmup)
         extra["config0_q4k_gemv"] = {"GB/s": round(p0 * a.steps / s0 / 1e9, 2),
                                      "us_per_launch": round(s0 / a.steps * 1e6, 3), "copies": c0}
