@@ -116,6 +116,26 @@ def bench_config1(torch, qk, synth, lib, steps, warmup, warm=False):
     return per_set, copies, secs
 
 
+def config1_each(torch, qk, synth, lib, steps):
+    """Each distinct config-1 matrix alone (one-descriptor launches), then
+    the set, `steps` launches each, for per-kernel counters: a profiling
+    aid, not a benchmark figure (one weight copy)."""
+    items, seen, out = [], set(), {}
+    for i, (t, n, k) in enumerate(CONFIG1):
+        w = torch.from_numpy(synth.blocks(t, n, k, seed=0, tag=i)).cuda()
+        x = torch.from_numpy(synth.activations(1, k, seed=0, tag=i)).cuda()
+        items.append((t, w, n, k, lib.quantize_for(t, x)[0], torch.empty(n, dtype=torch.float32, device="cuda")))
+    ev = Events(torch)
+    for it in items:
+        key = f"{it[0]}_{it[2]}x{it[3]}"
+        if key in seen:
+            continue
+        seen.add(key)
+        out[key] = round(ev.time(lambda i: lib.matvec_group([it]), steps, 2) / steps * 1e6, 3)
+    out["set"] = round(ev.time(lambda i: lib.matvec_group(items), steps, 2) / steps * 1e6, 3)
+    return out
+
+
 def bench_config0(torch, qk, synth, lib, steps, warmup):
     t, n, k = 12, 3584, 1024
     per = alg_bytes(t, n, k)
@@ -265,8 +285,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["all", "config3"], default="all",
-                    help="config3: time only the prefill GEMM cases (a profiling aid)")
+    ap.add_argument("--only", choices=["all", "config3", "each"], default="all",
+                    help="config3: time only the prefill GEMM cases; each: launch every config-1 "
+                         "matrix alone, then the set (profiling aids)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run 8 plain device copies of MIB MiB each: the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -287,6 +308,10 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    if a.only == "each":
+        print(json.dumps({"metric": "config-1 matrices alone, us per launch", "unit": "us",
+                          "extra": config1_each(torch, qk, synth, lib, a.steps)}))
+        return
     if a.only == "config3":
         print(json.dumps({"metric": "prefill int8 TOPS (config 3)", "unit": "TOPS", "dtype": "int8",
                           "extra": config3_extras(torch, qk, synth, lib, a.steps)}))
