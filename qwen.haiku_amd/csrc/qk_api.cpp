@@ -456,7 +456,15 @@ int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f, int64_t k, c
         dx = static_cast<const float *>(s.dx);
     }
     uint8_t *dxq = static_cast<uint8_t *>(s.dxq);
+    // y likewise: a small output (decode rows, <= 64 KB) is written by the
+    // kernel straight into pinned host memory; a larger one goes by DMA.
     float *dy = static_cast<float *>(s.dy);
+    const bool y_direct = yb <= 65536;
+    if (y_direct) {
+        void *hy_dev = nullptr;
+        HIP_OK(hipHostGetDevicePointer(&hy_dev, s.hy, 0), "hipHostGetDevicePointer");
+        dy = static_cast<float *>(hy_dev);
+    }
     if (type == QK_TYPE_Q8_0) {
         HIP_OK(qk::launch_quantize_q8_0(dx, n_tok * (k / QK8_0), dxq, s.stream), "quantize");
         // tensor_matmul_q8_0_f32 has no batched form: up to 16 tokens per launch.
@@ -495,7 +503,8 @@ int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f, int64_t k, c
                    "gemm launch");
         }
     }
-    HIP_OK(hipMemcpyAsync(s.hy, dy, yb, hipMemcpyDeviceToHost, s.stream), "hipMemcpyAsync(out)");
+    if (!y_direct)
+        HIP_OK(hipMemcpyAsync(s.hy, dy, yb, hipMemcpyDeviceToHost, s.stream), "hipMemcpyAsync(out)");
     HIP_OK(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
     std::memcpy(out, s.hy, yb);
     return QK_OK;
