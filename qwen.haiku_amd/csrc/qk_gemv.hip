@@ -225,7 +225,7 @@ __device__ __forceinline__ void read_sb(Raw<14> &r, const uint8_t *wb, int off, 
 __device__ __forceinline__ uint32_t bl32(__amdgpu_buffer_rsrc_t r, int off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
-__device__ __forceinline__ uint4 bl128a(__amdgpu_buffer_rsrc_t r, int off) {   // 4-byte aligned
+__device__ __forceinline__ uint4 bl128(__amdgpu_buffer_rsrc_t r, int off) {    // 4-byte aligned offset
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
@@ -233,10 +233,10 @@ __device__ __forceinline__ uint4 bl128a(__amdgpu_buffer_rsrc_t r, int off) {   /
 struct ActK { uint4 a0, a1, a2, a3; uint32_t bs0, bs1; float d; };
 __device__ __forceinline__ void load_act(ActK &x, __amdgpu_buffer_rsrc_t r, int b, int j) {
     const int o = b * Q8K_BYTES;
-    x.a0 = bl128a(r, o + 4 + 64 * j);
-    x.a1 = bl128a(r, o + 20 + 64 * j);
-    x.a2 = bl128a(r, o + 36 + 64 * j);
-    x.a3 = bl128a(r, o + 52 + 64 * j);
+    x.a0 = bl128(r, o + 4 + 64 * j);
+    x.a1 = bl128(r, o + 20 + 64 * j);
+    x.a2 = bl128(r, o + 36 + 64 * j);
+    x.a3 = bl128(r, o + 52 + 64 * j);
     x.bs0 = bl32(r, o + 260 + 8 * j);
     x.bs1 = bl32(r, o + 264 + 8 * j);
     x.d = __uint_as_float(bl32(r, o));
@@ -246,10 +246,10 @@ __device__ __forceinline__ void load_act(ActK &x, __amdgpu_buffer_rsrc_t r, int 
 struct Act6 { uint4 a0, a1, a4, a5; uint32_t bl, bh; float d; };
 __device__ __forceinline__ void load_act(Act6 &x, __amdgpu_buffer_rsrc_t r, int b, int j) {
     const int o = b * Q8K_BYTES, s = 8 * (j >> 1) + 2 * (j & 1);
-    x.a0 = bl128a(r, o + 4 + 16 * s);
-    x.a1 = bl128a(r, o + 20 + 16 * s);
-    x.a4 = bl128a(r, o + 68 + 16 * s);
-    x.a5 = bl128a(r, o + 84 + 16 * s);
+    x.a0 = bl128(r, o + 4 + 16 * s);
+    x.a1 = bl128(r, o + 20 + 16 * s);
+    x.a4 = bl128(r, o + 68 + 16 * s);
+    x.a5 = bl128(r, o + 84 + 16 * s);
     x.bl = bl32(r, o + 260 + 2 * s);
     x.bh = bl32(r, o + 268 + 2 * s);
     x.d = __uint_as_float(bl32(r, o));
@@ -505,10 +505,6 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
 // Q4_K / Q5_K: the same tiles and gather as run_kq, with each lane's block
 // fields loaded straight into registers (buffer loads, range-checked by
 // the item).
-__device__ __forceinline__ uint4 bl128(__amdgpu_buffer_rsrc_t r, int off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-    return make_uint4(v[0], v[1], v[2], v[3]);
-}
 __device__ __forceinline__ void load_direct(Raw<12> &r, __amdgpu_buffer_rsrc_t rs, int off, int j) {
     r.hdr = bl128(rs, off);
     r.q0 = bl128(rs, off + 16 + 32 * j);
