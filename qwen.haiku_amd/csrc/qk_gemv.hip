@@ -373,8 +373,9 @@ __device__ __forceinline__ uint64_t argkey(float v, int64_t row) {
 // The P super-block terms of a row, from the first lane of each of its P
 // four-lane groups, into the row's first lane (the only lane that adds
 // and stores them, in order). P = 4: the groups sit 4 lanes apart in one
-// 16-lane row, so DPP row_shl moves them; wider rows cross DPP rows and
-// use ds_bpermute.
+// 16-lane row, so DPP row_shl moves them. P = 16 (one row per wave):
+// row_shl inside each 16-lane row, then the four rows' first lanes read
+// as uniform values. P = 8 (two rows per wave) uses ds_bpermute.
 template <int P>
 __device__ __forceinline__ void gather_terms(float (&tg)[P], float t, int src0) {
     if constexpr (P == 4) {
@@ -382,6 +383,20 @@ __device__ __forceinline__ void gather_terms(float (&tg)[P], float t, int src0) 
         tg[1] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x104, 0xF, 0xF, true));
         tg[2] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x108, 0xF, 0xF, true));
         tg[3] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x10C, 0xF, 0xF, true));
+    } else if constexpr (P == 16) {
+        // one row per wave: each 16-lane DPP row gathers its four groups
+        // into its first lane, which the wave then reads as uniform values
+        const int v0 = __float_as_int(t);
+        const int v1 = __builtin_amdgcn_mov_dpp(v0, 0x104, 0xF, 0xF, true);
+        const int v2 = __builtin_amdgcn_mov_dpp(v0, 0x108, 0xF, 0xF, true);
+        const int v3 = __builtin_amdgcn_mov_dpp(v0, 0x10C, 0xF, 0xF, true);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            tg[4 * r + 0] = __int_as_float(__builtin_amdgcn_readlane(v0, 16 * r));
+            tg[4 * r + 1] = __int_as_float(__builtin_amdgcn_readlane(v1, 16 * r));
+            tg[4 * r + 2] = __int_as_float(__builtin_amdgcn_readlane(v2, 16 * r));
+            tg[4 * r + 3] = __int_as_float(__builtin_amdgcn_readlane(v3, 16 * r));
+        }
     } else {
 #pragma unroll
         for (int g2 = 0; g2 < P; g2++) tg[g2] = __shfl(t, src0 + 4 * g2);
