@@ -178,11 +178,10 @@ __device__ __forceinline__ float kterm(float yd, uint32_t xd, uint32_t xdmin, in
 
 // AVX2/VNNI return the row sum through an 8-lane broadcast:
 // hsum(8 x s) / 8 (simd/avx.c:231-240), which is s unless 8s overflows.
+// The three doublings of the sum are exact unless they overflow, and so
+// is s * 8, at the same exponent: both give 8s or the same infinity.
 __device__ __forceinline__ float bcast8(float s) {
-    const float s2 = __fadd_rn(s, s);
-    const float s4 = __fadd_rn(s2, s2);
-    const float s8 = __fadd_rn(s4, s4);
-    return __fmul_rn(s8, 0.125f);      // x / 8 and x * 2^-3 round the same exact value
+    return __fmul_rn(__fmul_rn(s, 8.0f), 0.125f);   // x / 8 and x * 2^-3 round the same exact value
 }
 
 // Q6_K term (all tiers, simd/quants.h:399): rn(rn(fp16(x.d)*y.d) * (float)v).

@@ -72,8 +72,8 @@ __device__ __forceinline__ void stage_q80(const uint8_t *__restrict__ xq, int nb
 #define M4 0x0F0F0F0Fu
 
 __device__ __forceinline__ int32_t dot16(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
-                                         const uint4 a) {
-    int32_t s = dot4(w0, a.x, 0);
+                                         const uint4 a, int32_t c) {
+    int32_t s = dot4(w0, a.x, c);
     s = dot4(w1, a.y, s);
     s = dot4(w2, a.z, s);
     return dot4(w3, a.w, s);
@@ -144,6 +144,20 @@ __device__ __forceinline__ void chunk_load(ChunkN<NL> &c, const Span &sp, int la
             const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16, u * 1024, 0);
             c.v[u] = make_uint4(v[0], v[1], v[2], v[3]);
         }
+    }
+}
+
+// Every load issued, whatever the item's length (pieces past it read
+// zeros), so the wait counts of a loop that keeps two items in flight are
+// known at compile time.
+template <int NL>
+__device__ __forceinline__ void chunk_load_all(ChunkN<NL> &c, const Span &sp, int lane) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(sp.base), 0, sp.npc * 16, 0x00020000);
+#pragma unroll
+    for (int u = 0; u < NL; u++) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16, u * 1024, 0);
+        c.v[u] = make_uint4(v[0], v[1], v[2], v[3]);
     }
 }
 
@@ -296,12 +310,14 @@ template <bool FUSED>
 __device__ __forceinline__ float term_sb(const Raw<13> &r, const ActK &x, int j) {
     const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
     const uint32_t qh[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
-    const uint32_t s0 = 2 * j, s1 = 2 * j + 1;
+    // rotations that bring bit 2j (2j+1) of every byte to its bit 4, where
+    // the fifth bit belongs; the bit moves by at most 3, inside its byte
+    const uint32_t r0 = (uint32_t)(2 * j - 4) & 31u, r1 = (uint32_t)(2 * j - 3) & 31u;
     uint32_t lo[8], hi[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        lo[i] = (q[i] & M4) | (((qh[i] >> s0) & 0x01010101u) << 4);
-        hi[i] = ((q[i] >> 4) & M4) | (((qh[i] >> s1) & 0x01010101u) << 4);
+        lo[i] = (q[i] & M4) | (__builtin_amdgcn_alignbit(qh[i], qh[i], r0) & 0x10101010u);
+        hi[i] = ((q[i] >> 4) & M4) | (__builtin_amdgcn_alignbit(qh[i], qh[i], r1) & 0x10101010u);
     }
     const int32_t slo = dot32r(lo, x.a0, x.a1), shi = dot32r(hi, x.a2, x.a3);
     int32_t sc0, m0, sc1, m1;
@@ -311,29 +327,34 @@ __device__ __forceinline__ float term_sb(const Raw<13> &r, const ActK &x, int j)
     return kterm<FUSED>(x.d, r.hdr.x & 0xffffu, r.hdr.x >> 16, isum, mins);
 }
 // Q6_K: the lane's share of isum - 32*isum_mins over sub-blocks s, s+1,
-// s+4, s+5 (see read_sb), exact in int32.
+// s+4, s+5 (see read_sb), exact in int32. Each sub-block's dot chain
+// starts from -32*bsum, so it yields sum((q - 32) * a) directly; the seed
+// depends on the activations only and is formed once per wave when they
+// stay put. |chain| < 2^18 fits the 24-bit multiply.
 template <bool FUSED>
 __device__ __forceinline__ float term_sb(const Raw<14> &r, const Act6 &x, int j) {
     const int qq = j & 1;
-    const uint32_t sh = r.sh, sa = 2 * qq;
+    const uint32_t sh = r.sh, sb = 8 * sh + 2 * qq;
     uint32_t lo[8], hi[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const uint32_t ql = __builtin_amdgcn_alignbyte(r.l[i + 1], r.l[i], sh);
-        const uint32_t qh = __builtin_amdgcn_alignbyte(r.h[i + 1], r.h[i], sh) >> sa;
-        lo[i] = (ql & M4) | ((qh << 4) & 0x30303030u);
-        hi[i] = ((ql >> 4) & M4) | (qh & 0x30303030u);
+        // one funnel shift aligns the qh bytes and brings the lane's bit
+        // pairs to bits 0-1 (low nibble's) and 4-5 (high nibble's) of
+        // each byte; the mask drops the bits shifted in from the next byte
+        const uint32_t qh = __builtin_amdgcn_alignbit(r.h[i + 1], r.h[i], sb) & 0x33333333u;
+        lo[i] = (ql & M4) | ((qh << 4) & ~M4);
+        hi[i] = ((ql >> 4) & M4) | (qh & ~M4);
     }
-    const int32_t d0 = dot16(lo[0], lo[1], lo[2], lo[3], x.a0);
-    const int32_t d1 = dot16(lo[4], lo[5], lo[6], lo[7], x.a1);
-    const int32_t d4 = dot16(hi[0], hi[1], hi[2], hi[3], x.a4);
-    const int32_t d5 = dot16(hi[4], hi[5], hi[6], hi[7], x.a5);
-    const int32_t sc0 = (int32_t)(int8_t)(r.sc & 0xffu), sc1 = (int32_t)(int8_t)(r.sc >> 8);
-    const int32_t sc4 = (int32_t)(int8_t)(r.sc2 & 0xffu), sc5 = (int32_t)(int8_t)(r.sc2 >> 8);
     const int32_t b0 = (int16_t)(x.bl & 0xffffu), b1 = (int16_t)(x.bl >> 16);
     const int32_t b4 = (int16_t)(x.bh & 0xffffu), b5 = (int16_t)(x.bh >> 16);
-    const int32_t v = __mul24(d0, sc0) + __mul24(d1, sc1) + __mul24(d4, sc4) + __mul24(d5, sc5) -
-                      32 * (__mul24(b0, sc0) + __mul24(b1, sc1) + __mul24(b4, sc4) + __mul24(b5, sc5));
+    const int32_t d0 = dot16(lo[0], lo[1], lo[2], lo[3], x.a0, -32 * b0);
+    const int32_t d1 = dot16(lo[4], lo[5], lo[6], lo[7], x.a1, -32 * b1);
+    const int32_t d4 = dot16(hi[0], hi[1], hi[2], hi[3], x.a4, -32 * b4);
+    const int32_t d5 = dot16(hi[4], hi[5], hi[6], hi[7], x.a5, -32 * b5);
+    const int32_t sc0 = (int32_t)(int8_t)(r.sc & 0xffu), sc1 = (int32_t)(int8_t)(r.sc >> 8);
+    const int32_t sc4 = (int32_t)(int8_t)(r.sc2 & 0xffu), sc5 = (int32_t)(int8_t)(r.sc2 >> 8);
+    const int32_t v = __mul24(d0, sc0) + __mul24(d1, sc1) + __mul24(d4, sc4) + __mul24(d5, sc5);
     const int32_t tot = sum4(v);
     return q6term(x.d, r.d, tot);
 }
@@ -413,7 +434,13 @@ __device__ __forceinline__ void gather_terms(float (&tg)[P], float t, int src0) 
 // i+1's loads are issued before item i is reduced; the activation
 // operands' loads go out before the first item's. Item offsets are
 // 32-bit: the API limits a matrix to 4 GB.
-template <int TYPE, int LP, bool FUSED>
+//
+// LM (the LM-head kernel, which has registers to spare at its 4 waves per
+// SIMD): waves of many one-item rows alternate two register sets, so the
+// loads of the next item are in flight while the wave waits for the
+// current one's. The general loop must instead wait for all loads before
+// it moves the look-ahead registers into place.
+template <int TYPE, int LP, bool FUSED, bool LM>
 __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best, bool keys) {
     constexpr int BB = TYPE == 12 ? Q4K_BYTES : (TYPE == 13 ? Q5K_BYTES : Q6K_BYTES);
     constexpr int P = 1 << LP;
@@ -463,6 +490,18 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
     if (nit == niter) { nit = 0; ntile += nwg; }
     Span nsp = span(ntile, nit);                       // computed while the loads are in flight
     float sum = 0.0f;
+    // Argmax keys: each storing lane keeps its first-index maximum as a
+    // value and a row, and forms the 64-bit key once at the end. Its rows
+    // ascend, so only a strictly larger value replaces the one held; bv
+    // starts as NaN (no row yet) and a NaN row is never taken.
+    float bv = __int_as_float(0x7fc00000);
+    int brow = -1;
+    auto finish = [&]() __attribute__((always_inline)) {
+        if (keys && brow >= 0) {
+            const uint64_t k = argkey(bv, brow);
+            best = k > best ? k : best;
+        }
+    };
     // item (tile, it) from registers c (range sp): through the window, the
     // term, gathered into the row's first lane, which stores the row after
     // its last item
@@ -470,28 +509,32 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
         chunk_store(c, wb, sp, lane);
         wave_sync();
         // Lanes of a block past the row end or of a row past n compute a
-        // term from in-range LDS bytes that is never added or stored.
+        // term from in-range LDS bytes that is replaced by +0.0 or never
+        // stored.
         Raw<TYPE> r;
         read_sb(r, wb, sp.ofs + lofs, j);
         if (it != xit) {                               // rows of several items: next super-blocks
             load_act(xa, ar, it * P + g, j);
             xit = it;
         }
-        const float t = term_sb<FUSED>(r, xa, j);
+        // A group past the row end contributes +0.0: the sum starts at
+        // +0.0 and can never become -0.0, so adding +0.0 leaves it as is.
+        const int lim = (nb - it * P < P) ? nb - it * P : P;
+        const float t0 = term_sb<FUSED>(r, xa, j);
+        const float t = g < lim ? t0 : 0.0f;
         float tg[P];
         gather_terms<P>(tg, t, src0);
-        const int lim = (nb - it * P < P) ? nb - it * P : P;
 #pragma unroll
-        for (int g2 = 0; g2 < P; g2++)
-            if (g2 < lim) sum += tg[g2];
+        for (int g2 = 0; g2 < P; g2++) sum += tg[g2];
         if (it == niter - 1) {
             const int row = tile * (4 * RPW) + wave * RPW + team;
             if (FUSED) sum = bcast8(sum);
             if (row < n && g == 0 && j == 0) {
                 *(QK_GLOBAL float *)(y + row) = sum;
                 if (keys) {
-                    const uint64_t k = argkey(sum, row);
-                    best = k > best ? k : best;
+                    const bool take = !(sum <= bv) && sum == sum;
+                    bv = take ? sum : bv;
+                    brow = take ? row : brow;
                 }
             }
             sum = 0.0f;
@@ -500,7 +543,31 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
     };
     if (ntile >= ntiles) {                             // one item (a decode launch): no look-ahead
         item(cur, sp, tile, it);
+        finish();
         return;
+    }
+    if constexpr (LM) {
+        if (niter == 1) {
+            Chunk nxt;
+            while (true) {
+                chunk_load_all(nxt, nsp, lane);        // past the last tile: zeros, never stored
+                item(cur, sp, tile, 0);
+                sp = nsp;
+                tile = ntile;
+                ntile += nwg;
+                nsp = span(ntile, 0);
+                if (tile >= ntiles) break;
+                chunk_load_all(cur, nsp, lane);
+                item(nxt, sp, tile, 0);
+                sp = nsp;
+                tile = ntile;
+                ntile += nwg;
+                nsp = span(ntile, 0);
+                if (tile >= ntiles) break;
+            }
+            finish();
+            return;
+        }
     }
     while (tile < ntiles) {
         Chunk nxt;
@@ -515,6 +582,7 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
         if (nit == niter) { nit = 0; ntile += nwg; }
         nsp = span(ntile, nit);
     }
+    finish();
 }
 
 // Q4_K / Q5_K: the same tiles and gather as run_kq, with each lane's block
@@ -581,13 +649,14 @@ __device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t
             load_act(xa, ar, it * P + g, j);
             xit = it;
         }
-        const float t = term_sb<FUSED>(c, xa, j);
+        // a group past the row end contributes +0.0 (as in run_kq)
+        const int lim = (nb - it * P < P) ? nb - it * P : P;
+        const float t0 = term_sb<FUSED>(c, xa, j);
+        const float t = g < lim ? t0 : 0.0f;
         float tg[P];
         gather_terms<P>(tg, t, src0);
-        const int lim = (nb - it * P < P) ? nb - it * P : P;
 #pragma unroll
-        for (int g2 = 0; g2 < P; g2++)
-            if (g2 < lim) sum += tg[g2];
+        for (int g2 = 0; g2 < P; g2++) sum += tg[g2];
         if (it == niter - 1) {
             const int row = tile * (4 * RPW) + wave * RPW + team;
             if (FUSED) sum = bcast8(sum);
@@ -882,8 +951,11 @@ __device__ __forceinline__ void run_q80r(const KDesc &D, int lw, int nwg, uint8_
 // per descriptor passed.
 __device__ __forceinline__ int wg0_of(uint32_t t, int hi) { return (int)(hi ? t >> 16 : t & 0xffffu); }
 
-template <bool FUSED>
-__global__ __launch_bounds__(256, 5) void k_gemv(uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3,
+// LM: the LM-head instantiation (one Q6_K matrix, many items per wave),
+// allowed 128 VGPRs for its two register sets; decode launches keep the
+// 5-wave bound.
+template <bool FUSED, bool LM>
+__global__ __launch_bounds__(256, LM ? 4 : 5) void k_gemv(uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3,
                                               uint32_t t4, uint32_t t5, uint32_t t6, uint32_t t7,
                                               KArgs args, uint64_t *__restrict__ amax_partial,
                                               uint32_t *__restrict__ zero_ctr) {
@@ -918,9 +990,9 @@ __global__ __launch_bounds__(256, 5) void k_gemv(uint32_t t0, uint32_t t1, uint3
             else run_kqd<13, 4, FUSED>(D, lw, D.nwg, lds, best, keys);
             break;
         case 14:
-            if (D.p == 4) run_kq<14, 2, FUSED>(D, lw, D.nwg, lds, best, keys);
-            else if (D.p == 8) run_kq<14, 3, FUSED>(D, lw, D.nwg, lds, best, keys);
-            else run_kq<14, 4, FUSED>(D, lw, D.nwg, lds, best, keys);
+            if (D.p == 4) run_kq<14, 2, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
+            else if (D.p == 8) run_kq<14, 3, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
+            else run_kq<14, 4, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
             break;
         default:
             if (D.p == 4 && D.nb == 32) run_q80r<32, FUSED>(D, lw, D.nwg, lds, best, keys);
@@ -1025,12 +1097,11 @@ static hipError_t launch_gemv_impl(GemvArgs &a, int max_wg_per_desc, uint64_t *a
     }
     a.lds_bytes = lds;
     if (grid_out) *grid_out = wg;
-    if (a.fused)
-        hipLaunchKernelGGL(k_gemv<true>, dim3(wg), dim3(256), lds, s, tab[0], tab[1], tab[2], tab[3], tab[4],
-                           tab[5], tab[6], tab[7], ka, amax_partial, zero_ctr);
-    else
-        hipLaunchKernelGGL(k_gemv<false>, dim3(wg), dim3(256), lds, s, tab[0], tab[1], tab[2], tab[3], tab[4],
-                           tab[5], tab[6], tab[7], ka, amax_partial, zero_ctr);
+    // the LM head (argmax keys wanted) runs the LM instantiation
+    auto kern = amax_partial ? (a.fused ? k_gemv<true, true> : k_gemv<false, true>)
+                             : (a.fused ? k_gemv<true, false> : k_gemv<false, false>);
+    hipLaunchKernelGGL(kern, dim3(wg), dim3(256), lds, s, tab[0], tab[1], tab[2], tab[3], tab[4], tab[5], tab[6],
+                       tab[7], ka, amax_partial, zero_ctr);
     return hipGetLastError();
 }
 
