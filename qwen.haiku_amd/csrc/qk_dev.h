@@ -139,6 +139,16 @@ __device__ __forceinline__ uint32_t ld_u8(const uint8_t *p) {
     return *(const QK_GLOBAL uint8_t *)(p);
 }
 
+// Buffer loads: offsets past the resource's byte range read zeros without
+// a memory access, so a load needs no per-lane guard.
+__device__ __forceinline__ uint32_t bl32(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint4 bl128(__amdgpu_buffer_rsrc_t r, int off) {    // 4-byte aligned offset
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 // ---- Q4_K / Q5_K 6-bit scale and min of sub-block s (0..7) from the
 // 12 packed bytes held in three dwords (q4k_get_scale_min,
 // simd/quants.h:215-224).

@@ -88,19 +88,19 @@ __device__ __forceinline__ void lds_st16(void *p, uint32_t a, uint32_t b, uint32
 // q = tid%4 of it, so all of a thread's loads in a step are immediate
 // offsets from one row pointer computed once per kernel.
 
-// Activations: the thread holds dwords q, q+4, ..., q+72 (those < 73) of
-// its token's 292-byte Q8_K block (d | 64 dwords of qs | 8 dwords of
-// bsums).
-struct ActRaw { uint32_t v[19]; };
+// Activations: quarter q of a token holds qs[64q, 64q+64) of its 292-byte
+// Q8_K block (d | qs[256] | bsums[16]) as four 16-byte loads at 4-byte
+// aligned offsets, bsum pairs 2q and 2q+1, and d. The buffer covers the
+// workgroup's tokens, so rows past m read zeros.
+struct ActRaw { uint4 q[4]; uint32_t b0, b1, d; };
 
-__device__ __forceinline__ void load_act(ActRaw &a, const uint8_t *row, int q, int i) {
+__device__ __forceinline__ void load_act(ActRaw &a, __amdgpu_buffer_rsrc_t r, int row_off, int q, int i) {
+    const int o = row_off + i * Q8K_BYTES;
 #pragma unroll
-    for (int j = 0; j < 19; j++) a.v[j] = 0;
-    if (!row) return;
-    const uint8_t *p = row + (int64_t)i * Q8K_BYTES;
-#pragma unroll
-    for (int j = 0; j < 18; j++) a.v[j] = ld32(p + 16 * j);
-    if (q == 0) a.v[18] = ld32(p + 288);
+    for (int j = 0; j < 4; j++) a.q[j] = bl128(r, o + 4 + 64 * q + 16 * j);
+    a.b0 = bl32(r, o + 260 + 8 * q);
+    a.b1 = bl32(r, o + 264 + 8 * q);
+    a.d = bl32(r, o);
 }
 
 // bsum pair j (bsums[2j] + bsums[2j+1], one dword of the block) as two
@@ -114,19 +114,11 @@ __device__ __forceinline__ void store_pair(GL &s, int t, int j, uint32_t v) {
 
 template <typename GL>
 __device__ __forceinline__ void store_act(GL &s, const ActRaw &a, int t, int q) {
-    // dword r = q + 4j: r = 0 is d, 1..64 the quants, 65..72 the bsums
-    if (q == 0) s.yd[t] = __uint_as_float(a.v[0]);
-    else *(QK_LDS uint32_t *)&s.a[t][4 * q - 4] = a.v[0];
 #pragma unroll
-    for (int j = 1; j < 16; j++) *(QK_LDS uint32_t *)&s.a[t][4 * q + 16 * j - 4] = a.v[j];
-    if (q == 0) {
-        *(QK_LDS uint32_t *)&s.a[t][252] = a.v[16];
-        store_pair(s, t, 3, a.v[17]);
-        store_pair(s, t, 7, a.v[18]);
-    } else {
-        store_pair(s, t, q - 1, a.v[16]);
-        store_pair(s, t, 3 + q, a.v[17]);
-    }
+    for (int j = 0; j < 4; j++) *(QK_LDS uint4 *)&s.a[t][64 * q + 16 * j] = a.q[j];   // rows: 16-byte aligned
+    store_pair(s, t, 2 * q, a.b0);
+    store_pair(s, t, 2 * q + 1, a.b1);
+    if (q == 0) s.yd[t] = __uint_as_float(a.d);
 }
 
 // Mins, d and dmin of a Q4_K / Q5_K header (d | dmin | scales[12]).
@@ -376,7 +368,12 @@ void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb, const uint8_t *__r
     // weight rows, the rest (BN = 32) nothing; row st of the tile, quarter sq
     const int role = threadIdx.x < 256 ? 0 : (threadIdx.x < 256 + 4 * BN ? 1 : 2);
     const int st = (threadIdx.x & 255) >> 2, sq = threadIdx.x & 3;
-    const uint8_t *xrow = (role == 0 && t0 + st < m) ? xq + (t0 + st) * nb * Q8K_BYTES + 4 * sq : nullptr;
+    // activation rows of this token tile: one buffer of at most 64 x 64 x
+    // 292 bytes, so every offset is 32-bit
+    const int mrows = (m - t0 < GM_BM) ? (int)(m - t0) : GM_BM;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(xq + t0 * nb * Q8K_BYTES), 0, mrows * nb * Q8K_BYTES, 0x00020000);
+    const int xoff = st * nb * Q8K_BYTES;
     const uint8_t *wrow = (role == 1 && r0 + st < n) ? w + (r0 + st) * nb * BB : nullptr;
 
     const int8_t *arow = &s.a[tm + col][0];
@@ -389,7 +386,7 @@ void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb, const uint8_t *__r
 #pragma unroll
         for (int v = 0; v < VPW; v++) sum[v] = 0.0f;
         if constexpr (R == 1) load_w(raw, wrow, sq, 0);
-        if constexpr (R == 0) load_act(raw, xrow, sq, 0);
+        if constexpr (R == 0) load_act(raw, xr, xoff, sq, 0);
 
         for (int i = 0; i < nb; i++) {
             lds_barrier();                                       // previous super-block's reads done
@@ -397,7 +394,7 @@ void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb, const uint8_t *__r
             if constexpr (R == 0) store_act(s, raw, st, sq);
             if (i + 1 < nb) {                                    // next super-block in flight during compute
                 if constexpr (R == 1) load_w(raw, wrow, sq, i + 1);
-                if constexpr (R == 0) load_act(raw, xrow, sq, i + 1);
+                if constexpr (R == 0) load_act(raw, xr, xoff, sq, i + 1);
             }
             lds_barrier();
 

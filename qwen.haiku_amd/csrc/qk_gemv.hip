@@ -236,13 +236,6 @@ __device__ __forceinline__ void read_sb(Raw<14> &r, const uint8_t *wb, int off, 
 // buffer loads (a lane of a super-block past the row end reads zeros and
 // its term is never added). Every workgroup reads the same row, so these
 // loads hit the L2 after the first.
-__device__ __forceinline__ uint32_t bl32(__amdgpu_buffer_rsrc_t r, int off) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-}
-__device__ __forceinline__ uint4 bl128(__amdgpu_buffer_rsrc_t r, int off) {    // 4-byte aligned offset
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-    return make_uint4(v[0], v[1], v[2], v[3]);
-}
 // Q4_K / Q5_K lane j: qs[64j, 64j+64), bsums 4j..4j+3 (pairs 2j, 2j+1), d.
 struct ActK { uint4 a0, a1, a2, a3; uint32_t bs0, bs1; float d; };
 __device__ __forceinline__ void load_act(ActK &x, __amdgpu_buffer_rsrc_t r, int b, int j) {
