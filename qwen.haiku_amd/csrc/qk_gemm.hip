@@ -258,16 +258,37 @@ __device__ __forceinline__ uint32_t u6_minus_32(uint32_t x) {
 // 2 bits of qh[32h + l] at 2qq, minus 32. Quarter q covers positions
 // l0..l0+15 (l0 = 16(q&1)) of all four quarters of half h = q/2, read as
 // three 16-byte runs, each through the five aligned dwords that contain
-// it (the last ends at most at byte 196 of the block); quarter 0 also
-// reads the scales (eight 2-byte words) and d.
-struct WRaw14 { uint32_t v[15]; uint32_t sc[8]; uint32_t d, sh; };
+// it (a 16-byte and a 4-byte load; the last ends at most at byte 196 of
+// the block); quarter 0 also reads the 16 scale bytes the same way and d.
+// The buffer starts at the 4-byte aligned address at or below the tile's
+// first row and ends with its last row, so offsets are 32-bit, every
+// aligned load stays inside it, and rows past n read zeros.
+struct WRaw14 { uint32_t v[15]; uint4 sc; uint32_t sc4, d, sh; };
 
+__device__ __forceinline__ void load_w(WRaw14 &a, __amdgpu_buffer_rsrc_t r, int row_off, int q, int i) {
+    const int b = row_off + i * Q6K_BYTES;             // block start; the base is 4-byte aligned
+    const int h = q >> 1, l0 = 16 * (q & 1);
+    const int sh = b & 3;
+    a.sh = (uint32_t)sh;
+    const int p0 = b - sh + 64 * h + l0, p2 = b - sh + 128 + 32 * h + l0;
+    const uint4 x0 = bl128(r, p0), x1 = bl128(r, p0 + 32), x2 = bl128(r, p2);
+    a.v[0] = x0.x, a.v[1] = x0.y, a.v[2] = x0.z, a.v[3] = x0.w, a.v[4] = bl32(r, p0 + 16);
+    a.v[5] = x1.x, a.v[6] = x1.y, a.v[7] = x1.z, a.v[8] = x1.w, a.v[9] = bl32(r, p0 + 48);
+    a.v[10] = x2.x, a.v[11] = x2.y, a.v[12] = x2.z, a.v[13] = x2.w, a.v[14] = bl32(r, p2 + 16);
+    // every quarter loads them (one wave-wide load each); quarter 0 stores them
+    a.sc = bl128(r, b - sh + 192);
+    a.sc4 = bl32(r, b - sh + 208);                     // needed only when sh > 0, then inside the block
+    a.d = __builtin_amdgcn_raw_buffer_load_b16(r, b + 208, 0, 0);
+}
+
+// The same registers from plain loads (64-row tiles, where the wider loads
+// above push the kernel past its register budget). The fifth scale dword
+// is read only when sh > 0, so no load passes the block's end.
 __device__ __forceinline__ void load_w(WRaw14 &a, const uint8_t *row, int q, int i) {
 #pragma unroll
     for (int j = 0; j < 15; j++) a.v[j] = 0;
-#pragma unroll
-    for (int j = 0; j < 8; j++) a.sc[j] = 0;
-    a.d = a.sh = 0;
+    a.sc = make_uint4(0, 0, 0, 0);
+    a.sc4 = a.d = a.sh = 0;
     if (!row) return;
     const uint8_t *blk = row + (int64_t)i * Q6K_BYTES;
     const int h = q >> 1, l0 = 16 * (q & 1);
@@ -281,24 +302,24 @@ __device__ __forceinline__ void load_w(WRaw14 &a, const uint8_t *row, int q, int
         a.v[10 + j] = ld32(p2 + 4 * j);
     }
     if (q == 0) {
-#pragma unroll
-        for (int j = 0; j < 8; j++) a.sc[j] = ld_u16(blk + 192 + 2 * j);
+        const uint8_t *ps = blk - sh + 192;
+        a.sc = make_uint4(ld32(ps), ld32(ps + 4), ld32(ps + 8), ld32(ps + 12));
+        if (sh) a.sc4 = ld32(ps + 16);
         a.d = ld_u16(blk + 208);
     }
 }
 
 template <typename GL>
 __device__ __forceinline__ void store_w(GL &s, const WRaw14 &a, int r, int q) {
+    const uint32_t sh = a.sh;
     if (q == 0) {
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            s.sc[r][2 * j] = (int8_t)(a.sc[j] & 0xffu);
-            s.sc[r][2 * j + 1] = (int8_t)(a.sc[j] >> 8);
-        }
+        *(QK_LDS uint4 *)&s.sc[r][0] = make_uint4(__builtin_amdgcn_alignbyte(a.sc.y, a.sc.x, sh),
+                                                  __builtin_amdgcn_alignbyte(a.sc.z, a.sc.y, sh),
+                                                  __builtin_amdgcn_alignbyte(a.sc.w, a.sc.z, sh),
+                                                  __builtin_amdgcn_alignbyte(a.sc4, a.sc.w, sh));
         s.wd[r] = h2f(a.d);
     }
     const int h = q >> 1, l0 = 16 * (q & 1);
-    const uint32_t sh = a.sh;
     uint32_t qa[4], qb[4], hh[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -375,6 +396,13 @@ void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb, const uint8_t *__r
         const_cast<uint8_t *>(xq + t0 * nb * Q8K_BYTES), 0, mrows * nb * Q8K_BYTES, 0x00020000);
     const int xoff = st * nb * Q8K_BYTES;
     const uint8_t *wrow = (role == 1 && r0 + st < n) ? w + (r0 + st) * nb * BB : nullptr;
+    // Q6_K weight rows of this tile as one buffer (see load_w)
+    const uint8_t *wtile = w + r0 * nb * BB;
+    const int wmis = (int)(reinterpret_cast<uintptr_t>(wtile) & 3u);
+    const int nrows = (n - r0 < BN) ? (int)(n - r0) : BN;
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(wtile - wmis), 0, wmis + nrows * nb * BB, 0x00020000);
+    const int woff = wmis + st * nb * BB;
 
     const int8_t *arow = &s.a[tm + col][0];
     const v16i zero = {0};
@@ -385,7 +413,10 @@ void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb, const uint8_t *__r
         float sum[VPW];
 #pragma unroll
         for (int v = 0; v < VPW; v++) sum[v] = 0.0f;
-        if constexpr (R == 1) load_w(raw, wrow, sq, 0);
+        if constexpr (R == 1) {
+            if constexpr (TYPE == 14 && BN == 32) load_w(raw, wr, woff, sq, 0);
+            else load_w(raw, wrow, sq, 0);
+        }
         if constexpr (R == 0) load_act(raw, xr, xoff, sq, 0);
 
         for (int i = 0; i < nb; i++) {
@@ -393,7 +424,10 @@ void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb, const uint8_t *__r
             if constexpr (R == 1) store_w(s, raw, st, sq);
             if constexpr (R == 0) store_act(s, raw, st, sq);
             if (i + 1 < nb) {                                    // next super-block in flight during compute
-                if constexpr (R == 1) load_w(raw, wrow, sq, i + 1);
+                if constexpr (R == 1) {
+                    if constexpr (TYPE == 14 && BN == 32) load_w(raw, wr, woff, sq, i + 1);
+                    else load_w(raw, wrow, sq, i + 1);
+                }
                 if constexpr (R == 0) load_act(raw, xr, xoff, sq, i + 1);
             }
             lds_barrier();
