@@ -170,8 +170,14 @@ def test_matmul_gemm_m2048(lib, orc):
 # Group sizes of the top-k bound (maxima of 1, 4 or 16 GEMV workgroups):
 # k <= 64 of 1024 maxima uses 16, (248320, 256) and (31040, 100) use 4,
 # (5000, 256) uses 1, (300, 200) has fewer maxima than k (no bound).
+# Past 1024 tiles the LM-head waves run several items with two register
+# sets in turn: (16400, 1024) has 1025 tiles; (100003, 2048), (50001,
+# 4096) and (262147, 256) have rows of 8, 16 and 4 groups (the last with
+# three groups past the row end) and a partial last tile.
 @pytest.mark.parametrize("n,k,topk", [(248320, 1024, 40), (31040, 1024, 40), (5000, 512, 256), (77, 256, 1),
-                                      (300, 256, 200), (9000, 256, 64), (248320, 1024, 256), (31040, 1024, 100)])
+                                      (300, 256, 200), (9000, 256, 64), (248320, 1024, 256), (31040, 1024, 100),
+                                      (16400, 1024, 40), (100003, 2048, 40), (50001, 4096, 10),
+                                      (262147, 256, 40)])
 def test_lmhead_argmax_topk(lib, orc, n, k, topk):
     step(f"lmhead n={n} k={k} topk={topk}")
     w = synth.blocks(14, n, k, seed=2)
