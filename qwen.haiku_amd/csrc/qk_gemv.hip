@@ -1117,8 +1117,11 @@ hipError_t launch_gemv(GemvArgs &a, int max_grid, hipStream_t s) {
 // pathological flat distribution), k_topk_final falls back to k exact
 // passes over all logits.
 #define TOPK_CAND 4096
-#define LMHEAD_WG 1024                                 // workgroups of the LM-head GEMV (grid-stride
-                                                       // over tiles), one maximum each
+// Workgroups of the LM-head GEMV (grid-stride over tiles), one maximum
+// each: two per CU. Measured with argmax on 248320 x 1024: 1024 (four per
+// CU) 40.7 us, 768 40.2, 512 39.6, 384 45.6, 256 48.9; counts that leave
+// CUs unevenly loaded (640, 896) are slower than their neighbours.
+#define LMHEAD_WG 512
 
 __device__ __forceinline__ uint32_t valkey(float v) {
     uint32_t b = __float_as_uint(v);

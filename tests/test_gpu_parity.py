@@ -167,9 +167,10 @@ def test_matmul_gemm_m2048(lib, orc):
 
 # ---- LM head ---------------------------------------------------------------------------
 
-# Group sizes of the top-k bound (maxima of 1, 4 or 16 GEMV workgroups):
-# k <= 64 of 1024 maxima uses 16, (248320, 256) and (31040, 100) use 4,
-# (5000, 256) uses 1, (300, 200) has fewer maxima than k (no bound).
+# Group sizes of the top-k bound (maxima of 1, 4 or 16 GEMV workgroups,
+# at most 512 of them): k <= 32 uses 16, (248320, 40) and (9000, 64) use
+# 4, (248320, 256) and (5000, 256) use 1, (300, 200) has fewer maxima
+# than k (no bound).
 # Past 1024 tiles the LM-head waves run several items with two register
 # sets in turn: (16400, 1024) has 1025 tiles; (100003, 2048), (50001,
 # 4096) and (262147, 256) have rows of 8, 16 and 4 groups (the last with
