@@ -330,7 +330,7 @@ def main():
                    "weight_copies": copies, "bytes_per_step": per, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": CONFIG1_TRAFFIC_BYTES,
-                     "kernel": "k_gemv<true> (one launch per step)", "us_per_launch": round(us, 3)},
+                     "kernel": "k_gemv<true, false> (one launch per step)", "us_per_launch": round(us, 3)},
         "tier": lib.tier_label(),
     }
     if not a.no_extra:
