@@ -477,68 +477,134 @@ void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb, const uint8_t *__r
                     isum[v] = t;
                 }
             }
-            // The KS waves of a sub-tile exchange parts: wave g finishes
-            // outputs v = VPW*g .. VPW*g + VPW-1 and hands the others to
-            // their owners. Integer sums: exact in any order.
-            if (ALIAS) lds_barrier();                            // every wave is done reading s.a
+            if constexpr (KS == 4) {
+                // Four parts: one copy of the rest of the step per part, so
+                // every part index is a compile-time constant (the runtime
+                // selects below cost 2.5-4 % here; with two parts a copy per
+                // part gains nothing, and for 64-row Q6_K tiles it exceeds the
+                // register budget).
+                auto finish = [&](auto gc) __attribute__((always_inline)) {
+                    constexpr int G = decltype(gc)::value;
+                    if (ALIAS) lds_barrier();                            // every wave is done reading s.a
 #pragma unroll
-            for (int o = 0; o < KS; o++) {
-                if (o == g) continue;
-                const int slot = (g - o - 1 + KS) % KS;
-                int32_t *xo = xch + (((sub * KS + o) * (KS - 1) + slot) * VPW) * 64 + lane;
+                    for (int o = 0; o < KS; o++) {
+                        if (o == G) continue;
+                        const int slot = (G - o - 1 + KS) % KS;
+                        int32_t *xo = xch + (((sub * KS + o) * (KS - 1) + slot) * VPW) * 64 + lane;
 #pragma unroll
-                for (int v = 0; v < VPW; v++) xo[64 * v] = isum[VPW * o + v];
-            }
-            lds_barrier();
-            // own part (g is wave-uniform; selects keep every index static)
-            int32_t mine[VPW];
-#pragma unroll
-            for (int v = 0; v < VPW; v++) {
-                mine[v] = isum[v];
-#pragma unroll
-                for (int q = 1; q < KS; q++) mine[v] = g == q ? isum[VPW * q + v] : mine[v];
-            }
-#pragma unroll
-            for (int sl = 0; sl < KS - 1; sl++) {
-                const int32_t *xi = xch + (((sub * KS + g) * (KS - 1) + sl) * VPW) * 64 + lane;
-#pragma unroll
-                for (int v = 0; v < VPW; v++) mine[v] += xi[64 * v];
-            }
-
-            const float wd = s.wd[tn + col];
-            if constexpr (TYPE == 14) {
-#pragma unroll
-                for (int v = 0; v < VPW; v++) {
-                    const float yd = s.yd[tm + tok_of(VPW * g + v, h)];
-                    sum[v] = __fadd_rn(sum[v], __fmul_rn(__fmul_rn(wd, yd), (float)mine[v]));
-                }
-            } else {
-                // isum_mins = sum_j m_j * (bsums[2j] + bsums[2j+1]) as two small
-                // MFMAs: the bsum pairs enter as int8 digits (lo | hi), the mins
-                // sit against the lo half for one product and the hi half for
-                // the other, so mins = lo_product + 128 * hi_product exactly.
-                const long amv = *(const QK_LDS long *)&s.am[tm + col][8 * h];
-                const long mnv = *(const QK_LDS long *)&s.mn[tn + col][0];
-                const v16i dl = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 0 ? mnv : 0L, zero, 0, 0, 0);
-                const v16i dh = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 1 ? mnv : 0L, zero, 0, 0, 0);
-                const float wdm = s.wdm[tn + col];
-#pragma unroll
-                for (int v = 0; v < VPW; v++) {
-                    const int vv = VPW * g + v;
-                    int32_t ml = dl[v], mh = dh[v];
-#pragma unroll
-                    for (int q = 1; q < KS; q++) {
-                        ml = g == q ? dl[VPW * q + v] : ml;
-                        mh = g == q ? dh[VPW * q + v] : mh;
+                        for (int v = 0; v < VPW; v++) xo[64 * v] = isum[VPW * o + v];
                     }
-                    const int32_t mins = ml + mh * 128;
-                    const float yd = s.yd[tm + tok_of(vv, h)];
-                    const float d = __fmul_rn(yd, wd);
-                    const float dmin = __fmul_rn(yd, wdm);
-                    const float pm = __fmul_rn(dmin, (float)mins);
-                    const float term = FUSED ? __builtin_fmaf(d, (float)mine[v], -pm)
-                                             : __fsub_rn(__fmul_rn(d, (float)mine[v]), pm);
-                    sum[v] = __fadd_rn(sum[v], term);
+                    lds_barrier();
+                    // own part
+                    int32_t mine[VPW];
+#pragma unroll
+                    for (int v = 0; v < VPW; v++) mine[v] = isum[VPW * G + v];
+#pragma unroll
+                    for (int sl = 0; sl < KS - 1; sl++) {
+                        const int32_t *xi = xch + (((sub * KS + G) * (KS - 1) + sl) * VPW) * 64 + lane;
+#pragma unroll
+                        for (int v = 0; v < VPW; v++) mine[v] += xi[64 * v];
+                    }
+
+                    const float wd = s.wd[tn + col];
+                    if constexpr (TYPE == 14) {
+#pragma unroll
+                        for (int v = 0; v < VPW; v++) {
+                            const float yd = s.yd[tm + tok_of(VPW * G + v, h)];
+                            sum[v] = __fadd_rn(sum[v], __fmul_rn(__fmul_rn(wd, yd), (float)mine[v]));
+                        }
+                    } else {
+                        // isum_mins = sum_j m_j * (bsums[2j] + bsums[2j+1]) as two small
+                        // MFMAs: the bsum pairs enter as int8 digits (lo | hi), the mins
+                        // sit against the lo half for one product and the hi half for
+                        // the other, so mins = lo_product + 128 * hi_product exactly.
+                        const long amv = *(const QK_LDS long *)&s.am[tm + col][8 * h];
+                        const long mnv = *(const QK_LDS long *)&s.mn[tn + col][0];
+                        const v16i dl = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 0 ? mnv : 0L, zero, 0, 0, 0);
+                        const v16i dh = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 1 ? mnv : 0L, zero, 0, 0, 0);
+                        const float wdm = s.wdm[tn + col];
+#pragma unroll
+                        for (int v = 0; v < VPW; v++) {
+                            const int vv = VPW * G + v;
+                            const int32_t mins = dl[vv] + dh[vv] * 128;
+                            const float yd = s.yd[tm + tok_of(vv, h)];
+                            const float d = __fmul_rn(yd, wd);
+                            const float dmin = __fmul_rn(yd, wdm);
+                            const float pm = __fmul_rn(dmin, (float)mins);
+                            const float term = FUSED ? __builtin_fmaf(d, (float)mine[v], -pm)
+                                                     : __fsub_rn(__fmul_rn(d, (float)mine[v]), pm);
+                            sum[v] = __fadd_rn(sum[v], term);
+                        }
+                    }
+                };
+                if (g == 0) finish(std::integral_constant<int, 0>{});
+                else if (g == 1) finish(std::integral_constant<int, 1>{});
+                else if (g == 2) finish(std::integral_constant<int, 2>{});
+                else finish(std::integral_constant<int, 3>{});
+            } else {
+                // The KS waves of a sub-tile exchange parts: wave g finishes
+                // outputs v = VPW*g .. VPW*g + VPW-1 and hands the others to
+                // their owners. Integer sums: exact in any order.
+                if (ALIAS) lds_barrier();                            // every wave is done reading s.a
+#pragma unroll
+                for (int o = 0; o < KS; o++) {
+                    if (o == g) continue;
+                    const int slot = (g - o - 1 + KS) % KS;
+                    int32_t *xo = xch + (((sub * KS + o) * (KS - 1) + slot) * VPW) * 64 + lane;
+#pragma unroll
+                    for (int v = 0; v < VPW; v++) xo[64 * v] = isum[VPW * o + v];
+                }
+                lds_barrier();
+                // own part (g is wave-uniform; selects keep every index static)
+                int32_t mine[VPW];
+#pragma unroll
+                for (int v = 0; v < VPW; v++) {
+                    mine[v] = isum[v];
+#pragma unroll
+                    for (int q = 1; q < KS; q++) mine[v] = g == q ? isum[VPW * q + v] : mine[v];
+                }
+#pragma unroll
+                for (int sl = 0; sl < KS - 1; sl++) {
+                    const int32_t *xi = xch + (((sub * KS + g) * (KS - 1) + sl) * VPW) * 64 + lane;
+#pragma unroll
+                    for (int v = 0; v < VPW; v++) mine[v] += xi[64 * v];
+                }
+
+                const float wd = s.wd[tn + col];
+                if constexpr (TYPE == 14) {
+#pragma unroll
+                    for (int v = 0; v < VPW; v++) {
+                        const float yd = s.yd[tm + tok_of(VPW * g + v, h)];
+                        sum[v] = __fadd_rn(sum[v], __fmul_rn(__fmul_rn(wd, yd), (float)mine[v]));
+                    }
+                } else {
+                    // isum_mins = sum_j m_j * (bsums[2j] + bsums[2j+1]) as two small
+                    // MFMAs: the bsum pairs enter as int8 digits (lo | hi), the mins
+                    // sit against the lo half for one product and the hi half for
+                    // the other, so mins = lo_product + 128 * hi_product exactly.
+                    const long amv = *(const QK_LDS long *)&s.am[tm + col][8 * h];
+                    const long mnv = *(const QK_LDS long *)&s.mn[tn + col][0];
+                    const v16i dl = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 0 ? mnv : 0L, zero, 0, 0, 0);
+                    const v16i dh = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 1 ? mnv : 0L, zero, 0, 0, 0);
+                    const float wdm = s.wdm[tn + col];
+#pragma unroll
+                    for (int v = 0; v < VPW; v++) {
+                        const int vv = VPW * g + v;
+                        int32_t ml = dl[v], mh = dh[v];
+#pragma unroll
+                        for (int q = 1; q < KS; q++) {
+                            ml = g == q ? dl[VPW * q + v] : ml;
+                            mh = g == q ? dh[VPW * q + v] : mh;
+                        }
+                        const int32_t mins = ml + mh * 128;
+                        const float yd = s.yd[tm + tok_of(vv, h)];
+                        const float d = __fmul_rn(yd, wd);
+                        const float dmin = __fmul_rn(yd, wdm);
+                        const float pm = __fmul_rn(dmin, (float)mins);
+                        const float term = FUSED ? __builtin_fmaf(d, (float)mine[v], -pm)
+                                                 : __fsub_rn(__fmul_rn(d, (float)mine[v]), pm);
+                        sum[v] = __fadd_rn(sum[v], term);
+                    }
                 }
             }
         }
