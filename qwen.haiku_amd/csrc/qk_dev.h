@@ -111,7 +111,6 @@ __device__ __forceinline__ float swz_xor2(float v) {
 #define QK_GLOBAL   /* host pass: device bodies are parsed, never run */
 #define QK_LDS
 #endif
-struct __attribute__((aligned(4))) u32x4a4 { uint32_t x, y, z, w; };
 
 __device__ __forceinline__ uint4 ld16(const uint8_t *p) {       // 16-B aligned
     return *(const QK_GLOBAL uint4 *)(p);
@@ -119,16 +118,6 @@ __device__ __forceinline__ uint4 ld16(const uint8_t *p) {       // 16-B aligned
 
 __device__ __forceinline__ uint32_t ld32(const uint8_t *p) {    // 4-B aligned
     return *(const QK_GLOBAL uint32_t *)(p);
-}
-
-__device__ __forceinline__ u32x4a4 ld16_a4(const uint8_t *p) {  // 4-B aligned
-    const QK_GLOBAL uint32_t *q = (const QK_GLOBAL uint32_t *)(p);
-    u32x4a4 r;
-    r.x = q[0];
-    r.y = q[1];
-    r.z = q[2];
-    r.w = q[3];
-    return r;
 }
 
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) {  // 2-B aligned
