@@ -428,9 +428,9 @@ __device__ __forceinline__ void gather_terms(float (&tg)[P], float t, int src0) 
 // operands' loads go out before the first item's. Item offsets are
 // 32-bit: the API limits a matrix to 4 GB.
 //
-// LM (the LM-head kernel, which has registers to spare at its 4 waves per
-// SIMD): waves of many one-item rows alternate two register sets, so the
-// loads of the next item are in flight while the wave waits for the
+// LM (the LM-head kernel, whose register budget allows 4 waves per SIMD;
+// it runs 2): waves of many one-item rows alternate two register sets, so
+// the loads of the next item are in flight while the wave waits for the
 // current one's. The general loop must instead wait for all loads before
 // it moves the look-ahead registers into place.
 template <int TYPE, int LP, bool FUSED, bool LM>
