@@ -261,8 +261,9 @@ __device__ __forceinline__ uint32_t u6_minus_32(uint32_t x) {
 // it (a 16-byte and a 4-byte load; the last ends at most at byte 196 of
 // the block); quarter 0 also reads the 16 scale bytes the same way and d.
 // The buffer starts at the 4-byte aligned address at or below the tile's
-// first row and ends with its last row, so offsets are 32-bit, every
-// aligned load stays inside it, and rows past n read zeros.
+// first row and ends with its last row, so offsets are 32-bit and every
+// byte a lane uses lies inside it. Rows past n read zeros, and so does the
+// unused fifth scale dword of the tile's last block when sh = 0.
 struct WRaw14 { uint32_t v[15]; uint4 sc; uint32_t sc4, d, sh; };
 
 __device__ __forceinline__ void load_w(WRaw14 &a, __amdgpu_buffer_rsrc_t r, int row_off, int q, int i) {
