@@ -5,24 +5,33 @@ Workload: the decode-step GEMV set of one
 Qwen3.5-0.8B-shaped layer at batch 1 -- Q4_K gate and up (3584x1024),
 Q6_K down (1024x3584), Q5_K 2048x1024, 512x1024 and 1024x2048, Q8_0
 1024x1024 -- random blocks per the BASELINE recipe, activations already
-quantized (Q8_K / Q8_0) and resident in HBM. One step is one fused launch
-(hip_matvec_group) over the seven matrices. Steps rotate through enough
-distinct weight copies (> 512 MB) that every step streams its weights
-from HBM rather than the 256 MB MALL.
+quantized (Q8_K / Q8_0) and resident in HBM. One launch is one fused
+dispatch (hip_matvec_group) over the seven matrices.
+
+Timing. One step is one replay of a HIP graph holding R launches that
+rotate through enough distinct weight copies (> 512 MB) that every launch
+streams its weights from HBM rather than the 256 MB MALL; R is chosen so
+that a replay lasts about a millisecond, so the timed region is GPU-bound
+whatever --steps is (20 steps: about 25 ms of back-to-back launches).
+Warm-up replays run for at least 0.2 s (and at least --warmup replays).
+HIP events on the replay stream bracket the --steps timed replays.
 
 metric: GB/s of algorithmic bytes (weights + quantized activations + fp32
-outputs, 11,560,856 B per step) over the timed steps.
+outputs, 11,560,856 B per launch) over the timed launches.
 
-Also reported under "extra": config 0 (single Q4_K GEMV), config 2 (LM
-head with fused argmax / top-40), config 3 (prefill GEMM) when available.
-The CPU baseline times the reference's own tensor_matmul_* (oracle/_ref,
-compiled from its sources) on this host's cores over a bounded sample.
+Also reported under "extra": config 1 with its activation quantization in
+the step, config 0 (single Q4_K GEMV), config 2 (LM head with fused
+argmax / top-40, and its GEMV alone), a Q4_K GEMV of LM-head size
+(streaming), config 3 (prefill GEMM), config 4 (end-to-end tok/s of the
+drop-in and of the CPU reference), and the CPU reference beside each
+config, on one core and on every core this process may use.
 """
 import argparse
 import ctypes as C
 import importlib.util
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -31,13 +40,18 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 CONFIG1 = [(12, 3584, 1024), (12, 3584, 1024), (14, 1024, 3584), (13, 2048, 1024),
            (13, 512, 1024), (13, 1024, 2048), (8, 1024, 1024)]
 HBM_PEAK_GBS = 8000.0
+MFMA_I8_PEAK_TOPS = 5000.0
 MALL_DEFEAT_BYTES = 512 << 20
+REPLAY_TARGET_S = 1.0e-3          # a graph replay (one step) lasts about this long
+WARM_S = 0.2                      # minimum warm-up time
 # HBM bytes per config-1 launch of the current k_gemv, from rocprofv3 --pmc
 # FETCH_SIZE and WRITE_SIZE runs of this script (--copy-probe 256), each
 # scaled by its reading for a known-size copy / fill (FETCH x2.000,
 # WRITE x1.000); the runs are recorded in profiles/k_gemv_decode_set_lmhead.md.
 # None when the kernel has changed since the last counter run.
 CONFIG1_TRAFFIC_BYTES = 11_997_184 + 55_296
+E2E_GPU = os.path.join(ROOT, "qwen.haiku_amd", "host", "_build", "qwen_e2e_gpu")
+E2E_CPU = os.path.join(ROOT, "oracle", "_ref", "qwen_e2e_cpu")
 
 
 def _load(rel, name):
@@ -50,113 +64,196 @@ def _load(rel, name):
     return mod
 
 
-def alg_bytes(wtype, n, k):
+def act_bytes(wtype, k):
+    return (k // 32) * 34 if wtype == 8 else (k // 256) * 292
+
+
+def weight_bytes(wtype, n, k):
     bb = {8: 34, 12: 144, 13: 176, 14: 210}[wtype]
-    be = 32 if wtype == 8 else 256
-    xq = (k // 32) * 34 if wtype == 8 else (k // 256) * 292
-    return n * (k // be) * bb + xq + 4 * n
+    return n * (k // (32 if wtype == 8 else 256)) * bb
 
 
-class Events:
-    """HIP events on the stream the kernels run on."""
+def alg_bytes(wtype, n, k):
+    return weight_bytes(wtype, n, k) + act_bytes(wtype, k) + 4 * n
+
+
+def cores_available():
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def cpu_threads():
+    """Threads for the N-core CPU figures: every core this process may use,
+    at most 16 (a one-GPU box's share of its host)."""
+    return max(1, min(16, cores_available()))
+
+
+class GraphTimer:
+    """Launch sequences captured once in a HIP graph and replayed.
+
+    launch(i, stream) enqueues launch i (0 <= i < R) on `stream` (a
+    ctypes void pointer). The graph holds launches 0..R-1 in order; one
+    step is one replay."""
 
     def __init__(self, torch):
         self.torch = torch
 
-    def time(self, fn, steps, warmup):
+    def time(self, launch, R, steps, warmup):
         torch = self.torch
-        for i in range(warmup):
-            fn(i)
-        torch.cuda.synchronize()
-        s = torch.cuda.current_stream()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        for i in range(steps):
-            fn(warmup + i)
-        e1.record(s)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / 1e3            # seconds
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        sp = C.c_void_p(s.cuda_stream)
+        with torch.cuda.stream(s):
+            for i in range(R):                 # eager pass: the stream's own scratch exists before capture
+                launch(i, sp)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(R):
+                launch(i, sp)
+        with torch.cuda.stream(s):
+            n, t0 = 0, time.perf_counter()
+            while n < warmup or time.perf_counter() - t0 < WARM_S:
+                g.replay()
+                n += 1
+                if n % 16 == 0:
+                    s.synchronize()
+            s.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(steps):
+                g.replay()
+            e1.record(s)
+        s.synchronize()
+        secs = e0.elapsed_time(e1) / 1e3
+        del g
+        return secs                            # for steps x R launches
+
+
+def replays_for(copies, est_us):
+    """Launches per replay: whole passes over the copies, about
+    REPLAY_TARGET_S long (est_us: estimated microseconds per launch)."""
+    per_pass = copies * est_us * 1e-6
+    passes = max(1, int(round(REPLAY_TARGET_S / per_pass)))
+    return copies * passes
+
+
+def rate(per_launch, R, steps, secs):
+    us = secs / (steps * R) * 1e6
+    return per_launch * steps * R / secs / 1e9, us
+
+
+def config1_mats(torch, synth, lib, copies, shared=False):
+    """The config-1 weights (copies of each) with activations. shared=True
+    gives the activations a decode layer has: one normed hidden row (k=1024)
+    feeds gate, up, both 1024-wide Q5_K projections and the Q8_0 matrix,
+    the FFN product (k=3584) feeds down, and a k=2048 row the last Q5_K."""
+    base = []
+    xs = {}
+    for i, (t, n, k) in enumerate(CONFIG1):
+        w = torch.from_numpy(synth.blocks(t, n, k, seed=0, tag=i)).cuda()
+        key = k if shared else i
+        if key not in xs:
+            xs[key] = torch.from_numpy(synth.activations(1, k, seed=0, tag=i)).cuda()
+        base.append((t, w, n, k, xs[key]))
+    sets = []
+    for c in range(copies):
+        sets.append([(t, w if c == 0 else w.clone(), n, k, x) for (t, w, n, k, x) in base])
+    return sets, xs
 
 
 def bench_config1(torch, qk, synth, lib, steps, warmup, warm=False):
     """Config 1 (the metric). warm=True: one weight copy, so the 11.5 MB
-    stay in the 256 MB MALL between steps (a labelled warm-cache figure,
+    stay in the 256 MB MALL between launches (a labelled warm-cache figure,
     never the metric)."""
-    per_set = sum(alg_bytes(*s) for s in CONFIG1)
-    wbytes = sum(alg_bytes(*s) - ((s[2] // 32) * 34 if s[0] == 8 else (s[2] // 256) * 292) - 4 * s[1] for s in CONFIG1)
+    per = sum(alg_bytes(*s) for s in CONFIG1)
+    wbytes = sum(weight_bytes(*s) for s in CONFIG1)
     copies = 1 if warm else max(2, -(-MALL_DEFEAT_BYTES // wbytes))
-    base = []
-    for i, (t, n, k) in enumerate(CONFIG1):
-        w = torch.from_numpy(synth.blocks(t, n, k, seed=0, tag=i)).cuda()
-        x = torch.from_numpy(synth.activations(1, k, seed=0, tag=i)).cuda()
-        xq = lib.quantize_for(t, x)[0]
-        base.append((t, w, n, k, xq))
-    sets = []
-    for c in range(copies):
-        items = []
-        for (t, w, n, k, xq) in base:
-            wc = w if c == 0 else w.clone()
-            items.append((t, wc, n, k, xq, torch.empty(n, dtype=torch.float32, device="cuda")))
-        sets.append(items)
+    sets, _ = config1_mats(torch, synth, lib, copies)
+    xq = {}
     descs = []
     for items in sets:
         arr = (qk.GemvDesc * len(items))()
-        for i, (t, w, n, k, xq, y) in enumerate(items):
+        for i, (t, w, n, k, x) in enumerate(items):
+            if (i, t) not in xq:
+                xq[(i, t)] = lib.quantize_for(t, x)[0]
+            y = torch.empty(n, dtype=torch.float32, device="cuda")
+            items[i] = (t, w, n, k, x, y)
+            arr[i] = qk.GemvDesc(t, 0, n, k, w.data_ptr(), xq[(i, t)].data_ptr(), y.data_ptr())
+        descs.append(arr)
+    torch.cuda.synchronize()
+    fn = lib.L.hip_matvec_group
+    R = replays_for(copies, 5.0) if not warm else 200
+
+    def launch(i, sp):
+        if fn(descs[i % copies], len(CONFIG1), sp):
+            raise RuntimeError(lib.last_error())
+
+    secs = GraphTimer(torch).time(launch, R, steps, warmup)
+    keep = (sets, xq, descs)
+    del keep
+    return per, copies, R, secs
+
+
+def bench_config1_quantize(torch, qk, synth, lib, steps, warmup):
+    """Config 1 from fp32 activations: each launch quantizes the layer's
+    activation rows (Q8_K for k = 1024, 3584, 2048; Q8_0 for k = 1024) and
+    then runs the seven GEMVs. Algorithmic bytes add the fp32 rows read
+    (4 B per element, once per distinct row) to the config-1 bytes; the
+    quantized rows are counted once, as in config 1."""
+    wbytes = sum(weight_bytes(*s) for s in CONFIG1)
+    copies = max(2, -(-MALL_DEFEAT_BYTES // wbytes))
+    sets, xs = config1_mats(torch, synth, lib, copies, shared=True)
+    per = sum(alg_bytes(*s) for s in CONFIG1) + sum(4 * x.numel() for x in xs.values())
+    q8k = {k: torch.empty((k // 256) * 292, dtype=torch.uint8, device="cuda") for k in xs}
+    q80 = torch.empty((1024 // 32) * 34, dtype=torch.uint8, device="cuda")
+    descs = []
+    for items in sets:
+        arr = (qk.GemvDesc * len(items))()
+        for i, (t, w, n, k, x) in enumerate(items):
+            y = torch.empty(n, dtype=torch.float32, device="cuda")
+            items[i] = (t, w, n, k, x, y)
+            xq = q80 if t == 8 else q8k[k]
             arr[i] = qk.GemvDesc(t, 0, n, k, w.data_ptr(), xq.data_ptr(), y.data_ptr())
         descs.append(arr)
-    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
-    fn = lib.L.hip_matvec_group
+    quants = [(lib.L.hip_quantize_q8k, xs[k], k, q8k[k]) for k in sorted(xs)] + \
+             [(lib.L.hip_quantize_q8_0, xs[1024], 1024, q80)]
+    R = replays_for(copies, 12.0)
 
-    def step(i):
-        if fn(descs[i % copies], len(CONFIG1), stream):
+    def launch(i, sp):
+        for f, x, k, out in quants:
+            if f(C.c_void_p(x.data_ptr()), 1, k, C.c_void_p(out.data_ptr()), sp):
+                raise RuntimeError(lib.last_error())
+        if lib.L.hip_matvec_group(descs[i % copies], len(CONFIG1), sp):
             raise RuntimeError(lib.last_error())
 
-    secs = Events(torch).time(step, steps, warmup)
-    return per_set, copies, secs
+    secs = GraphTimer(torch).time(launch, R, steps, warmup)
+    return per, copies, R, secs, len(quants) + 1
 
 
-def config1_each(torch, qk, synth, lib, steps):
-    """Each distinct config-1 matrix alone (one-descriptor launches), then
-    the set, `steps` launches each, for per-kernel counters: a profiling
-    aid, not a benchmark figure (one weight copy)."""
-    items, seen, out = [], set(), {}
-    for i, (t, n, k) in enumerate(CONFIG1):
-        w = torch.from_numpy(synth.blocks(t, n, k, seed=0, tag=i)).cuda()
-        x = torch.from_numpy(synth.activations(1, k, seed=0, tag=i)).cuda()
-        items.append((t, w, n, k, lib.quantize_for(t, x)[0], torch.empty(n, dtype=torch.float32, device="cuda")))
-    ev = Events(torch)
-    for it in items:
-        key = f"{it[0]}_{it[2]}x{it[3]}"
-        if key in seen:
-            continue
-        seen.add(key)
-        out[key] = round(ev.time(lambda i: lib.matvec_group([it]), steps, 2) / steps * 1e6, 3)
-    out["set"] = round(ev.time(lambda i: lib.matvec_group(items), steps, 2) / steps * 1e6, 3)
-    return out
-
-
-def bench_config0(torch, qk, synth, lib, steps, warmup):
-    t, n, k = 12, 3584, 1024
-    per = alg_bytes(t, n, k)
-    copies = -(-MALL_DEFEAT_BYTES // (per - 292 * 4 - 4 * n))
-    w = torch.from_numpy(synth.blocks(t, n, k, seed=0)).cuda()
+def bench_gemv(torch, qk, synth, lib, steps, warmup, wtype, n, k, est_us):
+    """One GEMV (hip_matvec_*) over rotating weight copies."""
+    per = alg_bytes(wtype, n, k)
+    copies = max(2, -(-MALL_DEFEAT_BYTES // weight_bytes(wtype, n, k)))
+    w = torch.from_numpy(synth.blocks(wtype, n, k, seed=0)).cuda()
     ws = [w] + [w.clone() for _ in range(copies - 1)]
-    xq = lib.quantize_q8k(torch.from_numpy(synth.activations(1, k, seed=0)).cuda())[0]
+    xq = lib.quantize_for(wtype, torch.from_numpy(synth.activations(1, k, seed=0)).cuda())[0]
     y = torch.empty(n, dtype=torch.float32, device="cuda")
-    # direct C calls with prebuilt pointers: a 2 MB GEMV is shorter than
-    # the binding's Python-side checks
     wp = [C.c_void_p(x.data_ptr()) for x in ws]
     xp, yp = C.c_void_p(xq.data_ptr()), C.c_void_p(y.data_ptr())
-    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
-    fn = lib.L.hip_matvec_q4k
+    fn = {8: lib.L.hip_matvec_q8_0, 12: lib.L.hip_matvec_q4k, 13: lib.L.hip_matvec_q5k,
+          14: lib.L.hip_matvec_q6k}[wtype]
+    R = replays_for(copies, est_us)
 
-    def step(i):
-        if fn(wp[i % copies], n, k, xp, yp, stream):
+    def launch(i, sp):
+        if fn(wp[i % copies], n, k, xp, yp, sp):
             raise RuntimeError(lib.last_error())
 
-    secs = Events(torch).time(step, steps, warmup)
-    return per, copies, secs
+    secs = GraphTimer(torch).time(launch, R, steps, warmup)
+    return per, copies, R, secs
 
 
 def bench_config2(torch, qk, synth, lib, steps, warmup):
@@ -170,23 +267,26 @@ def bench_config2(torch, qk, synth, lib, steps, warmup):
     ti = torch.empty(topk, dtype=torch.int32, device="cuda")
     tv = torch.empty(topk, dtype=torch.float32, device="cuda")
     lib.lmhead(w, n, k, xq, topk=topk, logits=logits)  # checked once through the binding
-    # the timed loop calls the C ABI directly with preallocated outputs, so
-    # host-side Python does not pace the launches
     f = lib.L.hip_lmhead_q6k_argmax_topk
     wp = [C.c_void_p(t.data_ptr()) for t in ws]
     xp, lp = C.c_void_p(xq.data_ptr()), C.c_void_p(logits.data_ptr())
     ap, ip, vp = C.c_void_p(am.data_ptr()), C.c_void_p(ti.data_ptr()), C.c_void_p(tv.data_ptr())
-    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
     per = n * 4 * 210 + 4 * 292 + 4 * n
-    secs = Events(torch).time(lambda i: f(wp[i % copies], n, k, xp, topk, lp, ap, ip, vp, stream), steps, warmup)
-    return per, copies, secs
+    R = replays_for(copies, 45.0)
+
+    def launch(i, sp):
+        if f(wp[i % copies], n, k, xp, topk, lp, ap, ip, vp, sp):
+            raise RuntimeError(lib.last_error())
+
+    secs = GraphTimer(torch).time(launch, R, steps, warmup)
+    return per, copies, R, secs
 
 
 def bench_config3(torch, qk, synth, lib, steps, warmup, wtype=12, n=3584, k=1024, m=512):
     """Chunked-prefill GEMM (int8 MFMA): xq resident, y fp32. Weight and
-    output buffers rotate through > 512 MB so each step reads its weights
-    from HBM and writes its outputs to fresh lines. Returns (seconds for
-    the GEMM alone, seconds for quantize + GEMM from fp32 x)."""
+    output buffers rotate through > 512 MB so each launch reads its weights
+    from HBM and writes its outputs to fresh lines. Returns (copies, R,
+    seconds for the GEMM alone, seconds for quantize + GEMM from fp32 x)."""
     per = n * (k // 256) * qk.BLOCK_BYTES[wtype] + 4 * m * n
     copies = max(2, -(-MALL_DEFEAT_BYTES // per))
     w = torch.from_numpy(synth.blocks(wtype, n, k, seed=0)).cuda()
@@ -198,53 +298,197 @@ def bench_config3(torch, qk, synth, lib, steps, warmup, wtype=12, n=3584, k=1024
     wp = [C.c_void_p(t.data_ptr()) for t in ws]
     yp = [C.c_void_p(t.data_ptr()) for t in ys]
     xp, xqp = C.c_void_p(x.data_ptr()), C.c_void_p(xq.data_ptr())
-    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
     quant = lib.L.hip_quantize_q8k
+    est = 2.0 * m * n * k / 250e12 * 1e6
+    R = replays_for(copies, est)
 
-    def gemm(i):
-        if fn(wp[i % copies], n, k, xqp, m, yp[i % copies], stream):
+    def gemm(i, sp):
+        if fn(wp[i % copies], n, k, xqp, m, yp[i % copies], sp):
             raise RuntimeError(lib.last_error())
 
-    def both(i):
-        if quant(xp, m, k, xqp, stream):
+    def both(i, sp):
+        if quant(xp, m, k, xqp, sp):
             raise RuntimeError(lib.last_error())
-        gemm(i)
+        gemm(i, sp)
 
-    ev = Events(torch)
-    return copies, ev.time(gemm, steps, warmup), ev.time(both, steps, warmup)
+    gt = GraphTimer(torch)
+    return copies, R, gt.time(gemm, R, steps, warmup), gt.time(both, R, steps, warmup)
+
+
+CONFIG3_CASES = ((12, 3584, 1024, 512), (12, 3584, 1024, 128), (12, 3584, 1024, 2048), (14, 1024, 3584, 512))
+
+
+def config3_extras(torch, qk, synth, lib, steps, warmup, peak_tops=None):
+    """Config 3 at M = 512 / 128 / 2048 (Q4_K) and the Q6_K down projection.
+    peak_tops: the measured int8 MFMA throughput, for a second fraction."""
+    extra = {}
+    for (t, n3, k3, m3) in CONFIG3_CASES:
+        c3, R, sg, sb = bench_config3(torch, qk, synth, lib, steps, warmup, t, n3, k3, m3)
+        ops = 2.0 * m3 * n3 * k3
+        launches = steps * R
+        alg = 4 * m3 * k3 + n3 * (k3 // 256) * qk.BLOCK_BYTES[t] + 4 * m3 * n3
+        tg, tb = ops * launches / sg, ops * launches / sb
+        name = {12: "q4k", 14: "q6k"}[t]
+        e = {"TOPS_gemm": round(tg / 1e12, 2), "us_gemm": round(sg / launches * 1e6, 3),
+             "TOPS_with_quantize": round(tb / 1e12, 2), "us_with_quantize": round(sb / launches * 1e6, 3),
+             "frac_of_5POPS_gemm": round(tg / (MFMA_I8_PEAK_TOPS * 1e12), 4),
+             "frac_of_5POPS_with_quantize": round(tb / (MFMA_I8_PEAK_TOPS * 1e12), 4),
+             "frac_of_bw_x_ai": round(tb / (HBM_PEAK_GBS * 1e9 * ops / alg), 4),
+             "copies": c3, "launches_per_step": R}
+        if peak_tops:
+            e["frac_of_measured_mfma_peak_gemm"] = round(tg / (peak_tops * 1e12), 4)
+        extra[f"config3_gemm_{name}_m{m3}_n{n3}_k{k3}"] = e
+    return extra
+
+
+# ---- CPU reference ------------------------------------------------------------------
+
+def host_description():
+    """CPU model, sockets, cores, SMT, governor and memory of this host."""
+    d = {"logical_cpus": os.cpu_count(), "cpus_available": cores_available()}
+    try:
+        phys, model = set(), None
+        pid = cid = None
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name" and model is None:
+                model = v
+            elif k == "physical id":
+                pid = v
+            elif k == "core id":
+                cid = v
+            elif not k and pid is not None:
+                phys.add((pid, cid))
+                pid = cid = None
+        if pid is not None:
+            phys.add((pid, cid))
+        d["model"] = model
+        d["sockets"] = len({p for p, _ in phys}) or None
+        d["physical_cores"] = len(phys) or None
+        if d["physical_cores"]:
+            d["threads_per_core"] = round(os.cpu_count() / d["physical_cores"], 2)
+    except OSError:
+        pass
+    try:
+        d["governor"] = open("/sys/devices/system/cpu/cpu0/cpufreq/scaling_governor").read().strip()
+    except OSError:
+        d["governor"] = "unavailable"
+    try:
+        for line in open("/proc/meminfo"):
+            if line.startswith("MemTotal"):
+                d["mem_total_gib"] = round(int(line.split()[1]) / 2**20, 1)
+    except OSError:
+        pass
+    return d
+
+
+def _cpu_backend():
+    oracle = _load("oracle/oracle.py", "qk_oracle_py")
+    if oracle.Ref.available():
+        R = oracle.Ref()
+        return "reference", R.label(), (lambda t, w, n, k, x, th: R.matmul(t, w, n, k, x, threads=th))
+    O = oracle.Oracle()
+    return "port", "oracle restatement", (lambda t, w, n, k, x, th: O.matmul(t, w, n, k, x, oracle.EPI_FUSED,
+                                                                              threads=th))
+
+
+def _cpu_rate(run, mats, threads, seconds, per_pass):
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        for (t, w, n, k, x) in mats:
+            run(t, w, n, k, x, threads)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            return per_pass * reps / dt, reps, dt
 
 
 def cpu_baseline(synth, seconds=10.0):
     """The reference's tensor_matmul_*_f32 (one core, as shipped) over the
     config-1 set, repeated for a bounded time."""
-    oracle = _load("oracle/oracle.py", "qk_oracle_py")
-    if oracle.Ref.available():
-        R = oracle.Ref()
-        kind, label = "reference", R.label()
-        run = lambda t, w, n, k, x: R.matmul(t, w, n, k, x)
-    else:
-        R = oracle.Oracle()
-        kind, label = "port", "oracle restatement"
-        run = lambda t, w, n, k, x: R.matmul(t, w, n, k, x, oracle.EPI_FUSED, threads=1)
+    kind, label, run = _cpu_backend()
     mats = [(t, synth.blocks(t, n, k, seed=0, tag=i), n, k, synth.activations(1, k, seed=0, tag=i))
             for i, (t, n, k) in enumerate(CONFIG1)]
     per_set = sum(alg_bytes(t, n, k) for (t, n, k) in CONFIG1)
-    reps = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        for (t, w, n, k, x) in mats:
-            run(t, w, n, k, x)
-        reps += 1
-    dt = time.perf_counter() - t0
-    return {"value": round(per_set * reps / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
+    bps, reps, dt = _cpu_rate(run, mats, 1, seconds, per_set)
+    return {"value": round(bps / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
             "sample": f"{reps} passes of the config-1 GEMV set (7 matrices, fp32 x quantized per call) "
                       f"through tensor_matmul_*_f32, {dt:.1f} s, dispatch {label}"}
+
+
+def cpu_extras(synth, seconds=2.0):
+    """The CPU reference beside configs 0-3: one core (as shipped,
+    LLM_PAR_FOR is a plain loop on Linux) and N cores (the reference's row
+    dots split over N threads by the harness; bit-identical, rows are
+    independent). Each figure is a bounded sample of about `seconds`."""
+    kind, label, run = _cpu_backend()
+    nth = cpu_threads()
+    out = {"kind": kind, "dispatch": label, "n_core_threads": nth}
+    c1 = [(t, synth.blocks(t, n, k, seed=0, tag=i), n, k, synth.activations(1, k, seed=0, tag=i))
+          for i, (t, n, k) in enumerate(CONFIG1)]
+    per1 = sum(alg_bytes(t, n, k) for (t, n, k) in CONFIG1)
+    w0 = synth.blocks(12, 3584, 1024, seed=0)
+    x0 = synth.activations(1, 1024, seed=0)
+    c0 = [(12, w0, 3584, 1024, x0)]
+    per0 = alg_bytes(12, 3584, 1024)
+    for name, mats, per in (("config0_q4k_gemv", c0, per0), ("config1_decode_set", c1, per1)):
+        for th in (1, nth):
+            bps, reps, dt = _cpu_rate(run, mats, th, seconds, per)
+            out[f"{name}_{th}core"] = {"GB/s": round(bps / 1e9, 3), "passes": reps, "seconds": round(dt, 2)}
+    # config 2: the LM-head GEMV on a bounded slice of the vocabulary, scaled
+    # to the full 248320 rows (rows are independent and equally sized)
+    n2, k2 = 31040, 1024
+    w2 = synth.blocks(14, n2, k2, seed=0)
+    x2 = synth.activations(1, k2, seed=0)
+    for th in (1, nth):
+        bps, reps, dt = _cpu_rate(run, [(14, w2, n2, k2, x2)], th, seconds, alg_bytes(14, n2, k2))
+        out[f"config2_lmhead_gemv_{th}core"] = {
+            "GB/s": round(bps / 1e9, 3), "us_per_full_call": round(209583248 / bps * 1e6, 1),
+            "sample": f"{reps} x {n2} of 248320 rows, {dt:.1f} s"}
+    # config 3: the prefill GEMM on a bounded number of tokens (each token is
+    # an independent quantize + GEMV in the reference's token loop)
+    for (t, n3, k3, m3) in CONFIG3_CASES[:1] + CONFIG3_CASES[3:]:
+        ms = 8
+        w3 = synth.blocks(t, n3, k3, seed=0)
+        x3 = synth.activations(ms, k3, seed=0)
+        ops = 2.0 * ms * n3 * k3
+        for th in (1, nth):
+            r, reps, dt = _cpu_rate(run, [(t, w3, n3, k3, x3)], th, seconds, ops)
+            out[f"config3_{'q4k' if t == 12 else 'q6k'}_m{m3}_{th}core"] = {
+                "TOPS": round(r / 1e9 / 1e3, 4), "sample": f"{reps} x {ms} tokens of {m3}, {dt:.1f} s"}
+    return out
+
+
+def e2e(prompt=512, gen=256, seed=0, timeout=600):
+    """Config 4: the reference's forward pass with its quantized matmuls on
+    the GPU (the drop-in) and the unchanged CPU reference, same model, same
+    prompt, same run."""
+    out = {}
+    for name, path in (("gpu_dropin", E2E_GPU), ("cpu_reference", E2E_CPU)):
+        if not os.path.exists(path):
+            out[name] = "not built"
+            continue
+        r = subprocess.run([path, "--prompt", str(prompt), "--gen", str(gen), "--seed", str(seed)],
+                           capture_output=True, text=True, timeout=timeout)
+        if r.returncode != 0:
+            raise RuntimeError(f"{path} failed ({r.returncode}): {r.stderr[-1000:]}")
+        j = json.loads(r.stdout.strip().splitlines()[-1])
+        out[name] = {k: j[k] for k in ("prefill_tok_s", "decode_tok_s", "prefill_s", "decode_s", "tier")}
+        out[name]["tokens"] = j["tokens"]
+    if isinstance(out.get("gpu_dropin"), dict) and isinstance(out.get("cpu_reference"), dict):
+        out["tokens_identical"] = out["gpu_dropin"]["tokens"] == out["cpu_reference"]["tokens"]
+        out["cpu_reference"]["cores"] = 1
+    for v in out.values():
+        if isinstance(v, dict):
+            v.pop("tokens", None)
+    out["workload"] = f"random Qwen3.5-0.8B-shaped Q4_K_M model, {prompt}-token prompt, {gen} greedy decode steps"
+    return out
 
 
 def mfma_peak():
     """Dense int8 MFMA throughput measured on this GPU by
     qwen.haiku_amd/mfma_peak (built with libqk), or None if it is not built."""
-    import subprocess
     exe = os.path.join(ROOT, "qwen.haiku_amd", "mfma_peak")
     if not os.path.exists(exe):
         return None
@@ -254,40 +498,17 @@ def mfma_peak():
     return json.loads(r.stdout.strip().splitlines()[-1])
 
 
-def config3_extras(torch, qk, synth, lib, steps, peak_tops=None):
-    """Config 3 at M = 512 / 128 / 2048 (Q4_K) and the Q6_K down projection.
-    peak_tops: the measured int8 MFMA throughput, for a second fraction."""
-    extra = {}
-    for (t, n3, k3, m3) in ((12, 3584, 1024, 512), (12, 3584, 1024, 128), (12, 3584, 1024, 2048),
-                            (14, 1024, 3584, 512)):
-        c3, sg, sb = bench_config3(torch, qk, synth, lib, steps, 10, t, n3, k3, m3)
-        ops = 2.0 * m3 * n3 * k3
-        xbytes = 4 * m3 * k3
-        alg = xbytes + n3 * (k3 // 256) * qk.BLOCK_BYTES[t] + 4 * m3 * n3
-        name = {12: "q4k", 14: "q6k"}[t]
-        extra[f"config3_gemm_{name}_m{m3}_n{n3}_k{k3}"] = {
-            "TOPS_gemm": round(ops * steps / sg / 1e12, 2), "us_gemm": round(sg / steps * 1e6, 3),
-            "TOPS_with_quantize": round(ops * steps / sb / 1e12, 2), "us_with_quantize": round(sb / steps * 1e6, 3),
-            "frac_of_5POPS": round(ops * steps / sb / 5.0e15, 4),
-            "frac_of_bw_x_ai": round((ops * steps / sb) / (HBM_PEAK_GBS * 1e9 * ops / alg), 4),
-            "copies": c3}
-        if peak_tops:
-            extra[f"config3_gemm_{name}_m{m3}_n{n3}_k{k3}"]["frac_of_measured_mfma_peak"] = round(
-                ops * steps / sb / (peak_tops * 1e12), 4)
-    return extra
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["all", "config3", "each"], default="all",
-                    help="config3: time only the prefill GEMM cases; each: launch every config-1 "
-                         "matrix alone, then the set (profiling aids)")
+    ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--only", choices=["all", "config1", "config3", "lmhead", "q4k_stream"], default="all",
+                    help="time one case only (profiling aids)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run 8 plain device copies of MIB MiB each: the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -308,52 +529,96 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    if a.only == "each":
-        print(json.dumps({"metric": "config-1 matrices alone, us per launch", "unit": "us",
-                          "extra": config1_each(torch, qk, synth, lib, a.steps)}))
-        return
+    def progress(msg):
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
     if a.only == "config3":
         print(json.dumps({"metric": "prefill int8 TOPS (config 3)", "unit": "TOPS", "dtype": "int8",
-                          "extra": config3_extras(torch, qk, synth, lib, a.steps)}))
+                          "extra": config3_extras(torch, qk, synth, lib, a.steps, a.warmup)}))
+        return
+    if a.only == "lmhead":
+        p2, c2, R2, s2 = bench_config2(torch, qk, synth, lib, a.steps, a.warmup)
+        g, us = rate(p2, R2, a.steps, s2)
+        print(json.dumps({"metric": "config2 LM head GB/s", "value": round(g, 2), "us_per_call": round(us, 3)}))
+        return
+    if a.only == "q4k_stream":
+        p, c, R, s = bench_gemv(torch, qk, synth, lib, a.steps, a.warmup, 12, 248320, 1024, 30.0)
+        g, us = rate(p, R, a.steps, s)
+        print(json.dumps({"metric": "Q4_K 248320x1024 GEMV GB/s", "value": round(g, 2), "us_per_launch": round(us, 3)}))
         return
 
-    per, copies, secs = bench_config1(torch, qk, synth, lib, a.steps, a.warmup)
-    gbs = per * a.steps / secs / 1e9
-    us = secs / a.steps * 1e6
+    progress("config 1")
+    per, copies, R, secs = bench_config1(torch, qk, synth, lib, a.steps, a.warmup)
+    gbs, us = rate(per, R, a.steps, secs)
     out = {
         "metric": "k-quant GEMV GB/s (% of 8 TB/s); prefill int8 TOPS; decode tok/s",
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
-        "ms_per_step": round(us / 1e3, 6), "higher_is_better": True, "scaling": "weak",
+        "ms_per_step": round(secs / a.steps * 1e3, 6), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": "config1 decode GEMV set: Q4_K 3584x1024 x2, Q6_K 1024x3584, "
                                "Q5_K 2048x1024/512x1024/1024x2048, Q8_0 1024x1024, batch 1",
-                   "weight_copies": copies, "bytes_per_step": per, "parallelism": "single GPU"},
+                   "weight_copies": copies, "bytes_per_launch": per, "launches_per_step": R,
+                   "step": "one HIP-graph replay of launches_per_step rotating launches",
+                   "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": CONFIG1_TRAFFIC_BYTES,
-                     "kernel": "k_gemv<true, false> (one launch per step)", "us_per_launch": round(us, 3)},
+                     "kernel": "k_gemv<true, false> (one launch)", "us_per_launch": round(us, 3)},
         "tier": lib.tier_label(),
     }
+    if a.only == "config1":
+        print(json.dumps(out))
+        return
     if not a.no_extra:
         extra = {}
-        pw, cw, sw = bench_config1(torch, qk, synth, lib, a.steps, a.warmup, warm=True)
-        extra["config1_warm_mall"] = {"GB/s": round(pw * a.steps / sw / 1e9, 2),
-                                      "us_per_launch": round(sw / a.steps * 1e6, 3), "copies": cw,
+        progress("config 1 with quantize, warm MALL")
+        pq, cq, Rq, sq, nl = bench_config1_quantize(torch, qk, synth, lib, a.steps, a.warmup)
+        g, u = rate(pq, Rq, a.steps, sq)
+        extra["config1_with_quantize"] = {"GB/s": round(g, 2), "us_per_step_unit": round(u, 3),
+                                          "frac": round(g / HBM_PEAK_GBS, 4), "launches": nl,
+                                          "bytes": pq, "copies": cq,
+                                          "note": "fp32 rows in: Q8_K/Q8_0 quantize launches + the group launch"}
+        pw, cw, Rw, sw = bench_config1(torch, qk, synth, lib, a.steps, a.warmup, warm=True)
+        g, u = rate(pw, Rw, a.steps, sw)
+        extra["config1_warm_mall"] = {"GB/s": round(g, 2), "us_per_launch": round(u, 3), "copies": cw,
                                       "note": "one weight copy, resident in the 256 MB MALL; not HBM"}
-        p0, c0, s0 = bench_config0(torch, qk, synth, lib, a.steps, a.warmup)
-        extra["config0_q4k_gemv"] = {"GB/s": round(p0 * a.steps / s0 / 1e9, 2),
-                                     "us_per_launch": round(s0 / a.steps * 1e6, 3), "copies": c0}
-        st2 = max(20, a.steps // 20)
-        p2, c2, s2 = bench_config2(torch, qk, synth, lib, st2, 5)
-        extra["config2_lmhead_q6k_argmax_top40"] = {"GB/s": round(p2 * st2 / s2 / 1e9, 2),
-                                                    "us_per_call": round(s2 / st2 * 1e6, 3), "copies": c2}
+        progress("config 0")
+        p0, c0, R0, s0 = bench_gemv(torch, qk, synth, lib, a.steps, a.warmup, 12, 3584, 1024, 3.2)
+        g, u = rate(p0, R0, a.steps, s0)
+        extra["config0_q4k_gemv"] = {"GB/s": round(g, 2), "us_per_launch": round(u, 3),
+                                     "frac": round(g / HBM_PEAK_GBS, 4), "copies": c0, "launches_per_step": R0}
+        progress("config 2")
+        st2 = max(10, a.steps // 10)
+        p2, c2, R2, s2 = bench_config2(torch, qk, synth, lib, st2, 3)
+        g, u = rate(p2, R2, st2, s2)
+        extra["config2_lmhead_q6k_argmax_top40"] = {"GB/s": round(g, 2), "us_per_call": round(u, 3),
+                                                    "frac": round(g / HBM_PEAK_GBS, 4), "copies": c2,
+                                                    "launches_per_step": R2, "steps": st2}
+        p2g, c2g, R2g, s2g = bench_gemv(torch, qk, synth, lib, st2, 3, 14, 248320, 1024, 37.0)
+        g, u = rate(p2g, R2g, st2, s2g)
+        extra["config2_lmhead_gemv_only"] = {"GB/s": round(g, 2), "us_per_launch": round(u, 3),
+                                             "frac": round(g / HBM_PEAK_GBS, 4), "copies": c2g}
+        progress("Q4_K streaming GEMV")
+        pq4, cq4, Rq4, sq4 = bench_gemv(torch, qk, synth, lib, st2, 3, 12, 248320, 1024, 30.0)
+        g, u = rate(pq4, Rq4, st2, sq4)
+        extra["q4k_gemv_248320x1024_stream"] = {"GB/s": round(g, 2), "us_per_launch": round(u, 3),
+                                                "frac": round(g / HBM_PEAK_GBS, 4), "copies": cq4,
+                                                "bytes": pq4}
+        progress("config 3")
         peak = mfma_peak()
         if peak:
             extra["mfma_int8_peak_measured"] = peak
         peak_tops = peak["mfma_i32_32x32x32_i8_tops"] if peak else None
-        extra.update(config3_extras(torch, qk, synth, lib, max(20, a.steps // 10), peak_tops))
+        extra.update(config3_extras(torch, qk, synth, lib, max(10, a.steps // 10), 3, peak_tops))
+        if not a.no_e2e:
+            progress("config 4 end to end")
+            extra["config4_e2e"] = e2e()
         out["extra"] = extra
     if not a.no_cpu:
+        progress("CPU reference")
         out["cpu_baseline"] = cpu_baseline(synth, a.cpu_seconds)
+        if not a.no_extra:
+            out["cpu_extra"] = cpu_extras(synth)
+            out["cpu_host"] = host_description()
     print(json.dumps(out))
 
 

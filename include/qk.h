@@ -106,11 +106,13 @@ enum {
 
 /* ---- lifecycle ------------------------------------------------------ */
 
-/* Select `device`, pick the tier (QK_TIER_AUTO) and create the library's
- * stream. Replaces simd_init() (simd/simd.c:191), called from
- * slm_model_load (slm/model.c:1134). Idempotent. */
+/* Select `device` and pick the tier (QK_TIER_AUTO). Replaces simd_init()
+ * (simd/simd.c:191), called from slm_model_load (slm/model.c:1134).
+ * Idempotent for the same device; another device needs hip_qk_shutdown
+ * first. */
 int         hip_qk_init(int device);
-/* Free every registered weight and the stream. */
+/* Wait for the device, then free every registered weight, every host
+ * thread's seam stream and staging, and all scratch. */
 void        hip_qk_shutdown(void);
 /* "gfx950 <name> / tier AVX2-FMA"; replaces simd_dispatch_label()
  * (simd/simd.c:234). */
@@ -202,8 +204,18 @@ int hip_dequant_q6k(const void *w, int64_t nblocks, float *y, void *stream);
  *   topk_idx/topk_val (optional when topk == 0): the topk largest
  *            logits, value-descending, ties broken by lower index; the
  *            set equals topk_collect's (slm/sampler.c:70-93) whenever
- *            the topk-th value is not tied.
- * 1 <= topk <= QK_TOPK_MAX. All outputs are device pointers. */
+ *            the topk-th value is not tied and no logit is NaN. NaN
+ *            logits rank below every number here; topk_collect instead
+ *            keeps a NaN that lands in its first k slots and, once one
+ *            holds its minimum slot, replaces nothing more.
+ * 0 <= topk <= QK_TOPK_MAX. All outputs are device pointers.
+ * Selection scratch is kept per stream: calls on different streams run
+ * concurrently without sharing it. A stream's scratch is replaced (never
+ * freed before hip_qk_shutdown) when a call needs more, so the first call
+ * on a stream, and a first call with logits == NULL or a larger n,
+ * allocate; later calls of the same or smaller size do not, and may be
+ * captured in a HIP graph on that stream. A call that would allocate on a
+ * stream that is capturing fails with QK_ERR_ARG and enqueues nothing. */
 #define QK_TOPK_MAX 256
 int hip_lmhead_q6k_argmax_topk(const void *w, int64_t n, int64_t k,
                                const void *xq, int topk, float *logits,
@@ -219,6 +231,13 @@ int hip_lmhead_q6k_argmax_topk(const void *w, int64_t n, int64_t k,
 int hip_qk_register_weight(const void *host_w, int type, int64_t k,
                            int64_t n);
 int hip_qk_unregister_weight(const void *host_w);
+/* Drop every registered weight whose host bytes overlap
+ * [base, base + bytes) and free its device copy; returns how many were
+ * dropped (0 when libqk is not initialized). The host seam calls it
+ * before the reference unmaps a GGUF file (gguf_close, slm/gguf.c:263),
+ * so a model loaded later at the same addresses is uploaded afresh.
+ * Waits for host-seam calls still using those weights. */
+int hip_qk_unregister_range(const void *base, size_t bytes);
 /* Device address of a registered weight (NULL if unknown). */
 const void *hip_qk_device_weight(const void *host_w);
 
@@ -226,7 +245,9 @@ const void *hip_qk_device_weight(const void *host_w);
  * tensor_matmul_q4k_f32 / _q5k_ / _q6k_ / _q8_0_ compute
  * (slm/tensor.c:827, 898, 1012, 952), for x of n_tok rows of k floats
  * in host memory and out in host memory. Registers the weight on first
- * use. Synchronous. */
+ * use. Synchronous. Each host thread runs its calls on a stream of its
+ * own (the reference's contexts are single-threaded, slm/slm.h:33-36), so
+ * calls from several threads overlap on the GPU. */
 int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f,
                        int64_t k, const float *x, int64_t n_tok,
                        float *out);

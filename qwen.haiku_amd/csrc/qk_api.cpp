@@ -6,12 +6,15 @@
 // the float-epilogue tier.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <shared_mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #if defined(__x86_64__) || defined(__i386__)
 #include <cpuid.h>
@@ -31,22 +34,40 @@ struct Weight {
     void *dev;
 };
 
-struct State {
-    std::mutex mu;
-    bool init = false;
-    int device = -1;
-    int tier = QK_TIER_SCALAR;
+// Host-seam working set of one host thread: its own stream (the
+// reference's contexts are single-threaded each, slm/slm.h:33-36, so a
+// thread stands for a context), device scratch and pinned staging.
+struct Lane {
     hipStream_t stream = nullptr;
-    std::string label;
-    std::unordered_map<const void *, Weight> weights;
-    // host-seam scratch (grown on demand)
     void *dx = nullptr;   size_t dx_cap = 0;
     void *dxq = nullptr;  size_t dxq_cap = 0;
     void *dy = nullptr;   size_t dy_cap = 0;
     void *dsel = nullptr; size_t dsel_cap = 0;
-    // pinned host staging of the host seam: x goes in, y comes out
     void *hx = nullptr;   size_t hx_cap = 0;
     void *hy = nullptr;   size_t hy_cap = 0;
+};
+
+// LM-head selection scratch of one caller stream.
+struct Sel {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+struct State {
+    std::mutex mu;                     // init/shutdown, lanes, sel, retired
+    std::shared_mutex wmu;             // the weight registry
+    bool init = false;
+    int device = -1;
+    std::atomic<int> tier{QK_TIER_SCALAR};
+    std::atomic<uint64_t> gen{0};      // bumped by shutdown: thread-local lanes go stale
+    std::string label;
+    std::unordered_map<const void *, Weight> weights;
+    std::vector<Lane *> lanes;
+    std::unordered_map<hipStream_t, Sel> sel;
+    // Scratch replaced by a larger one. Work already enqueued (or a
+    // captured graph) may still point at it, so it is freed only at
+    // shutdown.
+    std::vector<void *> retired;
     int cu_count = 256;
 };
 
@@ -153,6 +174,8 @@ int grow_host(void **p, size_t *cap, size_t need) {
     return QK_OK;
 }
 
+// Device scratch of at least `need` bytes (contents not kept). The old
+// buffer is freed: only for buffers that no enqueued work still uses.
 int grow(void **p, size_t *cap, size_t need) {
     if (*cap >= need) return QK_OK;
     if (*p) (void)hipFree(*p);
@@ -164,13 +187,67 @@ int grow(void **p, size_t *cap, size_t need) {
     return QK_OK;
 }
 
+// The calling thread's current device is the library's. HIP's current
+// device is per host thread, so a thread that reaches libqk first through
+// a seam call or a scratch allocation selects it here once.
+thread_local uint64_t t_dev_gen = ~0ull;
+
+int ensure_device() {
+    State &s = st();
+    const uint64_t g = s.gen.load();
+    if (t_dev_gen == g) return QK_OK;
+    HIP_OK(hipSetDevice(s.device), "hipSetDevice");
+    t_dev_gen = g;
+    return QK_OK;
+}
+
+// The host-seam lane of the calling thread, created on its first call.
+thread_local Lane *t_lane = nullptr;
+thread_local uint64_t t_lane_gen = ~0ull;
+
+int my_lane(Lane **out) {
+    State &s = st();
+    int rc;
+    if ((rc = ensure_device())) return rc;
+    if (t_lane && t_lane_gen == s.gen.load()) {
+        *out = t_lane;
+        return QK_OK;
+    }
+    Lane *l = new Lane();
+    hipError_t e = hipStreamCreateWithFlags(&l->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete l;
+        return hip_fail(e, "hipStreamCreate(lane)");
+    }
+    {
+        std::lock_guard<std::mutex> lk(s.mu);
+        s.lanes.push_back(l);
+    }
+    t_lane = l;
+    t_lane_gen = s.gen.load();
+    *out = l;
+    return QK_OK;
+}
+
+void free_lane(Lane *l) {
+    (void)hipStreamSynchronize(l->stream);
+    void *dev[] = {l->dx, l->dxq, l->dy, l->dsel};
+    for (void *p : dev)
+        if (p) (void)hipFree(p);
+    void *hst[] = {l->hx, l->hy};
+    for (void *p : hst)
+        if (p) (void)hipHostFree(p);
+    (void)hipStreamDestroy(l->stream);
+    delete l;
+}
+
 int matvec(int type, const void *w, int64_t n, int64_t k, const void *xq, float *y, void *s) {
     int rc = require_init();
     if (rc) return rc;
     if ((rc = check_mat(type, w, n, k, xq, y))) return rc;
     qk::GemvArgs a{};
     a.count = 1;
-    a.fused = fused_of(st().tier);
+    a.fused = fused_of(st().tier.load());
     a.d[0].type = type;
     a.d[0].n = n;
     a.d[0].k = k;
@@ -182,14 +259,17 @@ int matvec(int type, const void *w, int64_t n, int64_t k, const void *xq, float 
     return QK_OK;
 }
 
+// Token bound of the GEMM (grid.y = token tiles of 64).
+constexpr int64_t GEMM_MAX_M = 65535LL * 64;
+
 int matmul(int type, const void *w, int64_t n, int64_t k, const void *xq, int64_t m, float *y, void *s) {
     int rc = require_init();
     if (rc) return rc;
     if ((rc = check_mat(type, w, n, k, xq, y))) return rc;
-    if (m < 1 || m > 65535LL * 64) return fail(QK_ERR_ARG, "m=%lld tokens (1..%lld)", (long long)m, 65535LL * 64);
+    if (m < 1 || m > GEMM_MAX_M) return fail(QK_ERR_ARG, "m=%lld tokens (1..%lld)", (long long)m, GEMM_MAX_M);
     if (type == QK_TYPE_Q8_0) return fail(QK_ERR_UNSUPPORTED, "no Q8_0 GEMM; use hip_matvec_q8_0 per token");
-    HIP_OK(qk::launch_gemm(type, static_cast<const uint8_t *>(w), n, k,
-                           static_cast<const uint8_t *>(xq), m, y, fused_of(st().tier), stream_of(s)),
+    HIP_OK(qk::launch_gemm(type, static_cast<const uint8_t *>(w), n, k, static_cast<const uint8_t *>(xq), m, y,
+                           fused_of(st().tier.load()), stream_of(s)),
            "gemm launch");
     return QK_OK;
 }
@@ -201,7 +281,10 @@ extern "C" {
 int hip_qk_init(int device) {
     State &s = st();
     std::lock_guard<std::mutex> lk(s.mu);
-    if (s.init && s.device == device) return QK_OK;
+    if (s.init) {
+        if (s.device == device) return QK_OK;
+        return fail(QK_ERR_ARG, "libqk is initialized on device %d; hip_qk_shutdown first", s.device);
+    }
     int count = 0;
     HIP_OK(hipGetDeviceCount(&count), "hipGetDeviceCount");
     if (device < 0 || device >= count) return fail(QK_ERR_ARG, "device %d of %d", device, count);
@@ -210,11 +293,12 @@ int hip_qk_init(int device) {
     HIP_OK(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(QK_ERR_UNSUPPORTED, "libqk is built for gfx950, device is %s", prop.gcnArchName);
-    if (!s.stream) HIP_OK(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking), "hipStreamCreate");
     s.device = device;
     s.cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
-    s.tier = detect_tier();
-    s.label = std::string(prop.gcnArchName) + " " + prop.name + " / tier " + hip_qk_tier_label(s.tier);
+    s.tier.store(detect_tier());
+    s.label = std::string(prop.gcnArchName) + " " + prop.name + " / tier " + hip_qk_tier_label(s.tier.load());
+    s.gen.fetch_add(1);
+    t_dev_gen = s.gen.load();
     s.init = true;
     return QK_OK;
 }
@@ -223,23 +307,18 @@ void hip_qk_shutdown(void) {
     State &s = st();
     std::lock_guard<std::mutex> lk(s.mu);
     if (!s.init) return;
-    (void)hipStreamSynchronize(s.stream);
+    std::unique_lock<std::shared_mutex> wl(s.wmu);
+    (void)hipSetDevice(s.device);
+    (void)hipDeviceSynchronize();
+    for (Lane *l : s.lanes) free_lane(l);
+    s.lanes.clear();
+    for (auto &kv : s.sel) (void)hipFree(kv.second.p);
+    s.sel.clear();
+    for (void *p : s.retired) (void)hipFree(p);
+    s.retired.clear();
     for (auto &kv : s.weights) (void)hipFree(kv.second.dev);
     s.weights.clear();
-    void **bufs[] = {&s.dx, &s.dxq, &s.dy, &s.dsel};
-    for (void **b : bufs) {
-        if (*b) (void)hipFree(*b);
-        *b = nullptr;
-    }
-    s.dx_cap = s.dxq_cap = s.dy_cap = s.dsel_cap = 0;
-    void **hbufs[] = {&s.hx, &s.hy};
-    for (void **b : hbufs) {
-        if (*b) (void)hipHostFree(*b);
-        *b = nullptr;
-    }
-    s.hx_cap = s.hy_cap = 0;
-    (void)hipStreamDestroy(s.stream);
-    s.stream = nullptr;
+    s.gen.fetch_add(1);                    // every thread's lane and device choice are stale
     s.init = false;
 }
 
@@ -259,11 +338,11 @@ const char *hip_qk_tier_label(int tier) {
 int hip_qk_set_tier(int tier) {
     if (tier == QK_TIER_AUTO) tier = detect_tier();
     if (tier < QK_TIER_SCALAR || tier > QK_TIER_AVXVNNI) return fail(QK_ERR_ARG, "tier %d", tier);
-    st().tier = tier;
+    st().tier.store(tier);
     return QK_OK;
 }
 
-int hip_qk_get_tier(void) { return st().tier; }
+int hip_qk_get_tier(void) { return st().tier.load(); }
 
 int hip_quantize_q8k(const float *x, int64_t m, int64_t k, void *xq, void *stream) {
     int rc = require_init();
@@ -307,7 +386,7 @@ int hip_matvec_group(const qk_gemv_desc *desc, int count, void *stream) {
         return fail(QK_ERR_ARG, "group count %d (1..%d)", count, QK_GROUP_MAX);
     qk::GemvArgs a{};
     a.count = count;
-    a.fused = fused_of(st().tier);
+    a.fused = fused_of(st().tier.load());
     for (int i = 0; i < count; i++) {
         const qk_gemv_desc &d = desc[i];
         if ((rc = check_mat(d.type, d.w, d.n, d.k, d.xq, d.y))) {
@@ -351,26 +430,67 @@ int hip_dequant_q6k(const void *w, int64_t nb, float *y, void *s) { return dequa
 }  // extern "C"
 
 namespace {
-// Body of the LM-head entry point; the caller holds st().mu.
-int lmhead_locked(const void *w, int64_t n, int64_t k, const void *xq, int topk, float *logits,
-                  int32_t *argmax, int32_t *topk_idx, float *topk_val, hipStream_t stream) {
-    State &s = st();
-    int rc;
+
+int check_lmhead_outputs(int64_t n, int topk, const int32_t *argmax, const int32_t *topk_idx,
+                         const float *topk_val) {
     if (!argmax) return fail(QK_ERR_ARG, "argmax output is required");
     if (topk < 0 || topk > QK_TOPK_MAX || topk > n) return fail(QK_ERR_ARG, "topk=%d", topk);
     if (topk > 0 && (!topk_idx || !topk_val)) return fail(QK_ERR_ARG, "top-k outputs are required");
-    // Logits always go to device memory: the caller's buffer, or scratch.
+    return QK_OK;
+}
+
+// LM head on `stream` with selection scratch `scratch` (at least
+// lmhead_cand_bytes(n, topk) bytes, plus n floats of logits when `logits`
+// is NULL, placed at the first 256-byte boundary past the selection part).
+int lmhead_launch(const void *w, int64_t n, int64_t k, const void *xq, int topk, float *logits, int32_t *argmax,
+                  int32_t *topk_idx, float *topk_val, void *scratch, hipStream_t stream) {
+    int rc;
     const size_t sel = qk::lmhead_cand_bytes(n, topk);
-    const size_t lbytes = logits ? 0 : (size_t)n * sizeof(float);
-    if ((rc = grow(&s.dsel, &s.dsel_cap, sel + lbytes + 256))) return rc;
     float *lg = logits ? logits
-                       : reinterpret_cast<float *>(static_cast<uint8_t *>(s.dsel) + ((sel + 255) & ~(size_t)255));
+                       : reinterpret_cast<float *>(static_cast<uint8_t *>(scratch) + ((sel + 255) & ~(size_t)255));
     if ((rc = check_mat(QK_TYPE_Q6_K, w, n, k, xq, lg))) return rc;
     HIP_OK(qk::launch_lmhead(static_cast<const uint8_t *>(w), n, k, static_cast<const uint8_t *>(xq), topk, lg,
-                             argmax, topk_idx, topk_val, s.dsel, fused_of(s.tier), stream),
+                             argmax, topk_idx, topk_val, scratch, fused_of(st().tier.load()), stream),
            "lmhead launch");
     return QK_OK;
 }
+
+size_t lmhead_scratch_bytes(int64_t n, int topk, bool own_logits) {
+    const size_t sel = qk::lmhead_cand_bytes(n, topk);
+    return ((sel + 255) & ~(size_t)255) + (own_logits ? (size_t)n * sizeof(float) : 0);
+}
+
+// Selection scratch of `stream` with room for `need` bytes. A stream keeps
+// one buffer; a larger request replaces it and retires the old one, which
+// earlier launches on the stream (or a graph captured from them) may still
+// use, so it stays allocated until hip_qk_shutdown. Two streams never
+// share a buffer.
+int stream_scratch(hipStream_t stream, size_t need, void **out) {
+    State &s = st();
+    int rc;
+    if ((rc = ensure_device())) return rc;
+    std::lock_guard<std::mutex> lk(s.mu);
+    Sel &e = s.sel[stream];
+    if (e.cap < need) {
+        // An allocation would invalidate a graph capture under way on the
+        // stream: refuse instead, before anything is enqueued.
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return fail(QK_ERR_ARG,
+                        "LM-head scratch for this stream must grow to %zu bytes, which allocates, and the stream "
+                        "is capturing: make one call of this size on the stream before capture",
+                        need);
+        const size_t sz = need + need / 4 + 4096;
+        void *p = nullptr;
+        HIP_OK(hipMalloc(&p, sz), "hipMalloc(lmhead scratch)");
+        if (e.p) s.retired.push_back(e.p);
+        e.p = p;
+        e.cap = sz;
+    }
+    *out = e.p;
+    return QK_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -380,20 +500,20 @@ int hip_lmhead_q6k_argmax_topk(const void *w, int64_t n, int64_t k, const void *
                                void *stream) {
     int rc = require_init();
     if (rc) return rc;
-    std::lock_guard<std::mutex> lk(st().mu);
-    return lmhead_locked(w, n, k, xq, topk, logits, argmax, topk_idx, topk_val, stream_of(stream));
+    if ((rc = check_lmhead_outputs(n, topk, argmax, topk_idx, topk_val))) return rc;
+    if (n < 1) return fail(QK_ERR_ARG, "empty matrix (n=%lld)", (long long)n);
+    void *scratch = nullptr;
+    if ((rc = stream_scratch(stream_of(stream), lmhead_scratch_bytes(n, topk, logits == nullptr), &scratch)))
+        return rc;
+    return lmhead_launch(w, n, k, xq, topk, logits, argmax, topk_idx, topk_val, scratch, stream_of(stream));
 }
 
 // ---- host seam ---------------------------------------------------------------
 
-int hip_qk_register_weight(const void *host_w, int type, int64_t k, int64_t n) {
-    int rc = require_init();
-    if (rc) return rc;
-    if (!host_w) return fail(QK_ERR_ARG, "null weight");
-    if (block_bytes(type) == 0) return fail(QK_ERR_UNSUPPORTED, "unsupported tensor type %d", type);
-    if (k < 1 || n < 1 || k % block_elems(type)) return fail(QK_ERR_ARG, "bad weight shape");
+namespace {
+// Caller holds s.wmu exclusively.
+int register_locked(const void *host_w, int type, int64_t k, int64_t n) {
     State &s = st();
-    std::lock_guard<std::mutex> lk(s.mu);
     auto it = s.weights.find(host_w);
     if (it != s.weights.end()) {
         const Weight &w = it->second;
@@ -412,9 +532,53 @@ int hip_qk_register_weight(const void *host_w, int type, int64_t k, int64_t n) {
     return QK_OK;
 }
 
+int check_weight_args(const void *host_w, int type, int64_t k, int64_t n) {
+    if (!host_w) return fail(QK_ERR_ARG, "null weight");
+    if (block_bytes(type) == 0) return fail(QK_ERR_UNSUPPORTED, "unsupported tensor type %d", type);
+    if (k < 1 || n < 1 || k % block_elems(type)) return fail(QK_ERR_ARG, "bad weight shape");
+    return QK_OK;
+}
+
+// Look up the device copy of `host_w` under the registry's shared lock,
+// which the caller keeps for as long as it uses the copy, registering it
+// first (exclusive lock) when it is new. On success `rl` holds the lock.
+int acquire_weight(const void *host_w, int type, int64_t k, int64_t n, std::shared_lock<std::shared_mutex> &rl,
+                   Weight *out) {
+    State &s = st();
+    int rc;
+    for (int attempt = 0; attempt < 2; attempt++) {
+        rl = std::shared_lock<std::shared_mutex>(s.wmu);
+        auto it = s.weights.find(host_w);
+        if (it != s.weights.end()) {
+            const Weight &w = it->second;
+            if (w.type != type || w.k != k || w.n != n)
+                return fail(QK_ERR_ARG, "weight %p registered with a different shape/type", host_w);
+            *out = w;
+            return QK_OK;
+        }
+        rl.unlock();
+        std::unique_lock<std::shared_mutex> wl(s.wmu);
+        if ((rc = register_locked(host_w, type, k, n))) return rc;
+    }
+    return fail(QK_ERR_UNREGISTERED, "weight %p was unregistered during the call", host_w);
+}
+}  // namespace
+
+int hip_qk_register_weight(const void *host_w, int type, int64_t k, int64_t n) {
+    int rc = require_init();
+    if (rc) return rc;
+    if ((rc = check_weight_args(host_w, type, k, n))) return rc;
+    if ((rc = ensure_device())) return rc;
+    std::unique_lock<std::shared_mutex> wl(st().wmu);
+    return register_locked(host_w, type, k, n);
+}
+
 int hip_qk_unregister_weight(const void *host_w) {
     State &s = st();
-    std::lock_guard<std::mutex> lk(s.mu);
+    int rc;
+    if ((rc = require_init())) return rc;
+    if ((rc = ensure_device())) return rc;
+    std::unique_lock<std::shared_mutex> wl(s.wmu);
     auto it = s.weights.find(host_w);
     if (it == s.weights.end()) return fail(QK_ERR_UNREGISTERED, "weight %p is not registered", host_w);
     (void)hipFree(it->second.dev);
@@ -422,9 +586,29 @@ int hip_qk_unregister_weight(const void *host_w) {
     return QK_OK;
 }
 
+int hip_qk_unregister_range(const void *base, size_t bytes) {
+    State &s = st();
+    if (!s.init || !base || bytes == 0) return 0;
+    if (ensure_device()) return 0;
+    std::unique_lock<std::shared_mutex> wl(s.wmu);
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(base), hi = lo + bytes;
+    int count = 0;
+    for (auto it = s.weights.begin(); it != s.weights.end();) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(it->first), b = a + it->second.bytes;
+        if (a < hi && lo < b) {
+            (void)hipFree(it->second.dev);
+            it = s.weights.erase(it);
+            count++;
+        } else {
+            ++it;
+        }
+    }
+    return count;
+}
+
 const void *hip_qk_device_weight(const void *host_w) {
     State &s = st();
-    std::lock_guard<std::mutex> lk(s.mu);
+    std::shared_lock<std::shared_mutex> rl(s.wmu);
     auto it = s.weights.find(host_w);
     return it == s.weights.end() ? nullptr : it->second.dev;
 }
@@ -434,43 +618,50 @@ int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f, int64_t k, c
     int rc = require_init();
     if (rc) return rc;
     if (!x || !out || n_tok < 1) return fail(QK_ERR_ARG, "bad activation arguments");
-    if ((rc = hip_qk_register_weight(host_w, type, k, out_f))) return rc;
-    State &s = st();
-    std::lock_guard<std::mutex> lk(s.mu);
-    const Weight &w = s.weights.at(host_w);
+    if ((rc = check_weight_args(host_w, type, k, out_f))) return rc;
+    if (type != QK_TYPE_Q8_0 && n_tok > GEMM_MAX_M)
+        return fail(QK_ERR_ARG, "n_tok=%lld tokens (1..%lld)", (long long)n_tok, GEMM_MAX_M);
+    Lane *l = nullptr;
+    if ((rc = my_lane(&l))) return rc;
+    std::shared_lock<std::shared_mutex> rl;
+    Weight w;
+    if ((rc = acquire_weight(host_w, type, k, out_f, rl, &w))) return rc;
     const size_t xb = (size_t)(n_tok * k) * sizeof(float);
     const size_t qb = (size_t)(n_tok * act_bytes(type, k));
     const size_t yb = (size_t)(n_tok * out_f) * sizeof(float);
-    if ((rc = grow(&s.dx, &s.dx_cap, xb)) || (rc = grow(&s.dxq, &s.dxq_cap, qb)) ||
-        (rc = grow(&s.dy, &s.dy_cap, yb)) || (rc = grow_host(&s.hx, &s.hx_cap, xb)) ||
-        (rc = grow_host(&s.hy, &s.hy_cap, yb)))
+    if ((rc = grow(&l->dx, &l->dx_cap, xb)) || (rc = grow(&l->dxq, &l->dxq_cap, qb)) ||
+        (rc = grow(&l->dy, &l->dy_cap, yb)) || (rc = grow_host(&l->hx, &l->hx_cap, xb)) ||
+        (rc = grow_host(&l->hy, &l->hy_cap, yb)))
         return rc;
     // x through pinned memory: a decode row (<= 16 KB) is read by the
     // quantizer straight from host memory; a prefill chunk goes by DMA.
-    std::memcpy(s.hx, x, xb);
+    std::memcpy(l->hx, x, xb);
     void *hx_dev = nullptr;
-    HIP_OK(hipHostGetDevicePointer(&hx_dev, s.hx, 0), "hipHostGetDevicePointer");
+    HIP_OK(hipHostGetDevicePointer(&hx_dev, l->hx, 0), "hipHostGetDevicePointer");
     const float *dx = static_cast<const float *>(hx_dev);
     if (xb > 16384) {
-        HIP_OK(hipMemcpyAsync(s.dx, s.hx, xb, hipMemcpyHostToDevice, s.stream), "hipMemcpyAsync(x)");
-        dx = static_cast<const float *>(s.dx);
+        HIP_OK(hipMemcpyAsync(l->dx, l->hx, xb, hipMemcpyHostToDevice, l->stream), "hipMemcpyAsync(x)");
+        dx = static_cast<const float *>(l->dx);
     }
-    uint8_t *dxq = static_cast<uint8_t *>(s.dxq);
+    uint8_t *dxq = static_cast<uint8_t *>(l->dxq);
     // y likewise: a small output (decode rows, <= 64 KB) is written by the
     // kernel straight into pinned host memory; a larger one goes by DMA.
-    float *dy = static_cast<float *>(s.dy);
+    float *dy = static_cast<float *>(l->dy);
     const bool y_direct = yb <= 65536;
     if (y_direct) {
         void *hy_dev = nullptr;
-        HIP_OK(hipHostGetDevicePointer(&hy_dev, s.hy, 0), "hipHostGetDevicePointer");
+        HIP_OK(hipHostGetDevicePointer(&hy_dev, l->hy, 0), "hipHostGetDevicePointer");
         dy = static_cast<float *>(hy_dev);
     }
+    // the same contract as the device layer, on the device copy
+    if ((rc = check_mat(type, w.dev, out_f, k, dxq, dy))) return rc;
+    const int fused = fused_of(st().tier.load());
     if (type == QK_TYPE_Q8_0) {
-        HIP_OK(qk::launch_quantize_q8_0(dx, n_tok * (k / QK8_0), dxq, s.stream), "quantize");
+        HIP_OK(qk::launch_quantize_q8_0(dx, n_tok * (k / QK8_0), dxq, l->stream), "quantize");
         // tensor_matmul_q8_0_f32 has no batched form: up to 16 tokens per launch.
         for (int64_t t0 = 0; t0 < n_tok; t0 += QK_GROUP_MAX_DEV) {
             qk::GemvArgs a{};
-            a.fused = fused_of(s.tier);
+            a.fused = fused;
             a.count = (int32_t)((n_tok - t0) < QK_GROUP_MAX_DEV ? (n_tok - t0) : QK_GROUP_MAX_DEV);
             for (int i = 0; i < a.count; i++) {
                 a.d[i].type = type;
@@ -481,13 +672,13 @@ int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f, int64_t k, c
                 a.d[i].y = dy + (t0 + i) * out_f;
                 qk::gemv_plan(a.d[i]);
             }
-            HIP_OK(qk::launch_gemv(a, 1 << 20, s.stream), "gemv launch");
+            HIP_OK(qk::launch_gemv(a, 1 << 20, l->stream), "gemv launch");
         }
     } else {
-        HIP_OK(qk::launch_quantize_q8k(dx, n_tok * (k / QK_K), dxq, s.stream), "quantize");
+        HIP_OK(qk::launch_quantize_q8k(dx, n_tok * (k / QK_K), dxq, l->stream), "quantize");
         if (n_tok == 1) {
             qk::GemvArgs a{};
-            a.fused = fused_of(s.tier);
+            a.fused = fused;
             a.count = 1;
             a.d[0].type = type;
             a.d[0].n = out_f;
@@ -496,17 +687,17 @@ int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f, int64_t k, c
             a.d[0].xq = dxq;
             a.d[0].y = dy;
             qk::gemv_plan(a.d[0]);
-            HIP_OK(qk::launch_gemv(a, s.cu_count * 8, s.stream), "gemv launch");
+            HIP_OK(qk::launch_gemv(a, st().cu_count * 8, l->stream), "gemv launch");
         } else {
-            HIP_OK(qk::launch_gemm(type, static_cast<const uint8_t *>(w.dev), out_f, k, dxq, n_tok, dy,
-                                   fused_of(s.tier), s.stream),
+            HIP_OK(qk::launch_gemm(type, static_cast<const uint8_t *>(w.dev), out_f, k, dxq, n_tok, dy, fused,
+                                   l->stream),
                    "gemm launch");
         }
     }
     if (!y_direct)
-        HIP_OK(hipMemcpyAsync(s.hy, dy, yb, hipMemcpyDeviceToHost, s.stream), "hipMemcpyAsync(out)");
-    HIP_OK(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
-    std::memcpy(out, s.hy, yb);
+        HIP_OK(hipMemcpyAsync(l->hy, dy, yb, hipMemcpyDeviceToHost, l->stream), "hipMemcpyAsync(out)");
+    HIP_OK(hipStreamSynchronize(l->stream), "hipStreamSynchronize");
+    std::memcpy(out, l->hy, yb);
     return QK_OK;
 }
 
@@ -514,39 +705,43 @@ int hip_qk_lmhead_host(const void *host_w, int64_t n, int64_t k, const float *x,
                        float *logits, int32_t *argmax, int32_t *topk_idx, float *topk_val) {
     int rc = require_init();
     if (rc) return rc;
-    if (!x || !argmax) return fail(QK_ERR_ARG, "bad arguments");
-    if (topk < 0 || topk > QK_TOPK_MAX || topk > n) return fail(QK_ERR_ARG, "topk=%d", topk);
-    if (topk > 0 && (!topk_idx || !topk_val)) return fail(QK_ERR_ARG, "top-k outputs are required");
-    if ((rc = hip_qk_register_weight(host_w, QK_TYPE_Q6_K, k, n))) return rc;
-    State &s = st();
-    std::lock_guard<std::mutex> lk(s.mu);
-    const void *wdev = s.weights.at(host_w).dev;
+    if (!x) return fail(QK_ERR_ARG, "bad arguments");
+    if ((rc = check_lmhead_outputs(n, topk, argmax, topk_idx, topk_val))) return rc;
+    if ((rc = check_weight_args(host_w, QK_TYPE_Q6_K, k, n))) return rc;
+    Lane *l = nullptr;
+    if ((rc = my_lane(&l))) return rc;
+    std::shared_lock<std::shared_mutex> rl;
+    Weight w;
+    if ((rc = acquire_weight(host_w, QK_TYPE_Q6_K, k, n, rl, &w))) return rc;
     const size_t xb = (size_t)k * sizeof(float);
     const size_t qb = (size_t)act_bytes(QK_TYPE_Q6_K, k);
     // dy: logits (n) | argmax (1) | topk idx (QK_TOPK_MAX) | topk val (QK_TOPK_MAX)
     const size_t yb = (size_t)(n + 1 + 2 * QK_TOPK_MAX) * sizeof(float) + 64;
-    if ((rc = grow(&s.dx, &s.dx_cap, xb)) || (rc = grow(&s.dxq, &s.dxq_cap, qb)) ||
-        (rc = grow(&s.dy, &s.dy_cap, yb)))
+    // the lane's stream finishes every call before returning, so its
+    // scratch can be replaced freely
+    if ((rc = grow(&l->dx, &l->dx_cap, xb)) || (rc = grow(&l->dxq, &l->dxq_cap, qb)) ||
+        (rc = grow(&l->dy, &l->dy_cap, yb)) ||
+        (rc = grow(&l->dsel, &l->dsel_cap, lmhead_scratch_bytes(n, topk, false))))
         return rc;
-    HIP_OK(hipMemcpyAsync(s.dx, x, xb, hipMemcpyHostToDevice, s.stream), "hipMemcpyAsync(x)");
-    HIP_OK(qk::launch_quantize_q8k(static_cast<const float *>(s.dx), k / QK_K, static_cast<uint8_t *>(s.dxq),
-                                   s.stream),
+    HIP_OK(hipMemcpyAsync(l->dx, x, xb, hipMemcpyHostToDevice, l->stream), "hipMemcpyAsync(x)");
+    HIP_OK(qk::launch_quantize_q8k(static_cast<const float *>(l->dx), k / QK_K, static_cast<uint8_t *>(l->dxq),
+                                   l->stream),
            "quantize");
-    float *dl = static_cast<float *>(s.dy);
+    float *dl = static_cast<float *>(l->dy);
     int32_t *dam = reinterpret_cast<int32_t *>(dl + n);
     int32_t *dti = dam + 1;
     float *dtv = reinterpret_cast<float *>(dti + QK_TOPK_MAX);
-    if ((rc = lmhead_locked(wdev, n, k, s.dxq, topk, dl, dam, dti, dtv, s.stream))) return rc;
+    if ((rc = lmhead_launch(w.dev, n, k, l->dxq, topk, dl, dam, dti, dtv, l->dsel, l->stream))) return rc;
     if (logits)
-        HIP_OK(hipMemcpyAsync(logits, dl, (size_t)n * sizeof(float), hipMemcpyDeviceToHost, s.stream), "copy logits");
-    HIP_OK(hipMemcpyAsync(argmax, dam, sizeof(int32_t), hipMemcpyDeviceToHost, s.stream), "copy argmax");
+        HIP_OK(hipMemcpyAsync(logits, dl, (size_t)n * sizeof(float), hipMemcpyDeviceToHost, l->stream), "copy logits");
+    HIP_OK(hipMemcpyAsync(argmax, dam, sizeof(int32_t), hipMemcpyDeviceToHost, l->stream), "copy argmax");
     if (topk > 0) {
-        HIP_OK(hipMemcpyAsync(topk_idx, dti, (size_t)topk * sizeof(int32_t), hipMemcpyDeviceToHost, s.stream),
+        HIP_OK(hipMemcpyAsync(topk_idx, dti, (size_t)topk * sizeof(int32_t), hipMemcpyDeviceToHost, l->stream),
                "copy topk idx");
-        HIP_OK(hipMemcpyAsync(topk_val, dtv, (size_t)topk * sizeof(float), hipMemcpyDeviceToHost, s.stream),
+        HIP_OK(hipMemcpyAsync(topk_val, dtv, (size_t)topk * sizeof(float), hipMemcpyDeviceToHost, l->stream),
                "copy topk val");
     }
-    HIP_OK(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+    HIP_OK(hipStreamSynchronize(l->stream), "hipStreamSynchronize");
     return QK_OK;
 }
 

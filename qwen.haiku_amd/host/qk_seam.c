@@ -108,6 +108,22 @@ struct tensor *tensor_matmul_q8_0_f32(const q8_0_block *w, int64_t out_f, int64_
     return qk_seam_matmul(QK_TYPE_Q8_0, w, out_f, k, x);
 }
 
+/* Device copies are keyed by host address, and the reference borrows its
+ * weights from the GGUF mapping, so when that mapping goes (gguf_close,
+ * slm/gguf.c:263-275, from slm_model_unload, slm/model.c:1197-1205) the
+ * copies of every weight inside it are dropped first: a model mapped
+ * later at the same addresses is uploaded afresh instead of running on
+ * stale device weights. The reference's GGUF reader is included after
+ * this file, so its munmap calls reach this wrapper; <sys/mman.h> is
+ * included here first so that its declaration keeps the real name. */
+#include <sys/mman.h>
+
+static int qk_seam_munmap(void *addr, size_t len) {
+    (void)hip_qk_unregister_range(addr, len);
+    return munmap(addr, len);
+}
+#define munmap qk_seam_munmap
+
 /* Upload a weight matrix before the first forward pass (what
  * slm_model_load would do once per quantized tensor, slm/model.c:1130).
  * Optional: the first matmul with an unseen weight uploads it too. */
