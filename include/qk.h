@@ -215,12 +215,30 @@ int hip_dequant_q6k(const void *w, int64_t nblocks, float *y, void *stream);
  * on a stream, and a first call with logits == NULL or a larger n,
  * allocate; later calls of the same or smaller size do not, and may be
  * captured in a HIP graph on that stream. A call that would allocate on a
- * stream that is capturing fails with QK_ERR_ARG and enqueues nothing. */
+ * stream that is capturing fails with QK_ERR_ARG and enqueues nothing
+ * (hip_lmhead_q6k_argmax_topk_noalloc never allocates). */
 #define QK_TOPK_MAX 256
 int hip_lmhead_q6k_argmax_topk(const void *w, int64_t n, int64_t k,
                                const void *xq, int topk, float *logits,
                                int32_t *argmax, int32_t *topk_idx,
                                float *topk_val, void *stream);
+
+/* The LM head above with no allocation at all, for callers that cannot
+ * call hipMalloc: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation. It has no counterpart in the
+ * reference. Its selection scratch (and, when logits == NULL, the logits)
+ * live in a static device array of each GPU, about 1.1 MB, held until the
+ * process ends. With logits == NULL, n is at most QK_NOALLOC_MAX_N.
+ * Every call on one GPU shares that array, whichever stream it uses:
+ * calls that overlap in time on one GPU race, so keep them on one stream
+ * or order them. Same arguments and results as
+ * hip_lmhead_q6k_argmax_topk. */
+#define QK_NOALLOC_MAX_N 262144
+int hip_lmhead_q6k_argmax_topk_noalloc(const void *w, int64_t n, int64_t k,
+                                       const void *xq, int topk,
+                                       float *logits, int32_t *argmax,
+                                       int32_t *topk_idx, float *topk_val,
+                                       void *stream);
 
 /* ---- host seam ------------------------------------------------------ */
 

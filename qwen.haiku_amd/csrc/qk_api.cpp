@@ -96,6 +96,18 @@ int hip_fail(hipError_t e, const char *what) {
         if (e_ != hipSuccess) return hip_fail(e_, what); \
     } while (0)
 
+// Selection scratch of hip_lmhead_q6k_argmax_topk_noalloc: the argmax
+// partials, candidate keys and counter, then (when the caller passes no
+// logits buffer) up to QK_NOALLOC_MAX_N logits. One copy per GPU, held
+// for the life of the process. Host code never uses this name as an
+// address: hip_qk_init resolves each device's copy with
+// hipGetSymbolAddress and the entry point passes that pointer.
+constexpr size_t NOALLOC_SEL_BYTES = 40960;
+constexpr size_t NOALLOC_SCRATCH_BYTES = NOALLOC_SEL_BYTES + (size_t)QK_NOALLOC_MAX_N * sizeof(float);
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+constexpr int MAX_DEVICES = 64;
+void *g_noalloc[MAX_DEVICES];             // each device's `scratch`, set by hip_qk_init
+
 // detect_cpu + simd_init tier selection, simd/simd.c:142-170,208-229.
 int detect_tier() {
     int tier = QK_TIER_SCALAR;
@@ -293,6 +305,11 @@ int hip_qk_init(int device) {
     HIP_OK(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(QK_ERR_UNSUPPORTED, "libqk is built for gfx950, device is %s", prop.gcnArchName);
+    if (device < MAX_DEVICES && !g_noalloc[device]) {
+        void *p = nullptr;
+        HIP_OK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        g_noalloc[device] = p;
+    }
     s.device = device;
     s.cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     s.tier.store(detect_tier());
@@ -478,7 +495,8 @@ int stream_scratch(hipStream_t stream, size_t need, void **out) {
         if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
             return fail(QK_ERR_ARG,
                         "LM-head scratch for this stream must grow to %zu bytes, which allocates, and the stream "
-                        "is capturing: make one call of this size on the stream before capture",
+                        "is capturing: make one call of this size on the stream before capture, or use "
+                        "hip_lmhead_q6k_argmax_topk_noalloc",
                         need);
         const size_t sz = need + need / 4 + 4096;
         void *p = nullptr;
@@ -506,6 +524,26 @@ int hip_lmhead_q6k_argmax_topk(const void *w, int64_t n, int64_t k, const void *
     if ((rc = stream_scratch(stream_of(stream), lmhead_scratch_bytes(n, topk, logits == nullptr), &scratch)))
         return rc;
     return lmhead_launch(w, n, k, xq, topk, logits, argmax, topk_idx, topk_val, scratch, stream_of(stream));
+}
+
+int hip_lmhead_q6k_argmax_topk_noalloc(const void *w, int64_t n, int64_t k, const void *xq, int topk,
+                                       float *logits, int32_t *argmax, int32_t *topk_idx, float *topk_val,
+                                       void *stream) {
+    int rc = require_init();
+    if (rc) return rc;
+    if ((rc = check_lmhead_outputs(n, topk, argmax, topk_idx, topk_val))) return rc;
+    if (n < 1) return fail(QK_ERR_ARG, "empty matrix (n=%lld)", (long long)n);
+    const int dev = st().device;
+    void *p = dev < MAX_DEVICES ? g_noalloc[dev] : nullptr;
+    if (!p) return fail(QK_ERR_UNSUPPORTED, "no static scratch on device %d", dev);
+    if (!logits && n > QK_NOALLOC_MAX_N)
+        return fail(QK_ERR_ARG, "n=%lld rows without a logits buffer exceeds the static scratch (%d rows)",
+                    (long long)n, QK_NOALLOC_MAX_N);
+    if (lmhead_scratch_bytes(n, topk, logits == nullptr) > NOALLOC_SCRATCH_BYTES ||
+        qk::lmhead_cand_bytes(n, topk) > NOALLOC_SEL_BYTES)
+        return fail(QK_ERR_ARG, "static scratch too small for n=%lld", (long long)n);
+    // the kernels clear their own counter; nothing else must start at zero
+    return lmhead_launch(w, n, k, xq, topk, logits, argmax, topk_idx, topk_val, p, stream_of(stream));
 }
 
 // ---- host seam ---------------------------------------------------------------
