@@ -384,13 +384,17 @@ def host_description():
 
 
 def _cpu_backend():
+    """(kind, dispatch label, run, stop): run(type, w, n, k, x, threads) is
+    the reference's tensor_matmul_*_f32 at threads == 1 and its row dots
+    split over a persistent pool of `threads` threads otherwise; stop()
+    ends the pool."""
     oracle = _load("oracle/oracle.py", "qk_oracle_py")
     if oracle.Ref.available():
         R = oracle.Ref()
-        return "reference", R.label(), (lambda t, w, n, k, x, th: R.matmul(t, w, n, k, x, threads=th))
+        return "reference", R.label(), (lambda t, w, n, k, x, th: R.matmul(t, w, n, k, x, threads=th)), R.pool_stop
     O = oracle.Oracle()
     return "port", "oracle restatement", (lambda t, w, n, k, x, th: O.matmul(t, w, n, k, x, oracle.EPI_FUSED,
-                                                                              threads=th))
+                                                                              threads=th)), (lambda: None)
 
 
 def _cpu_rate(run, mats, threads, seconds, per_pass):
@@ -407,7 +411,7 @@ def _cpu_rate(run, mats, threads, seconds, per_pass):
 def cpu_baseline(synth, seconds=10.0):
     """The reference's tensor_matmul_*_f32 (one core, as shipped) over the
     config-1 set, repeated for a bounded time."""
-    kind, label, run = _cpu_backend()
+    kind, label, run, _ = _cpu_backend()
     mats = [(t, synth.blocks(t, n, k, seed=0, tag=i), n, k, synth.activations(1, k, seed=0, tag=i))
             for i, (t, n, k) in enumerate(CONFIG1)]
     per_set = sum(alg_bytes(t, n, k) for (t, n, k) in CONFIG1)
@@ -420,9 +424,10 @@ def cpu_baseline(synth, seconds=10.0):
 def cpu_extras(synth, seconds=2.0):
     """The CPU reference beside configs 0-3: one core (as shipped,
     LLM_PAR_FOR is a plain loop on Linux) and N cores (the reference's row
-    dots split over N threads by the harness; bit-identical, rows are
-    independent). Each figure is a bounded sample of about `seconds`."""
-    kind, label, run = _cpu_backend()
+    dots split over a persistent pool of N threads by the harness;
+    bit-identical, rows are independent). Each figure is a bounded sample
+    of about `seconds`."""
+    kind, label, run, stop = _cpu_backend()
     nth = cpu_threads()
     out = {"kind": kind, "dispatch": label, "n_core_threads": nth}
     c1 = [(t, synth.blocks(t, n, k, seed=0, tag=i), n, k, synth.activations(1, k, seed=0, tag=i))
@@ -457,6 +462,7 @@ def cpu_extras(synth, seconds=2.0):
             r, reps, dt = _cpu_rate(run, [(t, w3, n3, k3, x3)], th, seconds, ops)
             out[f"config3_{'q4k' if t == 12 else 'q6k'}_m{m3}_{th}core"] = {
                 "TOPS": round(r / 1e9 / 1e3, 4), "sample": f"{reps} x {ms} tokens of {m3}, {dt:.1f} s"}
+    stop()
     return out
 
 

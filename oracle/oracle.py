@@ -223,6 +223,9 @@ class Ref:
         L.ref_matmul.restype = C.c_int
         L.ref_matmul_threads.argtypes = [C.c_int, _vp, _i64, _i64, _vp, _i64, _vp, C.c_int]
         L.ref_matmul_threads.restype = C.c_int
+        L.ref_matmul_pool.argtypes = L.ref_matmul_threads.argtypes
+        L.ref_matmul_pool.restype = C.c_int
+        L.ref_pool_stop.restype = None
         L.ref_argmax.argtypes = [_vp, _i64]
         L.ref_argmax.restype = C.c_int32
         L.ref_topk_collect.argtypes = [_vp, _i64, C.c_int32, _vp, _vp]
@@ -290,10 +293,14 @@ class Ref:
         if threads <= 1:
             rc = self.L.ref_matmul(wtype, _ptr(w), n, k, _ptr(x), m, _ptr(out))
         else:
-            rc = self.L.ref_matmul_threads(wtype, _ptr(w), n, k, _ptr(x), m, _ptr(out), threads)
+            rc = self.L.ref_matmul_pool(wtype, _ptr(w), n, k, _ptr(x), m, _ptr(out), threads)
         if rc:
             raise RuntimeError("reference matmul failed")
         return out
+
+    def pool_stop(self):
+        """End the worker threads of matmul(threads > 1)."""
+        self.L.ref_pool_stop()
 
     def argmax(self, v):
         v = np.ascontiguousarray(v, np.float32)

@@ -200,6 +200,91 @@ int ref_matmul_threads(int type, const void *w, int64_t n, int64_t k,
     return 0;
 }
 
+/* The same row split on a persistent pool: nthreads - 1 workers are
+ * started once and spin (with pause) on a job generation counter, the
+ * calling thread takes the first row range, so a call costs no thread
+ * creation. Used by the N-core CPU baseline, where per-call thread
+ * creation would cost more than a decode GEMV's rows. ref_pool_stop()
+ * ends the workers. */
+#include <sched.h>
+#include <stdatomic.h>
+
+static struct {
+    int n;                                 /* workers (excluding the caller) */
+    pthread_t th[256];
+    struct rows_job jobs[256];
+    atomic_uint gen;
+    atomic_int done;
+    atomic_int stop;
+} g_pool;
+
+static void *pool_worker(void *p) {
+    const int id = (int)(intptr_t)p;
+    unsigned seen = 0;
+    for (;;) {
+        unsigned g;
+        int spins = 0;
+        while ((g = atomic_load_explicit(&g_pool.gen, memory_order_acquire)) == seen) {
+            if (atomic_load_explicit(&g_pool.stop, memory_order_relaxed)) return NULL;
+            if (++spins < 4096) __builtin_ia32_pause();
+            else sched_yield();
+        }
+        seen = g;
+        rows_worker(&g_pool.jobs[id]);
+        atomic_fetch_add_explicit(&g_pool.done, 1, memory_order_acq_rel);
+    }
+}
+
+void ref_pool_stop(void) {
+    if (g_pool.n == 0) return;
+    atomic_store(&g_pool.stop, 1);
+    for (int i = 1; i <= g_pool.n; i++) pthread_join(g_pool.th[i], NULL);
+    g_pool.n = 0;
+    atomic_store(&g_pool.stop, 0);
+}
+
+static int pool_start(int workers) {
+    if (g_pool.n == workers) return 0;
+    ref_pool_stop();
+    atomic_store(&g_pool.gen, 0);
+    for (int i = 1; i <= workers; i++) {
+        if (pthread_create(&g_pool.th[i], NULL, pool_worker, (void *)(intptr_t)i) != 0) {
+            g_pool.n = i - 1;
+            ref_pool_stop();
+            return -1;
+        }
+        g_pool.n = i;
+    }
+    return 0;
+}
+
+int ref_matmul_pool(int type, const void *w, int64_t n, int64_t k,
+                    const float *x, int64_t m, float *out, int nthreads) {
+    simd_init();
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    if (pool_start(nthreads - 1) != 0) return -1;
+    int q8_0 = (type == GGUF_TT_Q8_0);
+    int64_t nb = q8_0 ? k / QK8_0 : k / QK_K;
+    size_t xbytes = q8_0 ? (size_t)nb * sizeof(q8_0_block) : (size_t)nb * sizeof(q8k_block);
+    void *xq = malloc(xbytes);
+    if (!xq) return -1;
+    for (int64_t t = 0; t < m; t++) {
+        if (q8_0) tensor_quantize_row_q8_0(x + t * k, xq, k);
+        else      quantize_row_q8_K(x + t * k, xq, k);
+        for (int i = 0; i < nthreads; i++)
+            g_pool.jobs[i] = (struct rows_job){type, w, n, k, nb, xq, out + t * n,
+                                               n * i / nthreads, n * (i + 1) / nthreads};
+        atomic_store_explicit(&g_pool.done, 0, memory_order_relaxed);
+        atomic_fetch_add_explicit(&g_pool.gen, 1, memory_order_release);
+        rows_worker(&g_pool.jobs[0]);
+        while (atomic_load_explicit(&g_pool.done, memory_order_acquire) < nthreads - 1)
+            __builtin_ia32_pause();
+    }
+    free(xq);
+    return 0;
+}
+
 /* sample_argmax (slm/model.c:401) and topk_collect (slm/sampler.c:70)
  * on a 1-D view of v. */
 static struct tensor view1d(const float *v, int64_t n) {
