@@ -593,7 +593,7 @@ __device__ __forceinline__ void load_direct(Raw<13> &r, __amdgpu_buffer_rsrc_t r
     r.q0 = bl128(rs, off + 48 + 32 * j);
     r.q1 = bl128(rs, off + 64 + 32 * j);
 }
-template <int TYPE, int LP, bool FUSED>
+template <int TYPE, int LP, bool FUSED, bool LM>
 __device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best, bool keys) {
     constexpr int BB = TYPE == 12 ? Q4K_BYTES : Q5K_BYTES;
     constexpr int P = 1 << LP;
@@ -665,6 +665,27 @@ __device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t
     };
     if (ntile >= ntiles) {                             // one item (a decode launch): no look-ahead
         item(cur, tile, it);
+        return;
+    }
+    if (LM && TYPE == 12 && niter == 1) {
+        // Q4_K rows of one item (k <= 4096), many items per wave (the
+        // streaming instantiation): two register sets in turn, so one
+        // item's loads stay in flight while the wave waits for the other's.
+        // Moving look-ahead registers into place would wait for every load
+        // at the latch.
+        Raw<TYPE> nxt;
+        while (true) {
+            load_direct(nxt, rsrc(ntile, 0), lofs, j);   // past the last tile: zeros, never stored
+            item(cur, tile, 0);
+            tile = ntile;
+            ntile += nwg;
+            if (tile >= ntiles) break;
+            load_direct(cur, rsrc(ntile, 0), lofs, j);
+            item(nxt, tile, 0);
+            tile = ntile;
+            ntile += nwg;
+            if (tile >= ntiles) break;
+        }
         return;
     }
     while (tile < ntiles) {
@@ -973,14 +994,14 @@ __global__ __launch_bounds__(256, LM ? 4 : 5) void k_gemv(uint32_t t0, uint32_t 
     const bool keys = amax_partial != nullptr;        // argmax keys (LM head) wanted
     switch (D.type) {
         case 12:
-            if (D.p == 4) run_kqd<12, 2, FUSED>(D, lw, D.nwg, lds, best, keys);
-            else if (D.p == 8) run_kqd<12, 3, FUSED>(D, lw, D.nwg, lds, best, keys);
-            else run_kqd<12, 4, FUSED>(D, lw, D.nwg, lds, best, keys);
+            if (D.p == 4) run_kqd<12, 2, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
+            else if (D.p == 8) run_kqd<12, 3, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
+            else run_kqd<12, 4, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
             break;
         case 13:
-            if (D.p == 4) run_kqd<13, 2, FUSED>(D, lw, D.nwg, lds, best, keys);
-            else if (D.p == 8) run_kqd<13, 3, FUSED>(D, lw, D.nwg, lds, best, keys);
-            else run_kqd<13, 4, FUSED>(D, lw, D.nwg, lds, best, keys);
+            if (D.p == 4) run_kqd<13, 2, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
+            else if (D.p == 8) run_kqd<13, 3, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
+            else run_kqd<13, 4, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
             break;
         case 14:
             if (D.p == 4) run_kq<14, 2, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
@@ -1090,9 +1111,13 @@ static hipError_t launch_gemv_impl(GemvArgs &a, int max_wg_per_desc, uint64_t *a
     }
     a.lds_bytes = lds;
     if (grid_out) *grid_out = wg;
-    // the LM head (argmax keys wanted) runs the LM instantiation
-    auto kern = amax_partial ? (a.fused ? k_gemv<true, true> : k_gemv<false, true>)
-                             : (a.fused ? k_gemv<true, false> : k_gemv<false, false>);
+    // The LM head (argmax keys wanted) and streaming launches, whose waves
+    // loop over many items, run the LM instantiation (two register sets in
+    // turn); decode launches keep the leaner one.
+    bool stream = amax_partial != nullptr;
+    for (int i = 0; i < a.count; i++) stream = stream || a.d[i].ntiles > a.d[i].nwg;
+    auto kern = stream ? (a.fused ? k_gemv<true, true> : k_gemv<false, true>)
+                       : (a.fused ? k_gemv<true, false> : k_gemv<false, false>);
     hipLaunchKernelGGL(kern, dim3(wg), dim3(256), lds, s, tab[0], tab[1], tab[2], tab[3], tab[4], tab[5], tab[6],
                        tab[7], ka, amax_partial, zero_ctr);
     return hipGetLastError();
