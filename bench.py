@@ -199,39 +199,32 @@ def bench_config1(torch, qk, synth, lib, steps, warmup, warm=False):
 
 
 def bench_config1_quantize(torch, qk, synth, lib, steps, warmup):
-    """Config 1 from fp32 activations: each launch quantizes the layer's
-    activation rows (Q8_K for k = 1024, 3584, 2048; Q8_0 for k = 1024) and
-    then runs the seven GEMVs. Algorithmic bytes add the fp32 rows read
-    (4 B per element, once per distinct row) to the config-1 bytes; the
-    quantized rows are counted once, as in config 1."""
+    """Config 1 from fp32 activations in one dispatch
+    (hip_matvec_group_f32): the workgroups quantize the layer's activation
+    rows (Q8_K for k = 1024, 3584, 2048; Q8_0 for the Q8_0 matrix)
+    themselves, then run the seven GEMVs. Algorithmic bytes add the fp32
+    rows read (4 B per element, once per distinct row) to the config-1
+    bytes; the quantized rows are counted once, as in config 1."""
     wbytes = sum(weight_bytes(*s) for s in CONFIG1)
     copies = max(2, -(-MALL_DEFEAT_BYTES // wbytes))
     sets, xs = config1_mats(torch, synth, lib, copies, shared=True)
     per = sum(alg_bytes(*s) for s in CONFIG1) + sum(4 * x.numel() for x in xs.values())
-    q8k = {k: torch.empty((k // 256) * 292, dtype=torch.uint8, device="cuda") for k in xs}
-    q80 = torch.empty((1024 // 32) * 34, dtype=torch.uint8, device="cuda")
     descs = []
     for items in sets:
         arr = (qk.GemvDesc * len(items))()
         for i, (t, w, n, k, x) in enumerate(items):
             y = torch.empty(n, dtype=torch.float32, device="cuda")
             items[i] = (t, w, n, k, x, y)
-            xq = q80 if t == 8 else q8k[k]
-            arr[i] = qk.GemvDesc(t, 0, n, k, w.data_ptr(), xq.data_ptr(), y.data_ptr())
+            arr[i] = qk.GemvDesc(t, 0, n, k, w.data_ptr(), x.data_ptr(), y.data_ptr())
         descs.append(arr)
-    quants = [(lib.L.hip_quantize_q8k, xs[k], k, q8k[k]) for k in sorted(xs)] + \
-             [(lib.L.hip_quantize_q8_0, xs[1024], 1024, q80)]
-    R = replays_for(copies, 12.0)
+    R = replays_for(copies, 5.5)
 
     def launch(i, sp):
-        for f, x, k, out in quants:
-            if f(C.c_void_p(x.data_ptr()), 1, k, C.c_void_p(out.data_ptr()), sp):
-                raise RuntimeError(lib.last_error())
-        if lib.L.hip_matvec_group(descs[i % copies], len(CONFIG1), sp):
+        if lib.L.hip_matvec_group_f32(descs[i % copies], len(CONFIG1), sp):
             raise RuntimeError(lib.last_error())
 
     secs = GraphTimer(torch).time(launch, R, steps, warmup)
-    return per, copies, R, secs, len(quants) + 1
+    return per, copies, R, secs, 1
 
 
 def bench_gemv(torch, qk, synth, lib, steps, warmup, wtype, n, k, est_us):
@@ -579,10 +572,11 @@ def main():
         progress("config 1 with quantize, warm MALL")
         pq, cq, Rq, sq, nl = bench_config1_quantize(torch, qk, synth, lib, a.steps, a.warmup)
         g, u = rate(pq, Rq, a.steps, sq)
-        extra["config1_with_quantize"] = {"GB/s": round(g, 2), "us_per_step_unit": round(u, 3),
+        extra["config1_with_quantize"] = {"GB/s": round(g, 2), "us_per_launch": round(u, 3),
                                           "frac": round(g / HBM_PEAK_GBS, 4), "launches": nl,
                                           "bytes": pq, "copies": cq,
-                                          "note": "fp32 rows in: Q8_K/Q8_0 quantize launches + the group launch"}
+                                          "note": "fp32 rows in, one dispatch: each workgroup quantizes "
+                                                  "its row (hip_matvec_group_f32)"}
         pw, cw, Rw, sw = bench_config1(torch, qk, synth, lib, a.steps, a.warmup, warm=True)
         g, u = rate(pw, Rw, a.steps, sw)
         extra["config1_warm_mall"] = {"GB/s": round(g, 2), "us_per_launch": round(u, 3), "copies": cw,

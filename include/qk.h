@@ -174,6 +174,24 @@ typedef struct {
 } qk_gemv_desc;
 int hip_matvec_group(const qk_gemv_desc *desc, int count, void *stream);
 
+/* The same launch from fp32 activation rows: entry i computes
+ * y_i = W_i . quant(x_i), x_i being k_i floats (16-byte aligned; 4-byte
+ * for Q8_0). Each workgroup quantizes the row it needs into LDS, bit for
+ * bit as hip_quantize_q8k / hip_quantize_q8_0 would, so a decode layer's
+ * projections are one dispatch from the fp32 activations: the
+ * quantize-then-dot of tensor_matmul_*_f32 at n_tok == 1
+ * (slm/tensor.c:838-850) for up to QK_GROUP_MAX weights at once. Entries
+ * may share an x. */
+typedef struct {
+    int32_t     type;
+    int32_t     pad_;
+    int64_t     n, k;
+    const void *w;             /* device                              */
+    const float *x;            /* device, k floats                    */
+    float      *y;             /* device                              */
+} qk_gemv_desc_f32;
+int hip_matvec_group_f32(const qk_gemv_desc_f32 *desc, int count, void *stream);
+
 /* ---- device layer: chunked-prefill GEMM ----------------------------- */
 
 /* y[t*n + j] = row_dot(W row j, xq row t) for t < m, j < n: the token

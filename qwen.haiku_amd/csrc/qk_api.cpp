@@ -421,6 +421,33 @@ int hip_matvec_group(const qk_gemv_desc *desc, int count, void *stream) {
     return QK_OK;
 }
 
+int hip_matvec_group_f32(const qk_gemv_desc_f32 *desc, int count, void *stream) {
+    int rc = require_init();
+    if (rc) return rc;
+    if (!desc || count < 1 || count > QK_GROUP_MAX)
+        return fail(QK_ERR_ARG, "group count %d (1..%d)", count, QK_GROUP_MAX);
+    qk::GemvArgs a{};
+    a.count = count;
+    a.fused = fused_of(st().tier.load());
+    for (int i = 0; i < count; i++) {
+        const qk_gemv_desc_f32 &d = desc[i];
+        if ((rc = check_mat(d.type, d.w, d.n, d.k, d.x, d.y))) return fail(rc, "descriptor %d: %s", i, g_err.c_str());
+        // the workgroups read the row with 16-byte (Q8_K) or 4-byte (Q8_0) loads
+        if (!aligned(d.x, d.type == QK_TYPE_Q8_0 ? 4 : 16))
+            return fail(QK_ERR_ARG, "descriptor %d: x must be %d-byte aligned", i, d.type == QK_TYPE_Q8_0 ? 4 : 16);
+        a.d[i].type = d.type;
+        a.d[i].n = d.n;
+        a.d[i].k = d.k;
+        a.d[i].w = static_cast<const uint8_t *>(d.w);
+        a.d[i].xq = reinterpret_cast<const uint8_t *>(d.x);
+        a.d[i].y = d.y;
+        a.d[i].xf32 = 1;
+        qk::gemv_plan(a.d[i]);
+    }
+    HIP_OK(qk::launch_gemv(a, 1 << 20, stream_of(stream)), "gemv group launch");
+    return QK_OK;
+}
+
 int hip_matmul_q4k(const void *w, int64_t n, int64_t k, const void *xq, int64_t m, float *y, void *s) {
     return matmul(QK_TYPE_Q4_K, w, n, k, xq, m, y, s);
 }

@@ -156,6 +156,101 @@ __device__ __forceinline__ void scale_min(uint32_t s0, uint32_t s1, uint32_t s2,
     }
 }
 
+// ---- activation block quantizers (one wave / half-wave per block) --------
+// Both restate the reference bit for bit; the callers store the results
+// where their layout wants them (global Q8_K / Q8_0 rows, or an LDS copy
+// of a row inside a GEMV workgroup).
+
+// Largest value over the wave (inputs NaN-free): DPP within each 16-lane
+// row, then the four row results read as uniform values.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, __int_as_float(dpp_xor1(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_xor2(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_hmirror(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));  // row_mirror
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// One Q8_K block (quantize_row_q8_K, slm/tensor.c:683-720) by one wave,
+// elements 4 lane .. 4 lane + 3 in e[]. Results: `packed` = this lane's
+// four quants as bytes; `d` (wave-uniform); `bs` = bsums 2p | 2p+1 << 16
+// for lanes 8p (other lanes: don't care).
+//  * amax/xmax: the first element with the largest |x| (strict '>' in a
+//    sequential scan; NaN never compares greater, so it is never chosen).
+//    The wave takes the largest |x| (NaN as 0), then the first lane
+//    holding it (ballot) supplies its first such element.
+//  * iscale = -127/xmax, d = 1/iscale (IEEE division),
+//    q = clamp(nearest_int(iscale*x)), bsums over 16-element groups.
+__device__ __forceinline__ void q8k_block_wave(const float (&e)[4], int lane, uint32_t &packed, float &d,
+                                               uint32_t &bs) {
+    float a[4], la = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float ax = fabsf(e[i]);
+        a[i] = (ax != ax) ? 0.0f : ax;
+        la = fmaxf(la, a[i]);
+    }
+    const float amax = wave_max(la);
+    // this lane's first element at amax (scanning backwards keeps the first)
+    float mine = e[3];
+#pragma unroll
+    for (int i = 2; i >= 0; i--) mine = a[i] == amax ? e[i] : mine;
+    const uint64_t hit = __ballot(la == amax);
+    const int first = __builtin_ctzll(hit);            // amax == 0: lane 0, unused
+    const float xmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), first));
+    int32_t q[4] = {0, 0, 0, 0};
+    d = 0.0f;
+    if (amax != 0.0f) {
+        const float iscale = __fdiv_rn(-127.0f, xmax);
+        d = __fdiv_rn(1.0f, iscale);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int32_t t = nearest_int(__fmul_rn(iscale, e[i]));
+            q[i] = t > 127 ? 127 : (t < -128 ? -128 : t);
+        }
+    }
+    packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
+             ((uint32_t)(q[3] & 0xff) << 24);
+    // bsums[j] = sum of lanes 4j..4j+3; lane 8p gets bsums 2p, 2p+1 (lane
+    // 8p+4's sum arrives by DPP row_shl:4, inside the 16-lane row)
+    int32_t sm = q[0] + q[1] + q[2] + q[3];
+    sm += dpp_xor1(sm);
+    sm += dpp_xor2(sm);
+    const int32_t s_next = __builtin_amdgcn_mov_dpp(sm, 0x104, 0xF, 0xF, true);
+    bs = ((uint32_t)sm & 0xffffu) | ((uint32_t)s_next << 16);
+}
+
+// One Q8_0 block (tensor_quantize_row_q8_0, slm/tensor.c:930-950) by 32
+// lanes (lanes 0-31 and 32-63 of a wave take one block each): this lane's
+// quant and the block's d (before its fp16 store). d = amax/127,
+// id = 1/d (of the unrounded d), q = (int)roundf(x*id) (half away from
+// zero).
+__device__ __forceinline__ void q80_block_half(float v, int32_t &q, float &d) {
+    float a = fabsf(v);
+    a = (a != a) ? 0.0f : a;                           // '>' never picks NaN
+    // block maximum: DPP within each 16-lane row, then the two rows of
+    // this half-wave's block (read as uniform values)
+    a = fmaxf(a, __int_as_float(dpp_xor1(__float_as_int(a))));
+    a = fmaxf(a, __int_as_float(dpp_xor2(__float_as_int(a))));
+    a = fmaxf(a, __int_as_float(dpp_hmirror(__float_as_int(a))));
+    a = fmaxf(a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x140, 0xF, 0xF, true)));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 48));
+    a = (threadIdx.x & 32) ? fmaxf(r2, r3) : fmaxf(r0, r1);
+    d = __fdiv_rn(a, 127.0f);
+    const float id = (d != 0.0f) ? __fdiv_rn(1.0f, d) : 0.0f;
+    // Saturating conversion, as the reference's clang build behaves when
+    // d underflows and id = 1/d is inf.
+    const float r = roundf(__fmul_rn(v, id));
+    q = r >= 127.0f ? 127 : (r <= -128.0f ? -128 : (int32_t)r);
+}
+
 // ---- float epilogues (bit-exact per tier) --------------------------------
 // Q4_K/Q5_K super-block term. separate (scalar/AVX1, simd/quants.h:305,
 // simd/avx.c:654): rn(rn(d*isum) - rn(dmin*mins)); fused (AVX2/VNNI,

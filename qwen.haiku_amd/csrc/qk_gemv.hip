@@ -69,6 +69,45 @@ __device__ __forceinline__ void stage_q80(const uint8_t *__restrict__ xq, int nb
     }
 }
 
+// fp32 activation rows (hip_matvec_group_f32): the workgroup quantizes the
+// row it needs into LDS itself, bit for bit as the quantize launches would.
+// Q8_K blocks sit at a QXB-byte stride with the quants 16-byte aligned:
+// d @0 | qs[256] @16 | bsums[16] @272. Every wave of the workgroup calls
+// these (whole waves: the block quantizers use ballots and DPP).
+#define QXB 304
+__device__ __forceinline__ void stage_q8k_f32(const float *__restrict__ x, int nb, uint8_t *lds) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int b = wave; b < nb; b += 4) {
+        const float4 v = *(const QK_GLOBAL float4 *)(x + b * QK_K + 4 * lane);
+        const float e[4] = {v.x, v.y, v.z, v.w};
+        uint32_t packed, bs;
+        float d;
+        q8k_block_wave(e, lane, packed, d, bs);
+        uint8_t *o = lds + b * QXB;
+        *(QK_LDS uint32_t *)(o + 16 + 4 * lane) = packed;
+        if ((lane & 7) == 0) *(QK_LDS uint32_t *)(o + 272 + 4 * (lane >> 3)) = bs;
+        if (lane == 0) *(QK_LDS float *)(o) = d;
+    }
+}
+// Q8_0: the layout stage_q80 writes, qs[nb][32] | d[nb] (d rounded to
+// fp16 as the stored block holds it, then widened); each half-wave
+// quantizes one block.
+__device__ __forceinline__ void stage_q80_f32(const float *__restrict__ x, int nb, uint8_t *lds) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float *d_out = reinterpret_cast<float *>(lds + nb * 32);
+    for (int b0 = 2 * wave; b0 < nb; b0 += 8) {
+        const int b = b0 + (lane >> 5), l = lane & 31;
+        const float v = b < nb ? *(const QK_GLOBAL float *)(x + b * QK8_0 + l) : 0.0f;
+        int32_t q;
+        float d;
+        q80_block_half(v, q, d);
+        if (b < nb) {
+            *(QK_LDS uint8_t *)(lds + b * 32 + l) = (uint8_t)(q & 0xff);
+            if (l == 0) *(QK_LDS float *)(d_out + b) = h2f(f2h(d));
+        }
+    }
+}
+
 #define M4 0x0F0F0F0Fu
 
 __device__ __forceinline__ int32_t dot16(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
@@ -261,6 +300,28 @@ __device__ __forceinline__ void load_act(Act6 &x, __amdgpu_buffer_rsrc_t r, int 
     x.bh = bl32(r, o + 268 + 2 * s);
     x.d = __uint_as_float(bl32(r, o));
 }
+// The same fields from a row the workgroup quantized into LDS (QXB layout).
+__device__ __forceinline__ void load_act_lds(ActK &x, const uint8_t *l, int b, int j) {
+    const uint8_t *o = l + b * QXB;
+    x.a0 = *(const QK_LDS uint4 *)(o + 16 + 64 * j);
+    x.a1 = *(const QK_LDS uint4 *)(o + 32 + 64 * j);
+    x.a2 = *(const QK_LDS uint4 *)(o + 48 + 64 * j);
+    x.a3 = *(const QK_LDS uint4 *)(o + 64 + 64 * j);
+    x.bs0 = *(const QK_LDS uint32_t *)(o + 272 + 8 * j);
+    x.bs1 = *(const QK_LDS uint32_t *)(o + 276 + 8 * j);
+    x.d = *(const QK_LDS float *)(o);
+}
+__device__ __forceinline__ void load_act_lds(Act6 &x, const uint8_t *l, int b, int j) {
+    const uint8_t *o = l + b * QXB;
+    const int s = 8 * (j >> 1) + 2 * (j & 1);
+    x.a0 = *(const QK_LDS uint4 *)(o + 16 + 16 * s);
+    x.a1 = *(const QK_LDS uint4 *)(o + 32 + 16 * s);
+    x.a4 = *(const QK_LDS uint4 *)(o + 80 + 16 * s);
+    x.a5 = *(const QK_LDS uint4 *)(o + 96 + 16 * s);
+    x.bl = *(const QK_LDS uint32_t *)(o + 272 + 2 * s);
+    x.bh = *(const QK_LDS uint32_t *)(o + 280 + 2 * s);
+    x.d = *(const QK_LDS float *)(o);
+}
 template <int T> struct ActOf { typedef ActK type; };
 template <> struct ActOf<14> { typedef Act6 type; };
 
@@ -367,7 +428,7 @@ struct KDesc {
     int32_t nwg;
     int32_t lds_act;
     int32_t wg0;
-    int32_t pad;
+    int32_t xf32;          // 1: xq holds the fp32 row; the workgroup quantizes it into LDS
 };
 static_assert(sizeof(KDesc) == 64, "KDesc is one 64-byte scalar load");
 
@@ -433,7 +494,7 @@ __device__ __forceinline__ void gather_terms(float (&tg)[P], float t, int src0) 
 // the loads of the next item are in flight while the wave waits for the
 // current one's. The general loop must instead wait for all loads before
 // it moves the look-ahead registers into place.
-template <int TYPE, int LP, bool FUSED, bool LM>
+template <int TYPE, int LP, bool FUSED, bool LM, bool XF>
 __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best, bool keys) {
     constexpr int BB = TYPE == 12 ? Q4K_BYTES : (TYPE == 13 ? Q5K_BYTES : Q6K_BYTES);
     constexpr int P = 1 << LP;
@@ -472,13 +533,20 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
     // activation operands of super-block g first (those of every item
     // when a row is one item), then the first item's weights
     const __amdgpu_buffer_rsrc_t ar = act_rsrc(D.xq, nb * Q8K_BYTES);
+    // fp32 row: quantized into LDS after the first item's loads are issued
+    const uint8_t *xl = XF ? lds : nullptr;
     Act6 xa;
-    load_act(xa, ar, g, j);
+    if (!xl) load_act(xa, ar, g, j);
     int xit = 0;
     int tile = lw, it = 0;
     Span sp = span(tile, it);
     Chunk cur;
     chunk_load(cur, sp, lane);
+    if (xl) {
+        stage_q8k_f32(reinterpret_cast<const float *>(D.xq), nb, lds);
+        lds_barrier();
+        load_act_lds(xa, xl, g, j);
+    }
     int ntile = tile, nit = it + 1;
     if (nit == niter) { nit = 0; ntile += nwg; }
     Span nsp = span(ntile, nit);                       // computed while the loads are in flight
@@ -507,7 +575,8 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
         Raw<TYPE> r;
         read_sb(r, wb, sp.ofs + lofs, j);
         if (it != xit) {                               // rows of several items: next super-blocks
-            load_act(xa, ar, it * P + g, j);
+            if (xl) load_act_lds(xa, xl, it * P + g, j);
+            else load_act(xa, ar, it * P + g, j);
             xit = it;
         }
         // A group past the row end contributes +0.0: the sum starts at
@@ -593,7 +662,7 @@ __device__ __forceinline__ void load_direct(Raw<13> &r, __amdgpu_buffer_rsrc_t r
     r.q0 = bl128(rs, off + 48 + 32 * j);
     r.q1 = bl128(rs, off + 64 + 32 * j);
 }
-template <int TYPE, int LP, bool FUSED, bool LM>
+template <int TYPE, int LP, bool FUSED, bool LM, bool XF>
 __device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best, bool keys) {
     constexpr int BB = TYPE == 12 ? Q4K_BYTES : Q5K_BYTES;
     constexpr int P = 1 << LP;
@@ -626,12 +695,19 @@ __device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t
     // activation operands of super-block g first (those of every item
     // when a row is one item), then the first item's weights
     const __amdgpu_buffer_rsrc_t ar = act_rsrc(D.xq, nb * Q8K_BYTES);
+    // fp32 row: quantized into LDS after the first item's loads are issued
+    const uint8_t *xl = XF ? lds : nullptr;
     typename ActOf<TYPE>::type xa;
-    load_act(xa, ar, g, j);
+    if (!xl) load_act(xa, ar, g, j);
     int xit = 0;
     int tile = lw, it = 0;
     Raw<TYPE> cur;
     load_direct(cur, rsrc(tile, it), lofs, j);
+    if (xl) {
+        stage_q8k_f32(reinterpret_cast<const float *>(D.xq), nb, lds);
+        lds_barrier();
+        load_act_lds(xa, xl, g, j);
+    }
     int ntile = tile, nit = it + 1;
     if (nit == niter) { nit = 0; ntile += nwg; }
     float sum = 0.0f;
@@ -639,7 +715,8 @@ __device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t
     // first lane, which stores the row after its last item
     auto item = [&](const Raw<TYPE> &c, int tile, int it) __attribute__((always_inline)) {
         if (it != xit) {                               // rows of several items: next super-blocks
-            load_act(xa, ar, it * P + g, j);
+            if (xl) load_act_lds(xa, xl, it * P + g, j);
+            else load_act(xa, ar, it * P + g, j);
             xit = it;
         }
         // a group past the row end contributes +0.0 (as in run_kq)
@@ -711,7 +788,7 @@ __device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t
 //  fused (AVX2/VNNI): acc_s = fma((float)p_s, s_b, acc_s), then
 //        ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7));
 //  separate (scalar/AVX1): sum = sum + (float)(sum_s p_s) * s_b.
-template <bool FUSED>
+template <bool FUSED, bool XF>
 __device__ __forceinline__ void run_q80(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best, bool keys) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -737,7 +814,8 @@ __device__ __forceinline__ void run_q80(const KDesc &D, int lw, int nwg, uint8_t
     Span sp = span(tile, c);
     Chunk cur;
     chunk_load(cur, sp, lane);
-    stage_q80(D.xq, nb, lds);
+    if constexpr (XF) stage_q80_f32(reinterpret_cast<const float *>(D.xq), nb, lds);
+    else stage_q80(D.xq, nb, lds);
     __syncthreads();
     const QK_LDS uint32_t *aq = (const QK_LDS uint32_t *)(lds);
     const QK_LDS float *ad = (const QK_LDS float *)(lds + nb * 32);
@@ -847,7 +925,7 @@ __device__ __forceinline__ int32_t dpp_shl8(int32_t v) {
     return __builtin_amdgcn_mov_dpp(v, 0x108, 0xF, 0xF, true);   // row_shl:8
 }
 
-template <int NB, bool FUSED>
+template <int NB, bool FUSED, bool XF>
 __device__ __forceinline__ void run_q80r(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best, bool keys) {
     constexpr int ROWB = NB * Q80_BYTES;               // 544 or 1088
     const int lane = threadIdx.x & 63;
@@ -870,14 +948,19 @@ __device__ __forceinline__ void run_q80r(const KDesc &D, int lw, int nwg, uint8_
     constexpr int TOT = NB * 17, NR = (TOT + 255) / 256;
     const __amdgpu_buffer_rsrc_t ar = act_rsrc(D.xq, NB * Q80_BYTES);
     uint32_t av[NR];
+    if constexpr (!XF) {
 #pragma unroll
-    for (int u = 0; u < NR; u++)
-        av[u] = __builtin_amdgcn_raw_buffer_load_b16(ar, 2 * (256 * u + (int)threadIdx.x), 0, 0);
+        for (int u = 0; u < NR; u++)
+            av[u] = __builtin_amdgcn_raw_buffer_load_b16(ar, 2 * (256 * u + (int)threadIdx.x), 0, 0);
+    }
     int tile = lw;
     Span sp = span(tile);
     ChunkN<5> cur;
     chunk_load(cur, sp, lane);
-    {
+    if constexpr (XF) {
+        // fp32 row: quantized into the same layout after the weight loads
+        stage_q80_f32(reinterpret_cast<const float *>(D.xq), NB, lds);
+    } else {
         // qs[NB][32] as u16 pairs | d[NB] widened to float
         uint8_t *junk = lds + D.lds_act;
 #pragma unroll
@@ -968,7 +1051,9 @@ __device__ __forceinline__ int wg0_of(uint32_t t, int hi) { return (int)(hi ? t 
 // LM: the LM-head instantiation (one Q6_K matrix, many items per wave),
 // allowed 128 VGPRs for its two register sets; decode launches keep the
 // 5-wave bound.
-template <bool FUSED, bool LM>
+// XF: every descriptor's activations are fp32 rows, quantized by each
+// workgroup (hip_matvec_group_f32).
+template <bool FUSED, bool LM, bool XF>
 __global__ __launch_bounds__(256, LM ? 4 : 5) void k_gemv(uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3,
                                               uint32_t t4, uint32_t t5, uint32_t t6, uint32_t t7,
                                               KArgs args, uint64_t *__restrict__ amax_partial,
@@ -994,24 +1079,24 @@ __global__ __launch_bounds__(256, LM ? 4 : 5) void k_gemv(uint32_t t0, uint32_t 
     const bool keys = amax_partial != nullptr;        // argmax keys (LM head) wanted
     switch (D.type) {
         case 12:
-            if (D.p == 4) run_kqd<12, 2, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
-            else if (D.p == 8) run_kqd<12, 3, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
-            else run_kqd<12, 4, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
+            if (D.p == 4) run_kqd<12, 2, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
+            else if (D.p == 8) run_kqd<12, 3, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
+            else run_kqd<12, 4, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
             break;
         case 13:
-            if (D.p == 4) run_kqd<13, 2, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
-            else if (D.p == 8) run_kqd<13, 3, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
-            else run_kqd<13, 4, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
+            if (D.p == 4) run_kqd<13, 2, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
+            else if (D.p == 8) run_kqd<13, 3, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
+            else run_kqd<13, 4, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
             break;
         case 14:
-            if (D.p == 4) run_kq<14, 2, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
-            else if (D.p == 8) run_kq<14, 3, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
-            else run_kq<14, 4, FUSED, LM>(D, lw, D.nwg, lds, best, keys);
+            if (D.p == 4) run_kq<14, 2, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
+            else if (D.p == 8) run_kq<14, 3, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
+            else run_kq<14, 4, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
             break;
         default:
-            if (D.p == 4 && D.nb == 32) run_q80r<32, FUSED>(D, lw, D.nwg, lds, best, keys);
-            else if (D.p == 4) run_q80r<16, FUSED>(D, lw, D.nwg, lds, best, keys);
-            else run_q80<FUSED>(D, lw, D.nwg, lds, best, keys);
+            if (D.p == 4 && D.nb == 32) run_q80r<32, FUSED, XF>(D, lw, D.nwg, lds, best, keys);
+            else if (D.p == 4) run_q80r<16, FUSED, XF>(D, lw, D.nwg, lds, best, keys);
+            else run_q80<FUSED, XF>(D, lw, D.nwg, lds, best, keys);
             break;
     }
     if (amax_partial) {
@@ -1055,7 +1140,9 @@ void gemv_plan(GemvDesc &d) {
         while (p < 16 && p < d.nb) p *= 2;
         d.p = p;
         d.rows_per_tile = 4 * (16 / p);
-        d.lds_act = 0;                                 // activations go straight to registers
+        // activations go straight to registers, or (fp32 row) through the
+        // workgroup's quantized copy in LDS
+        d.lds_act = d.xf32 ? d.nb * QXB : 0;
     }
     d.tr = d.rows_per_tile;
     d.tile_cap = 0;
@@ -1105,7 +1192,7 @@ static hipError_t launch_gemv_impl(GemvArgs &a, int max_wg_per_desc, uint64_t *a
         k.nwg = d.nwg;
         k.lds_act = d.lds_act;
         k.wg0 = d.wg0;
-        k.pad = 0;
+        k.xf32 = d.xf32;
         const uint32_t sh = 16u * (uint32_t)(i & 1);
         tab[i >> 1] = (tab[i >> 1] & ~(0xffffu << sh)) | ((uint32_t)d.wg0 << sh);
     }
@@ -1116,8 +1203,11 @@ static hipError_t launch_gemv_impl(GemvArgs &a, int max_wg_per_desc, uint64_t *a
     // turn); decode launches keep the leaner one.
     bool stream = amax_partial != nullptr;
     for (int i = 0; i < a.count; i++) stream = stream || a.d[i].ntiles > a.d[i].nwg;
-    auto kern = stream ? (a.fused ? k_gemv<true, true> : k_gemv<false, true>)
-                       : (a.fused ? k_gemv<true, false> : k_gemv<false, false>);
+    auto kern = stream ? (a.fused ? k_gemv<true, true, false> : k_gemv<false, true, false>)
+                       : (a.fused ? k_gemv<true, false, false> : k_gemv<false, false, false>);
+    if (a.d[0].xf32)                                   // fp32 rows (every descriptor of the launch)
+        kern = stream ? (a.fused ? k_gemv<true, true, true> : k_gemv<false, true, true>)
+                      : (a.fused ? k_gemv<true, false, true> : k_gemv<false, false, true>);
     hipLaunchKernelGGL(kern, dim3(wg), dim3(256), lds, s, tab[0], tab[1], tab[2], tab[3], tab[4], tab[5], tab[6],
                        tab[7], ka, amax_partial, zero_ctr);
     return hipGetLastError();

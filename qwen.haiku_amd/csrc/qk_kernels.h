@@ -26,6 +26,7 @@ struct GemvDesc {
     int32_t wg0;           // first workgroup of the launch serving this descriptor
     int32_t nwg;           // workgroups serving it (grid-stride over tiles)
     int32_t lds_act;       // bytes of the staged activation row
+    int32_t xf32;          // 1: xq is the fp32 row (k floats), quantized by each workgroup
 };
 
 struct GemvArgs {

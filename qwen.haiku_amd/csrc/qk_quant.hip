@@ -8,28 +8,8 @@
 
 namespace qk {
 
-// Largest value over the wave (inputs NaN-free): DPP within each 16-lane
-// row, then the four row results read as uniform values.
-__device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, __int_as_float(dpp_xor1(__float_as_int(v))));
-    v = fmaxf(v, __int_as_float(dpp_xor2(__float_as_int(v))));
-    v = fmaxf(v, __int_as_float(dpp_hmirror(__float_as_int(v))));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));  // row_mirror
-    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
-}
-
 // quantize_row_q8_K (slm/tensor.c:683-720): one wave per 256-element
-// block, 4 elements per lane.
-//  * amax/xmax: the first element with the largest |x| (strict '>' in a
-//    sequential scan; NaN never compares greater, so it is never chosen).
-//    The wave takes the largest |x| (NaN as 0), then the first lane
-//    holding it (ballot) supplies its first such element.
-//  * iscale = -127/xmax, d = 1/iscale (IEEE division),
-//    q = clamp(nearest_int(iscale*x)), bsums over 16-element groups.
+// block, 4 elements per lane (q8k_block_wave).
 __global__ __launch_bounds__(256) void k_quantize_q8k(const float *__restrict__ x,
                                                       uint8_t *__restrict__ xq,
                                                       int64_t nblocks) {
@@ -38,78 +18,26 @@ __global__ __launch_bounds__(256) void k_quantize_q8k(const float *__restrict__ 
     if (blk >= nblocks) return;                        // whole wave
     const float4 v = reinterpret_cast<const float4 *>(x + blk * QK_K)[lane];
     const float e[4] = {v.x, v.y, v.z, v.w};
-    float a[4], la = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float ax = fabsf(e[i]);
-        a[i] = (ax != ax) ? 0.0f : ax;
-        la = fmaxf(la, a[i]);
-    }
-    const float amax = wave_max(la);
-    // this lane's first element at amax (scanning backwards keeps the first)
-    float mine = e[3];
-#pragma unroll
-    for (int i = 2; i >= 0; i--) mine = a[i] == amax ? e[i] : mine;
-    const uint64_t hit = __ballot(la == amax);
-    const int first = __builtin_ctzll(hit);            // amax == 0: lane 0, unused
-    const float xmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), first));
+    uint32_t packed, bs;
+    float d;
+    q8k_block_wave(e, lane, packed, d, bs);
     uint8_t *out = xq + blk * Q8K_BYTES;
-    int32_t q[4] = {0, 0, 0, 0};
-    float d = 0.0f;
-    if (amax != 0.0f) {
-        const float iscale = __fdiv_rn(-127.0f, xmax);
-        d = __fdiv_rn(1.0f, iscale);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            int32_t t = nearest_int(__fmul_rn(iscale, e[i]));
-            q[i] = t > 127 ? 127 : (t < -128 ? -128 : t);
-        }
-    }
-    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
-                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
     reinterpret_cast<uint32_t *>(out + 4)[lane] = packed;
-    // bsums[j] = sum of lanes 4j..4j+3; lane 8p stores bsums 2p, 2p+1
-    // (lane 8p+4's sum arrives by DPP row_shl:4, inside the 16-lane row).
-    int32_t s = q[0] + q[1] + q[2] + q[3];
-    s += dpp_xor1(s);
-    s += dpp_xor2(s);
-    const int32_t s_next = __builtin_amdgcn_mov_dpp(s, 0x104, 0xF, 0xF, true);
-    if ((lane & 7) == 0) {
-        reinterpret_cast<uint32_t *>(out + 260)[lane >> 3] =
-            ((uint32_t)s & 0xffffu) | ((uint32_t)s_next << 16);
-    }
+    if ((lane & 7) == 0) reinterpret_cast<uint32_t *>(out + 260)[lane >> 3] = bs;
     if (lane == 0) *reinterpret_cast<float *>(out) = d;
 }
 
-// tensor_quantize_row_q8_0 (slm/tensor.c:930-950): 32 lanes per block.
-// d = amax/127, id = 1/d (of the unrounded d), q = (int)roundf(x*id)
-// (half away from zero), d stored as fp16 round-to-nearest-even.
+// tensor_quantize_row_q8_0 (slm/tensor.c:930-950): 32 lanes per block
+// (q80_block_half), d stored as fp16 round-to-nearest-even.
 __global__ __launch_bounds__(256) void k_quantize_q8_0(const float *__restrict__ x,
                                                        uint8_t *__restrict__ xq,
                                                        int64_t nblocks) {
     const int lane = threadIdx.x & 31;
     const int64_t blk = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 5;
     if (blk >= nblocks) return;                        // whole half-wave
-    const float v = x[blk * QK8_0 + lane];
-    float a = fabsf(v);
-    a = (a != a) ? 0.0f : a;                           // '>' never picks NaN
-    // block maximum: DPP within each 16-lane row, then the two rows of
-    // this half-wave's block (read as uniform values)
-    a = fmaxf(a, __int_as_float(dpp_xor1(__float_as_int(a))));
-    a = fmaxf(a, __int_as_float(dpp_xor2(__float_as_int(a))));
-    a = fmaxf(a, __int_as_float(dpp_hmirror(__float_as_int(a))));
-    a = fmaxf(a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x140, 0xF, 0xF, true)));
-    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 0));
-    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 16));
-    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32));
-    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 48));
-    a = (threadIdx.x & 32) ? fmaxf(r2, r3) : fmaxf(r0, r1);
-    const float d = __fdiv_rn(a, 127.0f);
-    const float id = (d != 0.0f) ? __fdiv_rn(1.0f, d) : 0.0f;
-    // Saturating conversion, as the reference's clang build behaves when
-    // d underflows and id = 1/d is inf.
-    const float r = roundf(__fmul_rn(v, id));
-    const int32_t q = r >= 127.0f ? 127 : (r <= -128.0f ? -128 : (int32_t)r);
+    int32_t q;
+    float d;
+    q80_block_half(x[blk * QK8_0 + lane], q, d);
     uint8_t *out = xq + blk * Q80_BYTES;
     out[2 + lane] = (uint8_t)(q & 0xff);
     if (lane == 0) *reinterpret_cast<uint16_t *>(out) = (uint16_t)f2h(d);

@@ -90,6 +90,7 @@ class QK:
         for f in ("hip_matvec_q4k", "hip_matvec_q5k", "hip_matvec_q6k", "hip_matvec_q8_0"):
             getattr(L, f).argtypes = [_vp, _i64, _i64, _vp, _vp, _vp]
         L.hip_matvec_group.argtypes = [C.POINTER(GemvDesc), C.c_int, _vp]
+        L.hip_matvec_group_f32.argtypes = [C.POINTER(GemvDesc), C.c_int, _vp]
         for f in ("hip_matmul_q4k", "hip_matmul_q5k", "hip_matmul_q6k"):
             getattr(L, f).argtypes = [_vp, _i64, _i64, _vp, _i64, _vp, _vp]
         for f in ("hip_dequant_q4k", "hip_dequant_q5k", "hip_dequant_q6k"):
@@ -178,6 +179,17 @@ class QK:
             _need(y, 4 * n, "y")
             arr[i] = GemvDesc(t, 0, n, k, w.data_ptr(), xq.data_ptr(), y.data_ptr())
         self._ck(self.L.hip_matvec_group(arr, len(items), self._stream()))
+
+    def matvec_group_f32(self, items):
+        """items: list of (wtype, w, n, k, x, y) with device tensors; x is
+        the fp32 activation row (k floats), quantized inside the launch."""
+        arr = (GemvDesc * len(items))()
+        for i, (t, w, n, k, x, y) in enumerate(items):
+            _need(w, n * row_bytes(t, k), "w")
+            _need(x, 4 * k, "x")
+            _need(y, 4 * n, "y")
+            arr[i] = GemvDesc(t, 0, n, k, w.data_ptr(), x.data_ptr(), y.data_ptr())
+        self._ck(self.L.hip_matvec_group_f32(arr, len(items), self._stream()))
 
     def matmul(self, wtype, w, n, k, xq, m, y=None):
         import torch

@@ -112,6 +112,53 @@ def test_matvec_group_matches_single(lib, orc):
         assert_bits_equal(host(y), want, f"group type {t} {n}x{k}")
 
 
+F32_SHAPES = [(12, 3584, 1024), (14, 1024, 3584), (13, 2048, 1024), (13, 1024, 2048), (8, 1024, 1024),
+              (8, 70, 512), (8, 45, 96), (8, 3, 16384), (12, 33, 768), (13, 21, 8192), (14, 100, 2560),
+              (12, 40, 16384), (14, 9, 16384), (12, 40000, 256), (14, 30000, 1024)]
+
+
+@pytest.mark.parametrize("wtype,n,k", F32_SHAPES)
+@pytest.mark.parametrize("epi,t", EPI_TIERS)
+def test_matvec_group_f32_quantizes_in_launch(tier, orc, wtype, n, k, epi, t):
+    # fp32 rows in, the workgroups quantize them: the result must be the
+    # reference's quantize-then-dot (tensor_matmul_*_f32 at one token),
+    # including rows whose quantization hits the edge cases
+    lib = tier
+    import torch
+    step(f"matvec_group_f32 type={wtype} n={n} k={k} tier={t}")
+    lib.set_tier(t)
+    w = synth.blocks(wtype, n, k, seed=n + 7, tag=wtype)
+    xs = np.concatenate([synth.activations(2, k, seed=k + 3), edge_rows(k)[[0, 1, 3, 6, 7]], special_rows(k)])
+    wd = dev(w)
+    for r in range(xs.shape[0]):
+        xd = dev(xs[r])
+        y = torch.empty(n, dtype=torch.float32, device="cuda")
+        lib.matvec_group_f32([(wtype, wd, n, k, xd, y)])
+        want = orc.matmul(wtype, w, n, k, xs[r:r + 1], epi)[0]
+        assert_bits_equal(host(y), want, f"row {r}")
+
+
+def test_matvec_group_f32_layer(lib, orc):
+    # config 1 as one dispatch from fp32 activations, entries sharing rows
+    # the way a decode layer does
+    import torch
+    step("matvec_group_f32 config 1 layer")
+    k_rows = {1024: synth.activations(1, 1024, seed=60)[0], 3584: synth.activations(1, 3584, seed=61)[0],
+              2048: synth.activations(1, 2048, seed=62)[0]}
+    xd = {k: dev(v) for k, v in k_rows.items()}
+    specs = [(12, 3584, 1024), (12, 3584, 1024), (14, 1024, 3584), (13, 2048, 1024),
+             (13, 512, 1024), (13, 1024, 2048), (8, 1024, 1024)]
+    items, wants = [], []
+    for i, (t, n, k) in enumerate(specs):
+        w = synth.blocks(t, n, k, seed=63, tag=i)
+        y = torch.empty(n, dtype=torch.float32, device="cuda")
+        items.append((t, dev(w), n, k, xd[k], y))
+        wants.append(orc.matmul(t, w, n, k, k_rows[k][None], oracle.TIER_EPI[lib.tier()])[0])
+    lib.matvec_group_f32(items)
+    for (t, _, n, k, _, y), want in zip(items, wants):
+        assert_bits_equal(host(y), want, f"type {t} {n}x{k}")
+
+
 def test_quantize_then_matvec_on_device(lib, orc):
     step("quantize + matvec chain")
     k, n = 1024, 3584
