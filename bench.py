@@ -460,24 +460,39 @@ def cpu_extras(synth, seconds=2.0):
 
 
 def e2e(prompt=512, gen=256, seed=0, timeout=600):
-    """Config 4: the reference's forward pass with its quantized matmuls on
-    the GPU (the drop-in) and the unchanged CPU reference, same model, same
-    prompt, same run."""
+    """Config 4: the reference's forward pass on the same model and prompt
+    three ways in one run: "gpu_chain" (qk_decode.c: residual stream, norms,
+    FFN and the greedy pick on the device, the reference's mixers on the
+    host), "gpu_dropin" (the reference's slm_forward_step unchanged, its
+    quantized matmuls through the seam, one round trip each) and the CPU
+    reference. Prefill is slm_forward_batch through the seam in both GPU
+    runs."""
     out = {}
-    for name, path in (("gpu_dropin", E2E_GPU), ("cpu_reference", E2E_CPU)):
+    runs = (("gpu_chain", E2E_GPU, ["--decode", "chain"]), ("gpu_dropin", E2E_GPU, ["--decode", "seam"]),
+            ("cpu_reference", E2E_CPU, []))
+    keys = ("prefill_tok_s", "decode_tok_s", "prefill_s", "decode_s", "tier", "host_syncs_per_token")
+    for name, path, extra in runs:
         if not os.path.exists(path):
             out[name] = "not built"
             continue
-        r = subprocess.run([path, "--prompt", str(prompt), "--gen", str(gen), "--seed", str(seed)],
+        r = subprocess.run([path, "--prompt", str(prompt), "--gen", str(gen), "--seed", str(seed)] + extra,
                            capture_output=True, text=True, timeout=timeout)
         if r.returncode != 0:
             raise RuntimeError(f"{path} failed ({r.returncode}): {r.stderr[-1000:]}")
         j = json.loads(r.stdout.strip().splitlines()[-1])
-        out[name] = {k: j[k] for k in ("prefill_tok_s", "decode_tok_s", "prefill_s", "decode_s", "tier")}
+        out[name] = {k: j[k] for k in keys if k in j}
         out[name]["tokens"] = j["tokens"]
-    if isinstance(out.get("gpu_dropin"), dict) and isinstance(out.get("cpu_reference"), dict):
-        out["tokens_identical"] = out["gpu_dropin"]["tokens"] == out["cpu_reference"]["tokens"]
-        out["cpu_reference"]["cores"] = 1
+        if name == "gpu_chain":
+            out[name]["prefetch_misses"] = j["prefetch_misses"]
+    cpu = out.get("cpu_reference")
+    if isinstance(cpu, dict):
+        cpu["cores"] = 1
+        cpu.pop("host_syncs_per_token", None)
+        for name in ("gpu_chain", "gpu_dropin"):
+            if isinstance(out.get(name), dict):
+                out[name]["tokens_identical"] = out[name]["tokens"] == cpu["tokens"]
+        out["tokens_identical"] = all(out[n]["tokens_identical"] for n in ("gpu_chain", "gpu_dropin")
+                                      if isinstance(out.get(n), dict))
     for v in out.values():
         if isinstance(v, dict):
             v.pop("tokens", None)

@@ -212,6 +212,40 @@ int hip_dequant_q4k(const void *w, int64_t nblocks, float *y, void *stream);
 int hip_dequant_q5k(const void *w, int64_t nblocks, float *y, void *stream);
 int hip_dequant_q6k(const void *w, int64_t nblocks, float *y, void *stream);
 
+/* ---- device layer: the decode chain's elementwise links ------------- */
+
+/* Residual add + RMSNorm (+ Q8_K), per row t < m of k floats:
+ *   r = h + delta                 tensor_add, slm/tensor.c:284-291
+ *                                 (delta may be NULL: r = h)
+ *   x = rms_norm(r) * w           tensor_rms_norm, slm/tensor.c:345-367:
+ *                                 the sequential double sum of (r_i*r_i),
+ *                                 rscale = 1/sqrtf((float)(ssq/k) + eps),
+ *                                 x_i = (r_i*rscale)*w_i
+ *   xq = quantize_row_q8_K(x)     slm/tensor.c:683-720
+ * h_out (may be NULL, may equal h) receives r, x_out (may be NULL) x,
+ * xq (may be NULL, needs k % 256 == 0) the Q8_K row for the next GEMV;
+ * one of x_out / xq is required. w holds k floats shared by every row.
+ * k is a multiple of 4, at most QK_NORM_MAX_K. Bit-exact. Device
+ * pointers; float rows 16-byte aligned. The decode chain between two
+ * matmuls: slm/qwen.c:936-948 (h = h + mix; ffn_norm) and the norm that
+ * opens each layer's mixer (slm/qwen.c:332-334). */
+#define QK_NORM_MAX_K 16384
+int hip_add_rmsnorm_q8k(const float *h, const float *delta, const float *w,
+                        float eps, int64_t m, int64_t k, float *h_out,
+                        float *x_out, void *xq, void *stream);
+
+/* y = x / (1 + expf(-x)) elementwise over n floats (y may equal x):
+ * simd_silu_f32's x86 path (simd/simd.c:265-277) with expf bit for bit
+ * the glibc expf that x86 hosts with FMA run. */
+int hip_silu_f32(const float *x, int64_t n, float *y, void *stream);
+
+/* The FFN's SwiGLU link (slm/qwen.c:949-954): act = silu(gate) * up over
+ * m rows of k floats (simd_silu_f32 then tensor_mul, slm/tensor.c:293),
+ * written to act (may be NULL) and/or quantized to Q8_K rows in xq (may
+ * be NULL, needs k % 256 == 0) for the down projection. Bit-exact. */
+int hip_swiglu_q8k(const float *gate, const float *up, int64_t m, int64_t k,
+                   float *act, void *xq, void *stream);
+
 /* ---- device layer: LM head ------------------------------------------ */
 
 /* Q6_K GEMV over n vocabulary rows fused with the greedy pick and a

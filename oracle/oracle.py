@@ -88,6 +88,12 @@ class Oracle:
         L.qko_argmax.restype = C.c_int32
         L.qko_topk_collect.argtypes = [_vp, _i64, C.c_int32, _vp, _vp]
         L.qko_topk_collect.restype = C.c_int32
+        L.qko_add_rmsnorm.argtypes = [_vp, _vp, _vp, C.c_float, _i64, _i64, _vp, _vp]
+        L.qko_add_rmsnorm.restype = None
+        L.qko_silu.argtypes = [_i64, _vp, _vp]
+        L.qko_silu.restype = None
+        L.qko_swiglu.argtypes = [_i64, _vp, _vp, _vp]
+        L.qko_swiglu.restype = None
 
     # -- scalars -------------------------------------------------------
     def f16_to_f32(self, h):
@@ -192,6 +198,46 @@ class Oracle:
         f = self.L.qko_topk_collect(_ptr(v), v.size, k, _ptr(idx), _ptr(val))
         return idx[:f].copy(), val[:f].copy()
 
+    # -- decode-chain links (shared by Oracle and Ref) -------------------
+    def add_rmsnorm(self, h, delta, w, eps):
+        """(h + delta, rms_norm(h + delta) * w) per row; delta may be None."""
+        h = np.ascontiguousarray(h, np.float32)
+        m, k = h.reshape(-1, h.shape[-1]).shape
+        d = None if delta is None else np.ascontiguousarray(delta, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        r = np.empty((m, k), np.float32)
+        x = np.empty((m, k), np.float32)
+        rc = self._add_rmsnorm(_ptr(h), None if d is None else _ptr(d), _ptr(w), float(np.float32(eps)), m, k,
+                               _ptr(r), _ptr(x))
+        if rc:
+            raise RuntimeError("add_rmsnorm failed")
+        return r, x
+
+    def silu(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(x)
+        self._silu(x.size, _ptr(x), _ptr(y))
+        return y
+
+    def swiglu(self, gate, up):
+        g = np.ascontiguousarray(gate, np.float32)
+        u = np.ascontiguousarray(up, np.float32)
+        a = np.empty_like(g)
+        if self._swiglu(g.size, _ptr(g), _ptr(u), _ptr(a)):
+            raise RuntimeError("swiglu failed")
+        return a
+
+    def _add_rmsnorm(self, *a):
+        self.L.qko_add_rmsnorm(*a)
+        return 0
+
+    def _silu(self, *a):
+        self.L.qko_silu(*a)
+
+    def _swiglu(self, *a):
+        self.L.qko_swiglu(*a)
+        return 0
+
 
 class Ref:
     """The reference's own C (oracle/_ref/libqkref.so, built from /root/reference)."""
@@ -230,6 +276,12 @@ class Ref:
         L.ref_argmax.restype = C.c_int32
         L.ref_topk_collect.argtypes = [_vp, _i64, C.c_int32, _vp, _vp]
         L.ref_topk_collect.restype = C.c_int32
+        L.ref_add_rmsnorm.argtypes = [_vp, _vp, _vp, C.c_float, _i64, _i64, _vp, _vp]
+        L.ref_add_rmsnorm.restype = C.c_int
+        L.ref_silu.argtypes = [_i64, _vp, _vp]
+        L.ref_silu.restype = None
+        L.ref_swiglu.argtypes = [_i64, _vp, _vp, _vp]
+        L.ref_swiglu.restype = C.c_int
         L.ref_simd_init()
 
     def label(self):
@@ -312,3 +364,41 @@ class Ref:
         val = np.zeros(256, np.float32)
         f = self.L.ref_topk_collect(_ptr(v), v.size, k, _ptr(idx), _ptr(val))
         return idx[:f].copy(), val[:f].copy()
+
+    # -- decode-chain links (shared by Oracle and Ref) -------------------
+    def add_rmsnorm(self, h, delta, w, eps):
+        """(h + delta, rms_norm(h + delta) * w) per row; delta may be None."""
+        h = np.ascontiguousarray(h, np.float32)
+        m, k = h.reshape(-1, h.shape[-1]).shape
+        d = None if delta is None else np.ascontiguousarray(delta, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        r = np.empty((m, k), np.float32)
+        x = np.empty((m, k), np.float32)
+        rc = self._add_rmsnorm(_ptr(h), None if d is None else _ptr(d), _ptr(w), float(np.float32(eps)), m, k,
+                               _ptr(r), _ptr(x))
+        if rc:
+            raise RuntimeError("add_rmsnorm failed")
+        return r, x
+
+    def silu(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(x)
+        self._silu(x.size, _ptr(x), _ptr(y))
+        return y
+
+    def swiglu(self, gate, up):
+        g = np.ascontiguousarray(gate, np.float32)
+        u = np.ascontiguousarray(up, np.float32)
+        a = np.empty_like(g)
+        if self._swiglu(g.size, _ptr(g), _ptr(u), _ptr(a)):
+            raise RuntimeError("swiglu failed")
+        return a
+
+    def _add_rmsnorm(self, *a):
+        return self.L.ref_add_rmsnorm(*a)
+
+    def _silu(self, *a):
+        self.L.ref_silu(*a)
+
+    def _swiglu(self, *a):
+        return self.L.ref_swiglu(*a)

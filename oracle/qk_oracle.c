@@ -501,3 +501,51 @@ int32_t qko_topk_collect(const float *v, int64_t n, int32_t k,
     }
     return filled;
 }
+
+/* ---- the decode chain's elementwise links ---------------------------- */
+
+/* tensor_add (slm/tensor.c:284-291) of an optional delta, then
+ * tensor_rms_norm (slm/tensor.c:345-367) per row of k floats: a
+ * sequential double sum of the float squares, then
+ * rscale = 1/sqrtf((float)(ssq/k) + eps), x = (r*rscale)*w. */
+void qko_add_rmsnorm(const float *h, const float *delta, const float *w,
+                     float eps, int64_t m, int64_t k, float *h_out,
+                     float *x_out) {
+    for (int64_t t = 0; t < m; t++) {
+        const float *hr = h + t * k;
+        const float *dr = delta ? delta + t * k : NULL;
+        float *ro = h_out + t * k;
+        for (int64_t i = 0; i < k; i++) ro[i] = dr ? hr[i] + dr[i] : hr[i];
+        double ssq = 0.0;
+        for (int64_t i = 0; i < k; i++) {
+            float sq = ro[i] * ro[i];
+            ssq += (double)sq;
+        }
+        float mean = (float)(ssq / (double)k);
+        float rscale = 1.0f / sqrtf(mean + eps);
+        float *xo = x_out + t * k;
+        for (int64_t i = 0; i < k; i++) {
+            float a = ro[i] * rscale;
+            xo[i] = a * w[i];
+        }
+    }
+}
+
+/* simd_silu_f32's x86 path (simd/simd.c:265-269) with the host libm. */
+void qko_silu(int64_t n, const float *x, float *y) {
+    for (int64_t i = 0; i < n; i++) {
+        float v = x[i];
+        float den = 1.0f + expf(-v);
+        y[i] = v / den;
+    }
+}
+
+/* silu(gate) then tensor_mul (slm/tensor.c:293-300) by up
+ * (slm/qwen.c:949-954). */
+void qko_swiglu(int64_t n, const float *gate, const float *up, float *act) {
+    for (int64_t i = 0; i < n; i++) {
+        float v = gate[i];
+        float s = v / (1.0f + expf(-v));
+        act[i] = s * up[i];
+    }
+}

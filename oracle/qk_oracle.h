@@ -56,6 +56,14 @@ int qko_matmul_xq(int type, const void *w, int64_t n, int64_t k,
                   const void *xq, int64_t m, float *out, int epi,
                   int64_t row0, int64_t row1);
 
+/* Decode-chain links: residual add + RMSNorm (h_out gets h + delta,
+ * x_out the normalized rows; delta may be NULL), SiLU, SiLU(gate)*up. */
+void qko_add_rmsnorm(const float *h, const float *delta, const float *w,
+                     float eps, int64_t m, int64_t k, float *h_out,
+                     float *x_out);
+void qko_silu(int64_t n, const float *x, float *y);
+void qko_swiglu(int64_t n, const float *gate, const float *up, float *act);
+
 int32_t qko_argmax(const float *v, int64_t n);
 int32_t qko_topk_collect(const float *v, int64_t n, int32_t k,
                          int32_t *idx, float *val);

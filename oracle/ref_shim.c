@@ -307,3 +307,40 @@ int32_t ref_topk_collect(const float *v, int64_t n, int32_t k, int32_t *idx, flo
     struct tensor t = view1d(v, n);
     return topk_collect(&t, k, idx, val);
 }
+
+/* tensor_add then tensor_rms_norm (slm/tensor.c:284, 345) on m rows of k
+ * floats, through the reference's arena; delta may be NULL. */
+int ref_add_rmsnorm(const float *h, const float *delta, const float *w, float eps,
+                    int64_t m, int64_t k, float *h_out, float *x_out) {
+    struct arena *a = arena_new((size_t)(4 * m * k + 4 * k) * sizeof(float) + (1u << 16));
+    if (!a) return -1;
+    struct tensor *x = tensor_new_2d(a, k, m);
+    memcpy(x->data, h, (size_t)(m * k) * sizeof(float));
+    if (delta) {
+        struct tensor *d = tensor_new_2d(a, k, m);
+        memcpy(d->data, delta, (size_t)(m * k) * sizeof(float));
+        x = tensor_add(x, d);
+    }
+    struct tensor *wt = tensor_new_1d(a, k);
+    memcpy(wt->data, w, (size_t)k * sizeof(float));
+    struct tensor *y = tensor_rms_norm(x, wt, eps);
+    memcpy(h_out, x->data, (size_t)(m * k) * sizeof(float));
+    memcpy(x_out, y->data, (size_t)(m * k) * sizeof(float));
+    arena_free(a);
+    return 0;
+}
+
+/* simd_silu_f32 (simd/simd.c:271) and tensor_mul (slm/tensor.c:293). */
+void ref_silu(int64_t n, const float *x, float *y) { simd_silu_f32((int)n, y, x); }
+
+int ref_swiglu(int64_t n, const float *gate, const float *up, float *act) {
+    struct arena *a = arena_new((size_t)(3 * n) * sizeof(float) + (1u << 16));
+    if (!a) return -1;
+    struct tensor *g = tensor_new_1d(a, n), *u = tensor_new_1d(a, n);
+    memcpy(u->data, up, (size_t)n * sizeof(float));
+    simd_silu_f32((int)n, g->data, gate);
+    struct tensor *o = tensor_mul(g, u);
+    memcpy(act, o->data, (size_t)n * sizeof(float));
+    arena_free(a);
+    return 0;
+}

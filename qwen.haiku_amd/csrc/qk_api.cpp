@@ -471,6 +471,50 @@ int hip_dequant_q4k(const void *w, int64_t nb, float *y, void *s) { return dequa
 int hip_dequant_q5k(const void *w, int64_t nb, float *y, void *s) { return dequant(QK_TYPE_Q5_K, w, nb, y, s); }
 int hip_dequant_q6k(const void *w, int64_t nb, float *y, void *s) { return dequant(QK_TYPE_Q6_K, w, nb, y, s); }
 
+int hip_add_rmsnorm_q8k(const float *h, const float *delta, const float *w, float eps, int64_t m, int64_t k,
+                        float *h_out, float *x_out, void *xq, void *stream) {
+    int rc = require_init();
+    if (rc) return rc;
+    if (!h || !w) return fail(QK_ERR_ARG, "null pointer");
+    if (!x_out && !xq) return fail(QK_ERR_ARG, "x_out and xq are both NULL");
+    if (m < 1 || m > 0x7fffffffLL || k < 4 || k % 4 || k > QK_NORM_MAX_K)
+        return fail(QK_ERR_ARG, "bad shape m=%lld k=%lld (k a multiple of 4, at most %d)", (long long)m,
+                    (long long)k, QK_NORM_MAX_K);
+    if (xq && k % QK_K) return fail(QK_ERR_ARG, "k=%lld: a Q8_K row needs a multiple of 256", (long long)k);
+    if (!aligned(h, 16) || !aligned(delta, 16) || !aligned(w, 16) || !aligned(h_out, 16) || !aligned(x_out, 16) ||
+        !aligned(xq, 4))
+        return fail(QK_ERR_ARG, "float rows must be 16-byte and xq 4-byte aligned");
+    if (delta == h_out && delta) return fail(QK_ERR_ARG, "h_out may alias h, not delta");
+    HIP_OK(qk::launch_add_rmsnorm(h, delta, w, eps, m, k, h_out, x_out, static_cast<uint8_t *>(xq),
+                                  stream_of(stream)),
+           "add_rmsnorm launch");
+    return QK_OK;
+}
+
+int hip_silu_f32(const float *x, int64_t n, float *y, void *stream) {
+    int rc = require_init();
+    if (rc) return rc;
+    if (!x || !y || n < 1) return fail(QK_ERR_ARG, "bad silu arguments");
+    if (!aligned(x, 4) || !aligned(y, 4)) return fail(QK_ERR_ARG, "x/y misaligned");
+    HIP_OK(qk::launch_silu(x, y, n, stream_of(stream)), "silu launch");
+    return QK_OK;
+}
+
+int hip_swiglu_q8k(const float *gate, const float *up, int64_t m, int64_t k, float *act, void *xq, void *stream) {
+    int rc = require_init();
+    if (rc) return rc;
+    if (!gate || !up) return fail(QK_ERR_ARG, "null pointer");
+    if (!act && !xq) return fail(QK_ERR_ARG, "act and xq are both NULL");
+    if (m < 1 || k < 4 || k % 4 || m > ((int64_t)1 << 40) / k)
+        return fail(QK_ERR_ARG, "bad shape m=%lld k=%lld (k a multiple of 4)", (long long)m, (long long)k);
+    if (xq && k % QK_K) return fail(QK_ERR_ARG, "k=%lld: a Q8_K row needs a multiple of 256", (long long)k);
+    if (!aligned(gate, 16) || !aligned(up, 16) || !aligned(act, 16) || !aligned(xq, 4))
+        return fail(QK_ERR_ARG, "float rows must be 16-byte and xq 4-byte aligned");
+    HIP_OK(qk::launch_swiglu(gate, up, m * k, act, static_cast<uint8_t *>(xq), stream_of(stream)),
+           "swiglu launch");
+    return QK_OK;
+}
+
 }  // extern "C"
 
 namespace {

@@ -53,6 +53,13 @@ hipError_t launch_lmhead(const uint8_t *w, int64_t n, int64_t k, const uint8_t *
                          float *logits, int32_t *argmax, int32_t *topk_idx, float *topk_val,
                          void *scratch, int fused, hipStream_t s);
 
+// Decode chain links (qk_chain.hip). k_add_rmsnorm keeps a row in LDS:
+// k * 4 bytes per workgroup.
+hipError_t launch_add_rmsnorm(const float *h, const float *delta, const float *w, float eps, int64_t m, int64_t k,
+                              float *h_out, float *x_out, uint8_t *xq, hipStream_t s);
+hipError_t launch_silu(const float *src, float *dst, int64_t n, hipStream_t s);
+hipError_t launch_swiglu(const float *gate, const float *up, int64_t n, float *act, uint8_t *xq, hipStream_t s);
+
 // Prefill GEMM (int8 MFMA); y[t*n + j].
 hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, const uint8_t *xq,
                        int64_t m, float *y, int fused, hipStream_t s);

@@ -76,6 +76,54 @@ static void qk_seam_init(void) {
     }
 }
 
+/* Matmul results computed ahead of their call: a decode step that keeps
+ * the residual stream on the GPU (qk_decode.c) runs a layer's
+ * in-projections as one grouped launch from the normalized row it also
+ * returns, and files them here before the reference's mixer runs. A
+ * single-token call with the same weight is then answered from the table
+ * when its input row equals that row bit for bit (the reference normalizes
+ * the same h on the host, so it does whenever the device norm is exact);
+ * otherwise it is computed as usual and counted as a miss. Per thread,
+ * like the reference's contexts. */
+#define QK_SEAM_PREFETCH_MAX 8
+typedef struct {
+    const void *w;
+    int64_t out_f, k;
+    const float *x;     /* the input row the results belong to */
+    const float *y;     /* out_f results */
+} qk_seam_prefetch;
+static _Thread_local qk_seam_prefetch qk_seam_pf[QK_SEAM_PREFETCH_MAX];
+static _Thread_local int qk_seam_pf_n;
+static _Thread_local long long qk_seam_pf_hits, qk_seam_pf_misses, qk_seam_gpu_calls;
+
+static void qk_seam_prefetch_clear(void) { qk_seam_pf_n = 0; }
+
+static void qk_seam_prefetch_add(const void *w, int64_t out_f, int64_t k, const float *x, const float *y) {
+    assert(qk_seam_pf_n < QK_SEAM_PREFETCH_MAX);
+    qk_seam_prefetch *p = &qk_seam_pf[qk_seam_pf_n++];
+    p->w = w;
+    p->out_f = out_f;
+    p->k = k;
+    p->x = x;
+    p->y = y;
+}
+
+static int qk_seam_prefetched(const void *w, int64_t out_f, int64_t k, const struct tensor *x, float *out) {
+    if (x->ne[1] != 1) return 0;
+    for (int i = 0; i < qk_seam_pf_n; i++) {
+        const qk_seam_prefetch *p = &qk_seam_pf[i];
+        if (p->w != w || p->out_f != out_f || p->k != k) continue;
+        if (memcmp(p->x, x->data, (size_t)k * sizeof(float)) != 0) {
+            qk_seam_pf_misses++;
+            return 0;
+        }
+        memcpy(out, p->y, (size_t)out_f * sizeof(float));
+        qk_seam_pf_hits++;
+        return 1;
+    }
+    return 0;
+}
+
 static struct tensor *qk_seam_matmul(int type, const void *w, int64_t out_f, int64_t k,
                                      struct tensor *x) {
     assert(x->ndim == 2 && x->ne[0] == k);
@@ -83,6 +131,8 @@ static struct tensor *qk_seam_matmul(int type, const void *w, int64_t out_f, int
     qk_seam_init();
     int64_t n = x->ne[1];
     struct tensor *out = tensor_new_2d(x->arena, out_f, n);
+    if (qk_seam_prefetched(w, out_f, k, x, out->data)) return out;
+    qk_seam_gpu_calls++;
     int rc = hip_qk_matmul_host(w, type, out_f, k, x->data, n, out->data);
     if (rc != QK_OK) {
         fprintf(stderr, "qk_seam: matmul type %d (%lld x %lld, %lld tokens) failed (%d): %s\n", type,

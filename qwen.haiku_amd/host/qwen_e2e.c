@@ -41,8 +41,14 @@
  * place of building one; the prompt comes from its own seeded stream, so
  * both modes run the same workload.
  *
+ * Decode path of the GPU build (--decode): "chain" (default) runs each
+ * step through qk_decode.c, the residual stream and the FFN resident on
+ * the GPU and the greedy pick fused into the LM head; "seam" runs the
+ * reference's slm_forward_step unchanged, every matmul a round trip
+ * through the seam. Both report their host synchronisations per token.
+ *
  * Usage: qwen_e2e [--prompt P] [--gen G] [--seed S] [--layers L]
- *                 [--write-gguf PATH | --gguf PATH]
+ *                 [--write-gguf PATH | --gguf PATH] [--decode chain|seam]
  */
 #if defined(QK_E2E_GPU)
 #include "qk_seam.c"
@@ -50,6 +56,9 @@
 #include "qwen.c"
 #include "sampler.c"
 #include "gguf_write.c"
+#if defined(QK_E2E_GPU)
+#include "qk_decode.c"
+#endif
 
 #include <time.h>
 
@@ -250,7 +259,7 @@ static double e2e_now(void) {
 int main(int argc, char **argv) {
     int32_t n_prompt = 512, n_gen = 256, n_layers = 24;
     uint64_t seed = 0;
-    const char *write_path = NULL, *load_path = NULL;
+    const char *write_path = NULL, *load_path = NULL, *decode_mode = "chain";
     for (int i = 1; i + 1 < argc; i += 2) {
         if (strcmp(argv[i], "--prompt") == 0) n_prompt = atoi(argv[i + 1]);
         else if (strcmp(argv[i], "--gen") == 0) n_gen = atoi(argv[i + 1]);
@@ -258,10 +267,13 @@ int main(int argc, char **argv) {
         else if (strcmp(argv[i], "--layers") == 0) n_layers = atoi(argv[i + 1]);
         else if (strcmp(argv[i], "--write-gguf") == 0) write_path = argv[i + 1];
         else if (strcmp(argv[i], "--gguf") == 0) load_path = argv[i + 1];
+        else if (strcmp(argv[i], "--decode") == 0) decode_mode = argv[i + 1];
     }
-    if (n_prompt < 2 || n_gen < 1 || n_layers < 1 || (write_path && load_path)) {
+    const int chain = strcmp(decode_mode, "chain") == 0;
+    if (n_prompt < 2 || n_gen < 1 || n_layers < 1 || (write_path && load_path) ||
+        (!chain && strcmp(decode_mode, "seam") != 0)) {
         fprintf(stderr, "usage: %s [--prompt P>=2] [--gen G>=1] [--seed S] [--layers L>=1] "
-                        "[--write-gguf PATH | --gguf PATH]\n", argv[0]);
+                        "[--write-gguf PATH | --gguf PATH] [--decode chain|seam]\n", argv[0]);
         return 2;
     }
     simd_init();
@@ -398,15 +410,39 @@ int main(int argc, char **argv) {
     int32_t last = prompt[n_prompt - 1];
     int64_t nonfinite = 0;
     double lmin = 0, lmax = 0, lsum = 0, lsq = 0;
+    const int64_t nvocab = cfg.vocab_size;
+    float *lbuf = (float *)oom(malloc((size_t)nvocab * sizeof(float)));
+    long long syncs0 = 0, hits0 = 0, miss0 = 0;
+#if defined(QK_E2E_GPU)
+    qk_dec D;
+    if (chain) qk_dec_init(&D, m);
+    syncs0 = qk_seam_gpu_calls;
+    hits0 = qk_seam_pf_hits;
+    miss0 = qk_seam_pf_misses;
+#else
+    (void)chain;
+#endif
+    const double td = e2e_now();       /* decode clock: after the device step's one-time setup */
     for (int32_t g = 0; g < n_gen; g++) {
-        logits = slm_forward_step(c, last, pos);
-        int32_t next = sample_argmax(logits);
-        if (g == 0 || g == n_gen - 1) {
-            int64_t nv = tensor_nelements(logits);
-            lmin = lmax = logits->data[0];
+        const int stats = g == 0 || g == n_gen - 1;
+        int32_t next;
+        const float *lv = NULL;
+#if defined(QK_E2E_GPU)
+        if (chain) {
+            next = qk_decode_step(c, &D, last, pos, stats ? lbuf : NULL);
+            lv = lbuf;
+        } else
+#endif
+        {
+            logits = slm_forward_step(c, last, pos);
+            next = sample_argmax(logits);
+            lv = logits->data;
+        }
+        if (stats) {
+            lmin = lmax = lv[0];
             lsum = lsq = 0;
-            for (int64_t i = 0; i < nv; i++) {
-                float v = logits->data[i];
+            for (int64_t i = 0; i < nvocab; i++) {
+                float v = lv[i];
                 if (!(v == v) || v > 3e38f || v < -3e38f) nonfinite++;
                 lmin = v < lmin ? v : lmin;
                 lmax = v > lmax ? v : lmax;
@@ -420,6 +456,16 @@ int main(int argc, char **argv) {
         if ((g + 1) % 32 == 0) fprintf(stderr, "[e2e] decoded %d / %d\n", g + 1, n_gen);
     }
     double t2 = e2e_now();
+    /* host synchronisations with the GPU per decoded token: every seam
+       matmul that reached the GPU, plus the device step's own waits */
+    double syncs_per_tok = 0, pf_hits = 0, pf_misses = 0;
+#if defined(QK_E2E_GPU)
+    syncs_per_tok = (double)(qk_seam_gpu_calls - syncs0 + (chain ? D.syncs : 0)) / n_gen;
+    pf_hits = (double)(qk_seam_pf_hits - hits0);
+    pf_misses = (double)(qk_seam_pf_misses - miss0);
+#else
+    (void)syncs0; (void)hits0; (void)miss0;
+#endif
 
     int32_t distinct = 0;
     for (int32_t i = 0; i < n_gen; i++) {
@@ -430,6 +476,7 @@ int main(int argc, char **argv) {
     const double nv = (double)cfg.vocab_size;
     printf("{\"mode\": \"%s\", \"source\": \"%s\", \"tier\": \"%s\", \"layers\": %d, \"prompt\": %d, \"gen\": %d, \"seed\": %llu, "
            "\"prefill_s\": %.6f, \"decode_s\": %.6f, \"prefill_tok_s\": %.3f, \"decode_tok_s\": %.3f, "
+           "\"decode_path\": \"%s\", \"host_syncs_per_token\": %.2f, \"prefetch_hits\": %.0f, \"prefetch_misses\": %.0f, "
            "\"distinct_tokens\": %d, \"nonfinite_logits\": %lld, \"last_logits\": {\"min\": %.6g, \"max\": %.6g, "
            "\"mean\": %.6g, \"std\": %.6g}, \"tokens\": [",
 #if defined(QK_E2E_GPU)
@@ -437,8 +484,14 @@ int main(int argc, char **argv) {
 #else
            "cpu",
 #endif
-           load_path ? "gguf" : "built", simd_dispatch_label(), n_layers, n_prompt, n_gen, (unsigned long long)seed, t1 - t0, t2 - t1,
-           n_prompt / (t1 - t0), n_gen / (t2 - t1), distinct, (long long)nonfinite, lmin, lmax, lsum / nv,
+           load_path ? "gguf" : "built", simd_dispatch_label(), n_layers, n_prompt, n_gen, (unsigned long long)seed, t1 - t0, t2 - td,
+           n_prompt / (t1 - t0), n_gen / (t2 - td),
+#if defined(QK_E2E_GPU)
+           chain ? "gpu-chain" : "gpu-seam",
+#else
+           "cpu",
+#endif
+           syncs_per_tok, pf_hits, pf_misses, distinct, (long long)nonfinite, lmin, lmax, lsum / nv,
            sqrt(lsq / nv - (lsum / nv) * (lsum / nv)));
     for (int32_t i = 0; i < n_gen; i++) printf("%s%d", i ? ", " : "", toks[i]);
     printf("]}\n");

@@ -96,6 +96,9 @@ class QK:
         for f in ("hip_dequant_q4k", "hip_dequant_q5k", "hip_dequant_q6k"):
             getattr(L, f).argtypes = [_vp, _i64, _vp, _vp]
         L.hip_lmhead_q6k_argmax_topk.argtypes = [_vp, _i64, _i64, _vp, C.c_int, _vp, _vp, _vp, _vp, _vp]
+        L.hip_add_rmsnorm_q8k.argtypes = [_vp, _vp, _vp, C.c_float, _i64, _i64, _vp, _vp, _vp, _vp]
+        L.hip_silu_f32.argtypes = [_vp, _i64, _vp, _vp]
+        L.hip_swiglu_q8k.argtypes = [_vp, _vp, _i64, _i64, _vp, _vp, _vp]
         L.hip_qk_register_weight.argtypes = [_vp, C.c_int, _i64, _i64]
         L.hip_qk_unregister_weight.argtypes = [_vp]
         L.hip_qk_device_weight.argtypes = [_vp]
@@ -227,6 +230,35 @@ class QK:
                                                     _dp(ti) if topk else None, _dp(tv) if topk else None,
                                                     self._stream()))
         return logits, am, ti[:topk], tv[:topk]
+
+    def add_rmsnorm_q8k(self, h, delta, w, eps, h_out=None, x_out=None, xq=None):
+        """h, delta (or None): (m, k) fp32; w: k fp32. Writes h + delta to
+        h_out, the normalized rows to x_out and their Q8_K rows to xq (each
+        optional; pass the tensors to be filled)."""
+        m, k = h.shape
+        for t in (delta, h_out, x_out):
+            _need(t, 4 * m * k, "row")
+        _need(w, 4 * k, "w")
+        _need(xq, m * (k // 256) * Q8K_BYTES, "xq")
+        self._ck(self.L.hip_add_rmsnorm_q8k(_dp(h), _dp(delta), _dp(w), float(np.float32(eps)), m, k, _dp(h_out),
+                                            _dp(x_out), _dp(xq), self._stream()))
+
+    def silu(self, x, y=None):
+        import torch
+        if y is None:
+            y = torch.empty_like(x)
+        _need(y, _nbytes(x), "y")
+        self._ck(self.L.hip_silu_f32(_dp(x), x.numel(), _dp(y), self._stream()))
+        return y
+
+    def swiglu_q8k(self, gate, up, act=None, xq=None):
+        """gate, up: (m, k) fp32; writes silu(gate) * up to act and/or its
+        Q8_K rows to xq."""
+        m, k = gate.shape
+        _need(up, 4 * m * k, "up")
+        _need(act, 4 * m * k, "act")
+        _need(xq, m * (k // 256) * Q8K_BYTES, "xq")
+        self._ck(self.L.hip_swiglu_q8k(_dp(gate), _dp(up), m, k, _dp(act), _dp(xq), self._stream()))
 
     # -- host seam --------------------------------------------------------------
     def matmul_host(self, wtype, w_np, out_f, k, x_np):
