@@ -292,6 +292,39 @@ int hip_lmhead_q6k_argmax_topk_noalloc(const void *w, int64_t n, int64_t k,
                                        int32_t *topk_idx, float *topk_val,
                                        void *stream);
 
+/* ---- device layer: sampler chain ------------------------------------ */
+
+/* The fields of struct slm_sampler (slm/slm.h:117-124). */
+typedef struct {
+    float   temperature;        /* <= 0: greedy argmax                   */
+    int32_t top_k;              /* <= 0: 256; capped at 256              */
+    float   top_p;              /* (0, 1): nucleus; else off             */
+    float   min_p;              /* > 0: drop below min_p * top prob      */
+    float   repetition_penalty; /* 1: off                                */
+    int32_t repetition_window;  /* <= 0: the whole history               */
+} qk_sampler;
+
+/* One sampling step of slm_generate_raw (slm/slm.c:309-324) on device
+ * logits: the n_mask ids in mask (host array; eos / eot while fewer than
+ * min_new tokens exist) are set to -inf, then sample_with
+ * (slm/sampler.c:134-181): the repetition penalty over the last
+ * repetition_window of history (device, hist_n ids), applied in place as
+ * the reference does; with temperature <= 0 the first index of the
+ * largest logit (sample_argmax); otherwise topk_collect, the temperature
+ * softmax over its slots, the stable descending sort, top-p, min-p and
+ * the roulette pick with one draw from the reference's rng, whose two
+ * words (struct rng, slm/model.c:414) live in device memory at rng and
+ * advance exactly as rng_next does. *token (device) receives the id; the
+ * pick, the penalized logits and the rng state are bit for bit the
+ * reference's, NaN logits included. token may point into history (at
+ * entry hist_n) to append the pick. Scratch is per stream, as for the LM
+ * head. n is at most QK_SAMPLE_MAX_N. */
+#define QK_SAMPLE_MAX_MASK 2
+#define QK_SAMPLE_MAX_N 262144
+int hip_sample(float *logits, int64_t n, const qk_sampler *sp, uint64_t *rng,
+               const int32_t *history, int32_t hist_n, const int32_t *mask,
+               int32_t n_mask, int32_t *token, void *stream);
+
 /* ---- host seam ------------------------------------------------------ */
 
 /* Upload the n x k weight matrix at host address `host_w` (GGUF type

@@ -94,6 +94,10 @@ class Oracle:
         L.qko_silu.restype = None
         L.qko_swiglu.argtypes = [_i64, _vp, _vp, _vp]
         L.qko_swiglu.restype = None
+        L.qko_rng_seed.argtypes = [C.c_uint64, _vp]
+        L.qko_rng_seed.restype = None
+        L.qko_sample.argtypes = [_vp, _i64, C.c_float, C.c_int32, C.c_float, C.c_float, C.c_float, C.c_int32, _vp, _vp, C.c_int32, _vp, C.c_int32]
+        L.qko_sample.restype = C.c_int32
 
     # -- scalars -------------------------------------------------------
     def f16_to_f32(self, h):
@@ -231,6 +235,30 @@ class Oracle:
         self.L.qko_add_rmsnorm(*a)
         return 0
 
+    def _rng_seed(self, *a):
+        self.L.qko_rng_seed(*a)
+
+    def _sample(self, *a):
+        return self.L.qko_sample(*a)
+
+    # -- sampler chain (shared by Oracle and Ref) -------------------------
+    def rng_seed(self, seed):
+        st = np.zeros(2, np.uint64)
+        self._rng_seed(C.c_uint64(seed), _ptr(st))
+        return st
+
+    def sample(self, logits, sp, st, history=(), mask=()):
+        """One step of slm_generate_raw's sampling: returns (token, penalized
+        logits, advanced rng state). sp: dict of slm_sampler fields."""
+        lg = np.array(logits, np.float32, copy=True)
+        st = np.array(st, np.uint64, copy=True)
+        h = np.ascontiguousarray(history, np.int32)
+        mk = np.ascontiguousarray(mask, np.int32)
+        tok = self._sample(_ptr(lg), lg.size, C.c_float(sp["temperature"]), sp["top_k"], C.c_float(sp["top_p"]),
+                           C.c_float(sp["min_p"]), C.c_float(sp["repetition_penalty"]), sp["repetition_window"],
+                           _ptr(st), _ptr(h) if h.size else None, h.size, _ptr(mk) if mk.size else None, mk.size)
+        return tok, lg, st
+
     def _silu(self, *a):
         self.L.qko_silu(*a)
 
@@ -282,6 +310,10 @@ class Ref:
         L.ref_silu.restype = None
         L.ref_swiglu.argtypes = [_i64, _vp, _vp, _vp]
         L.ref_swiglu.restype = C.c_int
+        L.ref_rng_seed.argtypes = [C.c_uint64, _vp]
+        L.ref_rng_seed.restype = None
+        L.ref_sample.argtypes = [_vp, _i64, C.c_float, C.c_int32, C.c_float, C.c_float, C.c_float, C.c_int32, _vp, _vp, C.c_int32, _vp, C.c_int32]
+        L.ref_sample.restype = C.c_int32
         L.ref_simd_init()
 
     def label(self):
@@ -402,3 +434,27 @@ class Ref:
 
     def _swiglu(self, *a):
         return self.L.ref_swiglu(*a)
+
+    def _rng_seed(self, *a):
+        self.L.ref_rng_seed(*a)
+
+    def _sample(self, *a):
+        return self.L.ref_sample(*a)
+
+    # -- sampler chain (shared by Oracle and Ref) -------------------------
+    def rng_seed(self, seed):
+        st = np.zeros(2, np.uint64)
+        self._rng_seed(C.c_uint64(seed), _ptr(st))
+        return st
+
+    def sample(self, logits, sp, st, history=(), mask=()):
+        """One step of slm_generate_raw's sampling: returns (token, penalized
+        logits, advanced rng state). sp: dict of slm_sampler fields."""
+        lg = np.array(logits, np.float32, copy=True)
+        st = np.array(st, np.uint64, copy=True)
+        h = np.ascontiguousarray(history, np.int32)
+        mk = np.ascontiguousarray(mask, np.int32)
+        tok = self._sample(_ptr(lg), lg.size, C.c_float(sp["temperature"]), sp["top_k"], C.c_float(sp["top_p"]),
+                           C.c_float(sp["min_p"]), C.c_float(sp["repetition_penalty"]), sp["repetition_window"],
+                           _ptr(st), _ptr(h) if h.size else None, h.size, _ptr(mk) if mk.size else None, mk.size)
+        return tok, lg, st

@@ -549,3 +549,114 @@ void qko_swiglu(int64_t n, const float *gate, const float *up, float *act) {
         act[i] = s * up[i];
     }
 }
+
+/* ---- the sampler chain ------------------------------------------------ */
+
+/* xoroshiro128-style step and uniform draw of the reference
+ * (slm/model.c:414-447). */
+static uint64_t o_rotl(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+
+static uint64_t o_rng_next(uint64_t *st) {
+    uint64_t s0 = st[0], s1 = st[1];
+    uint64_t out = o_rotl(s0 * 5, 7) * 9;
+    s1 ^= s0;
+    st[0] = o_rotl(s0, 24) ^ s1 ^ (s1 << 16);
+    st[1] = o_rotl(s1, 37);
+    return out;
+}
+
+static float o_rng_uniform(uint64_t *st) {
+    return (float)(o_rng_next(st) >> 40) / (float)(1u << 24);
+}
+
+/* The rng state slm_ctx_create / slm_generate_raw seed from one 64-bit
+ * value (SplitMix64, slm/model.c:431-442). */
+void qko_rng_seed(uint64_t seed, uint64_t *st) {
+    uint64_t z = seed + 0x9e3779b97f4a7c15ULL;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+    st[0] = z ^ (z >> 31);
+    z = st[0] + 0x9e3779b97f4a7c15ULL;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+    st[1] = z ^ (z >> 31);
+    if (st[0] == 0 && st[1] == 0) st[0] = 1;
+}
+
+/* One sampling step of slm_generate_raw (slm/slm.c:309-322): the ids in
+ * mask (eos / eot while fewer than min_new tokens exist) set to -inf,
+ * then sample_with (slm/sampler.c:134-181): repetition penalty in place
+ * (:49-63), greedy argmax when temperature <= 0, else topk_collect
+ * (:70-93), topk_softmax (:97-111), topk_sort_desc (:116-129), top-p,
+ * min-p and the roulette pick with one uniform draw. logits are modified
+ * in place; st (2 words) advances on the sampling path only. */
+int32_t qko_sample(float *logits, int64_t n, float temperature, int32_t top_k, float top_p, float min_p,
+                   float penalty, int32_t window, uint64_t *st, const int32_t *history, int32_t hist_n,
+                   const int32_t *mask, int32_t n_mask) {
+    for (int32_t i = 0; i < n_mask; i++)
+        if (mask[i] >= 0 && mask[i] < n) logits[mask[i]] = -INFINITY;
+    if (penalty != 1.0f && hist_n != 0) {
+        int32_t start = (window > 0 && window < hist_n) ? hist_n - window : 0;
+        for (int32_t i = start; i < hist_n; i++) {
+            int32_t t = history[i];
+            if (t >= 0 && (int64_t)t < n) {
+                float lv = logits[t];
+                logits[t] = lv > 0.0f ? lv / penalty : lv * penalty;
+            }
+        }
+    }
+    if (temperature <= 0.0f) return qko_argmax(logits, n);
+    int32_t idx[256];
+    float val[256];
+    int32_t k = top_k > 0 ? top_k : 256;
+    if (k > 256) k = 256;
+    int32_t filled = qko_topk_collect(logits, n, k, idx, val);
+    /* softmax over the survivors */
+    float m = val[0];
+    for (int32_t j = 1; j < filled; j++)
+        if (val[j] > m) m = val[j];
+    float sum = 0.0f;
+    for (int32_t j = 0; j < filled; j++) {
+        float z = (val[j] - m) / temperature;
+        val[j] = expf(z);
+        sum += val[j];
+    }
+    if (sum > 0.0f)
+        for (int32_t j = 0; j < filled; j++) val[j] /= sum;
+    /* stable descending insertion sort */
+    for (int32_t i = 1; i < filled; i++) {
+        float v = val[i];
+        int32_t id = idx[i], j = i - 1;
+        while (j >= 0 && val[j] < v) {
+            val[j + 1] = val[j];
+            idx[j + 1] = idx[j];
+            j--;
+        }
+        val[j + 1] = v;
+        idx[j + 1] = id;
+    }
+    int32_t cutoff = filled;
+    if (top_p > 0.0f && top_p < 1.0f) {
+        float acc = 0.0f;
+        for (int32_t j = 0; j < filled; j++) {
+            acc += val[j];
+            if (acc >= top_p) { cutoff = j + 1; break; }
+        }
+    }
+    if (min_p > 0.0f) {
+        float thresh = min_p * val[0];
+        int32_t j = 1;
+        while (j < cutoff && val[j] >= thresh) j++;
+        cutoff = j;
+    }
+    float tot = 0.0f;
+    for (int32_t j = 0; j < cutoff; j++) tot += val[j];
+    float u = o_rng_uniform(st) * tot;
+    float c = 0.0f;
+    int32_t picked = 0;
+    for (int32_t j = 0; j < cutoff; j++) {
+        c += val[j];
+        if (u <= c) { picked = j; break; }
+    }
+    return idx[picked];
+}

@@ -65,6 +65,13 @@ void qko_silu(int64_t n, const float *x, float *y);
 void qko_swiglu(int64_t n, const float *gate, const float *up, float *act);
 
 int32_t qko_argmax(const float *v, int64_t n);
+
+/* Sampler chain (sample_with plus the min_new masking); st is the
+ * reference's two-word rng state, advanced on the sampling path. */
+void qko_rng_seed(uint64_t seed, uint64_t *st);
+int32_t qko_sample(float *logits, int64_t n, float temperature, int32_t top_k, float top_p, float min_p,
+                   float penalty, int32_t window, uint64_t *st, const int32_t *history, int32_t hist_n,
+                   const int32_t *mask, int32_t n_mask);
 int32_t qko_topk_collect(const float *v, int64_t n, int32_t k,
                          int32_t *idx, float *val);
 

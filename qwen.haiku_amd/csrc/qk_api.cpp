@@ -47,7 +47,7 @@ struct Lane {
     void *hy = nullptr;   size_t hy_cap = 0;
 };
 
-// LM-head selection scratch of one caller stream.
+// Selection scratch (LM head, sampler) of one caller stream.
 struct Sel {
     void *p = nullptr;
     size_t cap = 0;
@@ -565,13 +565,13 @@ int stream_scratch(hipStream_t stream, size_t need, void **out) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
             return fail(QK_ERR_ARG,
-                        "LM-head scratch for this stream must grow to %zu bytes, which allocates, and the stream "
-                        "is capturing: make one call of this size on the stream before capture, or use "
-                        "hip_lmhead_q6k_argmax_topk_noalloc",
+                        "selection scratch for this stream must grow to %zu bytes, which allocates, and the "
+                        "stream is capturing: make one call of this size on the stream before capture (for the "
+                        "LM head, or use hip_lmhead_q6k_argmax_topk_noalloc)",
                         need);
         const size_t sz = need + need / 4 + 4096;
         void *p = nullptr;
-        HIP_OK(hipMalloc(&p, sz), "hipMalloc(lmhead scratch)");
+        HIP_OK(hipMalloc(&p, sz), "hipMalloc(selection scratch)");
         if (e.p) s.retired.push_back(e.p);
         e.p = p;
         e.cap = sz;
@@ -595,6 +595,30 @@ int hip_lmhead_q6k_argmax_topk(const void *w, int64_t n, int64_t k, const void *
     if ((rc = stream_scratch(stream_of(stream), lmhead_scratch_bytes(n, topk, logits == nullptr), &scratch)))
         return rc;
     return lmhead_launch(w, n, k, xq, topk, logits, argmax, topk_idx, topk_val, scratch, stream_of(stream));
+}
+
+int hip_sample(float *logits, int64_t n, const qk_sampler *sp, uint64_t *rng, const int32_t *history,
+               int32_t hist_n, const int32_t *mask, int32_t n_mask, int32_t *token, void *stream) {
+    int rc = require_init();
+    if (rc) return rc;
+    if (!logits || !sp || !token) return fail(QK_ERR_ARG, "null pointer");
+    if (n < 1 || n > QK_SAMPLE_MAX_N) return fail(QK_ERR_ARG, "n=%lld logits (1..%d)", (long long)n, QK_SAMPLE_MAX_N);
+    if (hist_n < 0 || (hist_n > 0 && !history)) return fail(QK_ERR_ARG, "history of %d tokens", hist_n);
+    if (n_mask < 0 || n_mask > QK_SAMPLE_MAX_MASK || (n_mask > 0 && !mask))
+        return fail(QK_ERR_ARG, "n_mask=%d (0..%d)", n_mask, QK_SAMPLE_MAX_MASK);
+    if (sp->temperature > 0.0f && (!rng || !aligned(rng, 8)))
+        return fail(QK_ERR_ARG, "sampling needs the 8-byte aligned rng state");
+    if (!aligned(logits, 4) || !aligned(token, 4) || !aligned(history, 4))
+        return fail(QK_ERR_ARG, "misaligned logits/token/history");
+    int32_t k = sp->top_k > 0 ? sp->top_k : QK_TOPK_MAX;    // slm/sampler.c:143-144
+    if (k > QK_TOPK_MAX) k = QK_TOPK_MAX;
+    void *scratch = nullptr;
+    if ((rc = stream_scratch(stream_of(stream), qk::sample_scratch_bytes(n, k), &scratch))) return rc;
+    HIP_OK(qk::launch_sample(logits, n, sp->temperature, k, sp->top_p, sp->min_p, sp->repetition_penalty,
+                             sp->repetition_window, rng, history, hist_n, mask, n_mask, token, scratch,
+                             stream_of(stream)),
+           "sample launch");
+    return QK_OK;
 }
 
 int hip_lmhead_q6k_argmax_topk_noalloc(const void *w, int64_t n, int64_t k, const void *xq, int topk,

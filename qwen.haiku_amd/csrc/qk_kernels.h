@@ -60,6 +60,12 @@ hipError_t launch_add_rmsnorm(const float *h, const float *delta, const float *w
 hipError_t launch_silu(const float *src, float *dst, int64_t n, hipStream_t s);
 hipError_t launch_swiglu(const float *gate, const float *up, int64_t n, float *act, uint8_t *xq, hipStream_t s);
 
+// Sampler chain (qk_sample.hip); scratch must hold sample_scratch_bytes.
+size_t sample_scratch_bytes(int64_t n, int32_t k);
+hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k, float top_p, float min_p,
+                         float penalty, int32_t window, uint64_t *rng, const int32_t *history, int32_t hist_n,
+                         const int32_t *mask, int32_t n_mask, int32_t *token, void *scratch, hipStream_t s);
+
 // Prefill GEMM (int8 MFMA); y[t*n + j].
 hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, const uint8_t *xq,
                        int64_t m, float *y, int fused, hipStream_t s);

@@ -1,0 +1,732 @@
+// qk_sample.hip -- the sampler chain on the device (gfx950): repetition
+// penalty, greedy argmax, or topk_collect -> softmax -> sort -> top-p ->
+// min-p -> roulette pick with the reference's rng, bit for bit.
+//
+// The reference (slm/sampler.c:134-181) scans the vocabulary once with
+// topk_collect (:70-93): k slots filled with the first k logits, then each
+// later logit that is strictly greater than the smallest slot value
+// replaces the first slot holding that value. The softmax sums the
+// survivors in slot order, so the device must end with the same slots in
+// the same order, not just the same set. It does so without scanning the
+// vocabulary serially:
+//
+//  * after any prefix the slots hold the k largest values of the prefix
+//    (ties kept by the earlier element), so logit i (i >= k) enters iff
+//    fewer than k earlier logits are >= it;
+//  * per block of logits: the block's k largest values, sorted
+//    (k_smp_blocks); the k-th largest value T_b of everything before the
+//    block, by bisection over the union of those lists (held in LDS);
+//    then, for the block's logits above T_b, the exact count of earlier
+//    logits >= them (the earlier logits above T_b, fewer than k, plus the
+//    block's own earlier candidates). Those with a count below k are the
+//    entering events, listed in index order with their values
+//    (k_smp_events);
+//  * one wave gathers the events into LDS, replays them in order on the k
+//    slots, then runs the rest of the chain on the k survivors as the
+//    reference writes it (k_smp_finish).
+// A NaN logit after the first k never enters and never compares >=, so it
+// counts as -inf; a NaN among the first k breaks the prefix argument
+// (comparisons with it are false), so k_smp_finish then runs
+// topk_collect literally.
+#include "qk_dev.h"
+#include "qk_expf.h"
+#include "qk_kernels.h"
+
+namespace qk {
+
+constexpr int SMP_BLOCK = 1024;                        // logits per selection block
+constexpr int SMP_KMAX = 256;
+
+// Order-preserving integer key of a non-NaN float, with -0 and +0 one key
+// as IEEE comparisons (the reference's < and >) treat them.
+__device__ __forceinline__ uint32_t fkey(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) == 0) return 0x80000000u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float fkey_inv(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// Wave-wide reductions through DPP within each 16-lane row, then the four
+// row results read as uniform values (every lane gets the answer).
+__device__ __forceinline__ int32_t wave_sum_i(int32_t v) {
+    v += dpp_xor1(v);
+    v += dpp_xor2(v);
+    v += dpp_hmirror(v);
+    v += __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, true);   // row_mirror
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) +
+           __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
+}
+__device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
+    v = min(v, (uint32_t)dpp_xor1((int32_t)v));
+    v = min(v, (uint32_t)dpp_xor2((int32_t)v));
+    v = min(v, (uint32_t)dpp_hmirror((int32_t)v));
+    v = min(v, (uint32_t)__builtin_amdgcn_mov_dpp((int32_t)v, 0x140, 0xF, 0xF, true));
+    const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+    const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+    return min(min(a, b), min(c, d));
+}
+
+// ---- masking and repetition penalty ------------------------------------
+// slm_generate_raw's min_new masking (slm/slm.c:309-322), then
+// apply_rep_penalty (slm/sampler.c:49-63): for each history entry in the
+// window, in order, logits[t] = lv > 0 ? lv / penalty : lv * penalty.
+// Repeats of a token compound; different tokens are independent, so the
+// thread owning a token's first occurrence applies its count in turn.
+constexpr int SMP_HIST_LDS = 4096;                    // window entries staged in LDS
+
+__global__ __launch_bounds__(256) void k_smp_penalty(float *logits, int64_t n, const int32_t *history,
+                                                     int32_t start, int32_t hist_n, float penalty, int32_t m0,
+                                                     int32_t m1, int32_t n_mask) {
+    __shared__ int32_t hw[SMP_HIST_LDS];
+    if ((int)threadIdx.x < n_mask) {
+        const int32_t t = threadIdx.x ? m1 : m0;
+        if (t >= 0 && t < n) logits[t] = -__builtin_inff();
+    }
+    const int32_t w = hist_n - start;
+    const bool staged = w <= SMP_HIST_LDS;
+    if (staged)
+        for (int32_t i = threadIdx.x; i < w; i += 256) hw[i] = history[start + i];
+    __syncthreads();
+    if (penalty == 1.0f || hist_n == 0) return;
+    const int32_t *h = staged ? hw : history + start;
+    for (int32_t i = threadIdx.x; i < w; i += 256) {
+        const int32_t t = h[i];
+        if (t < 0 || t >= n) continue;
+        bool first = true;
+        for (int32_t j = 0; j < i && first; j++) first = h[j] != t;
+        if (!first) continue;
+        int32_t reps = 1;
+        for (int32_t j = i + 1; j < w; j++) reps += h[j] == t;
+        float v = logits[t];
+        for (int32_t r = 0; r < reps; r++) v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
+        logits[t] = v;
+    }
+}
+
+// ---- greedy: sample_argmax (slm/model.c:401-412) ---------------------------
+// First index of the largest non-NaN logit; index 0 when logits[0] is NaN
+// (no later comparison can succeed then). Per block, then over blocks.
+struct ArgPart {
+    float v;
+    int32_t i;                                         // -1: no non-NaN logit in the block
+};
+
+__device__ __forceinline__ void arg_better(float &bv, int32_t &bi, float v, int32_t i) {
+    if (i < 0) return;
+    if (bi < 0 || v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+__device__ __forceinline__ void arg_reduce_wg(float &bv, int32_t &bi, ArgPart *sh) {
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int32_t oi = __shfl_xor(bi, o);
+        arg_better(bv, bi, ov, oi);
+    }
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = ArgPart{bv, bi};
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int w = 1; w < 4; w++) arg_better(bv, bi, sh[w].v, sh[w].i);
+}
+
+__global__ __launch_bounds__(256) void k_smp_argmax_part(const float *logits, int64_t n, ArgPart *part) {
+    __shared__ ArgPart sh[4];
+    float bv = 0.0f;
+    int32_t bi = -1;
+    const int64_t base = (int64_t)blockIdx.x * SMP_BLOCK;
+    for (int j = 0; j < SMP_BLOCK / 256; j++) {
+        const int64_t i = base + j * 256 + threadIdx.x;
+        if (i < n) {
+            const float v = logits[i];
+            if (v == v) arg_better(bv, bi, v, (int32_t)i);
+        }
+    }
+    arg_reduce_wg(bv, bi, sh);
+    if (threadIdx.x == 0) part[blockIdx.x] = ArgPart{bv, bi};
+}
+
+__global__ __launch_bounds__(256) void k_smp_argmax_final(const float *logits, const ArgPart *part, int32_t nblk,
+                                                          int32_t *token) {
+    __shared__ ArgPart sh[4];
+    float bv = 0.0f;
+    int32_t bi = -1;
+    for (int32_t b = threadIdx.x; b < nblk; b += 256) arg_better(bv, bi, part[b].v, part[b].i);
+    arg_reduce_wg(bv, bi, sh);
+    if (threadIdx.x == 0) {
+        const float v0 = logits[0];
+        *token = (v0 != v0 || bi < 0) ? 0 : bi;
+    }
+}
+
+// ---- sampling path ------------------------------------------------------------
+// Blocks of sb logits (a power of two >= 1024, chosen by the launcher so
+// that nblk * k <= SMP_LIST_MAX). A NaN logit at an index >= k never
+// enters the slots and never compares >= anything, so it is read as -inf
+// here; a NaN among the first k (the initial fill) is flagged instead and
+// k_smp_finish then runs topk_collect literally.
+constexpr int SMP_LIST_MAX = 16384;                    // floats of top-k lists (64 KB of LDS)
+
+__device__ __forceinline__ float smp_load(const float *logits, int64_t n, int64_t i, int32_t k, int32_t &nan_fill) {
+    if (i >= n) return -__builtin_inff();
+    const float x = logits[i];
+    if (x != x) {
+        if (i < k) nan_fill = 1;
+        return -__builtin_inff();
+    }
+    return x;
+}
+
+// Per block: its k largest values (a multiset, in no particular order)
+// and whether the initial fill holds a NaN. The k-th largest key T is
+// found by bisection over the block's keys (held in registers); the list
+// is every value above T plus copies of T up to k.
+constexpr int SMP_PER_MAX = 16;                        // logits per thread (sb <= 4096)
+
+__global__ __launch_bounds__(256) void k_smp_blocks(const float *logits, int64_t n, int32_t k, int32_t sb,
+                                                    float *tops, int32_t *nan_flag) {
+    __shared__ int32_t wsum[4];
+    __shared__ int32_t cnt_sh;
+    const int64_t base = (int64_t)blockIdx.x * sb;
+    const int per = sb / 256;
+    int32_t nan_fill = 0;
+    uint32_t key[SMP_PER_MAX];
+#pragma unroll
+    for (int j = 0; j < SMP_PER_MAX; j++)
+        key[j] = j < per ? fkey(smp_load(logits, n, base + threadIdx.x * per + j, k, nan_fill)) : 0u;
+    if (threadIdx.x == 0) cnt_sh = 0;
+    uint32_t t = 0;                                    // largest key with count(>= key) >= k
+    for (int bit = 31; bit >= 0; bit--) {
+        const uint32_t cand = t | (1u << bit);
+        int32_t c = 0;
+#pragma unroll
+        for (int j = 0; j < SMP_PER_MAX; j++) c += (j < per) & (key[j] >= cand);
+        c = wave_sum_i(c);
+        if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = c;
+        __syncthreads();
+        const int32_t total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+        __syncthreads();
+        if (total >= k) t = cand;
+    }
+    float *out = tops + (int64_t)blockIdx.x * k;
+#pragma unroll
+    for (int j = 0; j < SMP_PER_MAX; j++)
+        if (j < per && key[j] > t) out[atomicAdd(&cnt_sh, 1)] = fkey_inv(key[j]);   // LDS counter
+    __syncthreads();
+    for (int32_t j = cnt_sh + threadIdx.x; j < k; j += 256) out[j] = fkey_inv(t);
+    const int32_t nf = wave_sum_i(nan_fill);
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = nf;
+    __syncthreads();
+    if (threadIdx.x == 0) nan_flag[blockIdx.x] = (wsum[0] | wsum[1] | wsum[2] | wsum[3]) != 0;
+}
+
+// Block b's entering events. With P = the logits before the block and
+// T = the k-th largest of P (bisection over the keys of the earlier
+// blocks' top-k lists, which hold every element of P that can matter),
+// a logit of the block can enter only if it exceeds T; for such a logit v
+// the count of earlier logits >= v is the count in R = {x in P : x > T}
+// (fewer than k elements, all inside those lists) plus the count among
+// the block's earlier candidates. Events are candidates at index >= k
+// whose count is below k, written in index order with their values.
+__device__ __forceinline__ int32_t wg_sum(int32_t c, int32_t *wsum) {
+    c = wave_sum_i(c);
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = c;
+    __syncthreads();
+    const int32_t total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    __syncthreads();
+    return total;
+}
+
+// count of keys >= x among keys[0, n4 * 4), n4 uint4 groups split over
+// the workgroup; four independent LDS reads in flight per step
+__device__ __forceinline__ int32_t count_keys_ge(const uint4 *keys4, int32_t n4, uint32_t x) {
+    int32_t c = 0;
+    int32_t j = threadIdx.x;
+    for (; j + 768 < n4; j += 1024) {
+        const uint4 a = keys4[j], b = keys4[j + 256], d = keys4[j + 512], e = keys4[j + 768];
+        c += (a.x >= x) + (a.y >= x) + (a.z >= x) + (a.w >= x) + (b.x >= x) + (b.y >= x) + (b.z >= x) +
+             (b.w >= x) + (d.x >= x) + (d.y >= x) + (d.z >= x) + (d.w >= x) + (e.x >= x) + (e.y >= x) +
+             (e.z >= x) + (e.w >= x);
+    }
+    for (; j < n4; j += 256) {
+        const uint4 a = keys4[j];
+        c += (a.x >= x) + (a.y >= x) + (a.z >= x) + (a.w >= x);
+    }
+    return c;
+}
+
+__global__ __launch_bounds__(256) void k_smp_events(const float *logits, int64_t n, int32_t k, int32_t sb,
+                                                    int32_t lcap, const float *tops, int32_t *ev_idx, float *ev_val,
+                                                    int32_t *ev_n) {
+    extern __shared__ uint4 lds4[];
+    const int32_t b = blockIdx.x;
+    const int32_t nlist = b * k;                       // prefix list elements (<= lcap, lcap % 4 == 0)
+    uint32_t *keys = reinterpret_cast<uint32_t *>(lds4);
+    float *cv = reinterpret_cast<float *>(keys + lcap);   // sb candidate values
+    int32_t *ci = reinterpret_cast<int32_t *>(cv + sb);   // sb candidate indices
+    float *rp = reinterpret_cast<float *>(ci + sb);    // R: the prefix values above T (< k)
+    __shared__ int32_t wsum[4];
+    __shared__ int32_t nr_sh, ncand_sh;
+    const int64_t base = (int64_t)b * sb;
+    const int32_t n4 = (nlist + 3) >> 2;
+    for (int32_t j = threadIdx.x; j < n4 * 4; j += 256) keys[j] = j < nlist ? fkey(tops[j]) : 0u;   // 0: below all
+    if (threadIdx.x == 0) nr_sh = 0;
+    __syncthreads();
+    uint32_t tkey = 0;
+    if (b > 0) {                                       // earlier blocks are full: sb >= k
+        for (int bit = 31; bit >= 0; bit--) {
+            const uint32_t cand = tkey | (1u << bit);
+            if (wg_sum(count_keys_ge(lds4, n4, cand), wsum) >= k) tkey = cand;
+        }
+        for (int32_t j = threadIdx.x; j < nlist; j += 256)
+            if (keys[j] > tkey) rp[atomicAdd(&nr_sh, 1)] = fkey_inv(keys[j]);   // LDS counter; order irrelevant
+    }
+    // candidates in index order: thread t owns elements [t*per, t*per + per)
+    const int per = sb / 256;                          // 4 .. 16
+    int32_t flag = 0, nan_fill = 0;
+    float x[SMP_PER_MAX];
+#pragma unroll
+    for (int j = 0; j < SMP_PER_MAX; j++) {
+        x[j] = j < per ? smp_load(logits, n, base + threadIdx.x * per + j, k, nan_fill) : -__builtin_inff();
+        const bool c = j < per && (b > 0 ? fkey(x[j]) > tkey : x[j] > -__builtin_inff());
+        flag |= (int32_t)c << j;
+    }
+    const int32_t mycount = __builtin_popcount(flag);
+    int32_t incl = mycount;                            // inclusive scan within the wave
+    for (int o = 1; o < 64; o <<= 1) {
+        const int32_t y = __shfl_up(incl, o);
+        if ((threadIdx.x & 63) >= o) incl += y;
+    }
+    if ((threadIdx.x & 63) == 63) wsum[threadIdx.x >> 6] = incl;
+    __syncthreads();
+    int32_t off = incl - mycount;
+    for (int w = 0; w < (int)(threadIdx.x >> 6); w++) off += wsum[w];
+    if (threadIdx.x == 255) ncand_sh = off + mycount;
+#pragma unroll
+    for (int j = 0; j < SMP_PER_MAX; j++)
+        if (flag >> j & 1) {
+            cv[off] = x[j];                            // a candidate is never NaN
+            ci[off] = (int32_t)(base + threadIdx.x * per + j);
+            off++;
+        }
+    __syncthreads();
+    const int32_t ncand = ncand_sh, nr = nr_sh;
+    for (int32_t c = threadIdx.x; c < ncand; c += 256) {
+        if (ci[c] < k) continue;                       // the initial fill
+        const float v = cv[c];
+        int32_t cnt = 0;
+        int32_t r = 0;
+        for (; r + 4 <= nr; r += 4) cnt += (rp[r] >= v) + (rp[r + 1] >= v) + (rp[r + 2] >= v) + (rp[r + 3] >= v);
+        for (; r < nr; r++) cnt += rp[r] >= v;
+        int32_t e = 0;
+        for (; e + 8 <= c && cnt < k; e += 8)
+            cnt += (cv[e] >= v) + (cv[e + 1] >= v) + (cv[e + 2] >= v) + (cv[e + 3] >= v) + (cv[e + 4] >= v) +
+                   (cv[e + 5] >= v) + (cv[e + 6] >= v) + (cv[e + 7] >= v);
+        for (; e < c && cnt < k; e++) cnt += cv[e] >= v;
+        if (cnt < k) ci[c] |= (int32_t)0x80000000;     // indices are < 2^31
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {                            // compact the events in order
+        int32_t written = 0;
+        for (int32_t c0 = 0; c0 < ncand; c0 += 64) {
+            const int32_t c = c0 + threadIdx.x;
+            const bool is_ev = c < ncand && ci[c] < 0;
+            const uint64_t m = __ballot(is_ev);
+            if (is_ev) {
+                const int32_t pos = written + __builtin_popcountll(m & ((1ull << threadIdx.x) - 1));
+                ev_idx[base + pos] = ci[c] & 0x7fffffff;
+                ev_val[base + pos] = cv[c];
+            }
+            written += __builtin_popcountll(m);
+        }
+        if (threadIdx.x == 0) ev_n[b] = written;
+    }
+}
+
+// One wave: the k slots (LDS), the replay of the events, then the rest of
+// sample_with on lane 0.
+struct SmpArgs {
+    float temperature, top_p, min_p;
+    int32_t k, sb, nblk;
+};
+
+__device__ __forceinline__ uint64_t rotl64(uint64_t x, int s) { return (x << s) | (x >> (64 - s)); }
+
+// rng_next then rng_uniform (slm/model.c:420-447)
+__device__ __forceinline__ float rng_uniform_dev(uint64_t *st) {
+    const uint64_t s0 = st[0];
+    uint64_t s1 = st[1];
+    const uint64_t out = rotl64(s0 * 5, 7) * 9;
+    s1 ^= s0;
+    st[0] = rotl64(s0, 24) ^ s1 ^ (s1 << 16);
+    st[1] = rotl64(s1, 37);
+    return __fdiv_rn((float)(uint32_t)(out >> 40), 16777216.0f);
+}
+
+// Slot s lives in register q = s / 64 of lane s % 64 while the events are
+// replayed; `worst` (the first slot holding the smallest value) is found
+// with a DPP minimum over the keys and a ballot per register.
+constexpr int SMP_Q = SMP_KMAX / 64;
+
+__device__ __forceinline__ void slot_min(const float (&sv)[SMP_Q], int32_t k, float &mv, int32_t &ms) {
+    uint32_t lk = 0xffffffffu;
+#pragma unroll
+    for (int q = 0; q < SMP_Q; q++)
+        if (q * 64 + (int)threadIdx.x < k) lk = min(lk, fkey(sv[q]));
+    const uint32_t mk = wave_min_u(lk);
+    ms = 0;
+#pragma unroll
+    for (int q = SMP_Q - 1; q >= 0; q--) {
+        const uint64_t m = __ballot(q * 64 + (int)threadIdx.x < k && fkey(sv[q]) == mk);
+        if (m) ms = q * 64 + __builtin_ctzll(m);
+    }
+    mv = fkey_inv(mk);
+}
+
+__device__ __forceinline__ float readlane_f(float v, int32_t l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// The events of positions [e0, e0 + 64) as lane values (idx -1 past the end).
+__device__ __forceinline__ void gather_events(const int32_t *off, int32_t nblk, int32_t sb, int32_t e0,
+                                              int32_t total, const int32_t *ev_idx, const float *ev_val,
+                                              int32_t &gi, float &gv) {
+    const int32_t e = e0 + (int32_t)threadIdx.x;
+    gi = -1;
+    gv = 0.0f;
+    if (e < total) {
+        int32_t lo = 0, hi = nblk;                     // last block with off[block] <= e
+        while (hi - lo > 1) {
+            const int32_t mid = (lo + hi) >> 1;
+            if (off[mid] <= e) lo = mid;
+            else hi = mid;
+        }
+        const int64_t a = (int64_t)lo * sb + (e - off[lo]);
+        gi = ev_idx[a];
+        gv = ev_val[a];
+    }
+}
+
+// The tail of sample_with exactly as written (slm/sampler.c:97-181) on
+// lane 0, for slots holding NaN or probabilities that come out NaN.
+__device__ void chain_literal(float *val, int32_t *idx, int32_t filled, const SmpArgs &a, uint64_t *rng,
+                              int32_t *token) {
+    float m = val[0];
+    for (int32_t j = 1; j < filled; j++)
+        if (val[j] > m) m = val[j];
+    float sum = 0.0f;
+    for (int32_t j = 0; j < filled; j++) {
+        val[j] = qk_expf(__fdiv_rn(__fsub_rn(val[j], m), a.temperature));
+        sum = __fadd_rn(sum, val[j]);
+    }
+    if (sum > 0.0f)
+        for (int32_t j = 0; j < filled; j++) val[j] = __fdiv_rn(val[j], sum);
+    for (int32_t i = 1; i < filled; i++) {
+        const float v = val[i];
+        const int32_t id = idx[i];
+        int32_t j = i - 1;
+        while (j >= 0 && val[j] < v) {
+            val[j + 1] = val[j];
+            idx[j + 1] = idx[j];
+            j--;
+        }
+        val[j + 1] = v;
+        idx[j + 1] = id;
+    }
+    int32_t cutoff = filled;
+    if (a.top_p > 0.0f && a.top_p < 1.0f) {
+        float acc = 0.0f;
+        for (int32_t j = 0; j < filled; j++) {
+            acc = __fadd_rn(acc, val[j]);
+            if (acc >= a.top_p) {
+                cutoff = j + 1;
+                break;
+            }
+        }
+    }
+    if (a.min_p > 0.0f) {
+        const float thresh = __fmul_rn(a.min_p, val[0]);
+        int32_t j = 1;
+        while (j < cutoff && val[j] >= thresh) j++;
+        cutoff = j;
+    }
+    float tot = 0.0f;
+    for (int32_t j = 0; j < cutoff; j++) tot = __fadd_rn(tot, val[j]);
+    uint64_t st[2] = {rng[0], rng[1]};
+    const float u = __fmul_rn(rng_uniform_dev(st), tot);
+    rng[0] = st[0];
+    rng[1] = st[1];
+    float c = 0.0f;
+    int32_t picked = 0;
+    for (int32_t j = 0; j < cutoff; j++) {
+        c = __fadd_rn(c, val[j]);
+        if (u <= c) {
+            picked = j;
+            break;
+        }
+    }
+    *token = idx[picked];
+}
+
+__global__ __launch_bounds__(64) void k_smp_finish(const float *logits, int64_t n, SmpArgs a, const int32_t *ev_idx,
+                                                   const float *ev_val, const int32_t *ev_n, const int32_t *nan_flag,
+                                                   uint64_t *rng, int32_t *token) {
+    __shared__ float val[SMP_KMAX];
+    __shared__ int32_t idx[SMP_KMAX];
+    __shared__ int32_t off[SMP_KMAX + 1];              // event offsets per block (nblk <= 256)
+    __shared__ float sp[SMP_KMAX];                     // probabilities in sorted order
+    __shared__ int32_t si[SMP_KMAX];
+    const int lane = threadIdx.x;
+    const int32_t k = a.k, nblk = a.nblk;
+    const int32_t filled = (int32_t)(n < k ? n : k);
+    // NaN in the fill; event offsets (wave-parallel exclusive scan, lane l
+    // owning blocks 4l .. 4l+3)
+    int32_t nf = 0, c4[4], own = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int32_t b = 4 * lane + q;
+        nf |= b < nblk ? nan_flag[b] : 0;
+        c4[q] = b < nblk ? ev_n[b] : 0;
+        own += c4[q];
+    }
+    const bool nan_in_fill = __ballot(nf != 0) != 0;
+    int32_t incl = own;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int32_t y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+    }
+    int32_t acc = incl - own;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        if (4 * lane + q <= nblk) off[4 * lane + q] = acc;
+        acc += c4[q];
+    }
+    const int32_t total = __builtin_amdgcn_readlane(incl, 63);
+    if (lane == 0) off[nblk] = total;
+    float sv[SMP_Q];
+    int32_t sx[SMP_Q];
+#pragma unroll
+    for (int q = 0; q < SMP_Q; q++) {
+        const int32_t s_ = q * 64 + lane;
+        sv[q] = s_ < filled ? logits[s_] : 0.0f;
+        sx[q] = s_;
+    }
+    __syncthreads();
+    if (!nan_in_fill && n > k && total > 0) {
+        float mv;
+        int32_t ms;
+        slot_min(sv, k, mv, ms);
+        int32_t gi, ni;
+        float gv, nv;
+        gather_events(off, nblk, a.sb, 0, total, ev_idx, ev_val, gi, gv);
+        for (int32_t e0 = 0; e0 < total; e0 += 64) {
+            gather_events(off, nblk, a.sb, e0 + 64, total, ev_idx, ev_val, ni, nv);   // next batch in flight
+            const int32_t cnt = total - e0 < 64 ? total - e0 : 64;
+            for (int32_t j = 0; j < cnt; j++) {
+                const float v = readlane_f(gv, j);
+                if (!(v > mv)) continue;               // not reached when the events are exact
+                const int32_t i = __builtin_amdgcn_readlane(gi, j);
+                const int32_t q = ms >> 6;
+                if (lane == (ms & 63)) {
+#pragma unroll
+                    for (int r = 0; r < SMP_Q; r++)
+                        if (r == q) {
+                            sv[r] = v;
+                            sx[r] = i;
+                        }
+                }
+                slot_min(sv, k, mv, ms);
+            }
+            gi = ni;
+            gv = nv;
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < SMP_Q; q++) {
+        const int32_t s_ = q * 64 + lane;
+        if (s_ < filled) {
+            val[s_] = sv[q];
+            idx[s_] = sx[q];
+        }
+    }
+    __syncthreads();
+    if (nan_in_fill) {
+        if (lane == 0) {
+            if (n > k)                                 // topk_collect as written (slm/sampler.c:74-92)
+                for (int64_t i = k; i < n; i++) {
+                    const float lv = logits[i];
+                    int32_t worst = 0;
+                    for (int32_t j = 1; j < k; j++)
+                        if (val[j] < val[worst]) worst = j;
+                    if (lv > val[worst]) {
+                        idx[worst] = (int32_t)i;
+                        val[worst] = lv;
+                    }
+                }
+            chain_literal(val, idx, filled, a, rng, token);
+        }
+        return;
+    }
+    // topk_softmax (slm/sampler.c:97-111): the max (its value is all that
+    // matters), the exponentials, their sum in slot order, the division
+    uint32_t mk = 0;
+#pragma unroll
+    for (int q = 0; q < SMP_Q; q++)
+        if (q * 64 + lane < filled) mk = max(mk, fkey(sv[q]));
+    mk = ~wave_min_u(~mk);
+    const float m = fkey_inv(mk);
+    float pe[SMP_Q];
+    int32_t bad = 0;
+#pragma unroll
+    for (int q = 0; q < SMP_Q; q++) {
+        pe[q] = q * 64 + lane < filled ? qk_expf(__fdiv_rn(__fsub_rn(sv[q], m), a.temperature)) : 0.0f;
+        bad |= pe[q] != pe[q];
+    }
+    if (__ballot(bad != 0)) {                          // NaN probabilities: the literal order matters
+        if (lane == 0) chain_literal(val, idx, filled, a, rng, token);
+        return;
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < SMP_Q; q++)
+        for (int32_t l = 0; l < 64 && q * 64 + l < filled; l++) sum = __fadd_rn(sum, readlane_f(pe[q], l));
+    if (sum > 0.0f)
+#pragma unroll
+        for (int q = 0; q < SMP_Q; q++) pe[q] = __fdiv_rn(pe[q], sum);
+    // topk_sort_desc (slm/sampler.c:116-129) is a stable sort by
+    // descending value: rank = #greater + #equal in earlier slots
+#pragma unroll
+    for (int q = 0; q < SMP_Q; q++)
+        if (q * 64 + lane < filled) val[q * 64 + lane] = pe[q];
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < SMP_Q; q++) {
+        const int32_t s_ = q * 64 + lane;
+        if (s_ < filled) {
+            const float v = pe[q];
+            int32_t r = 0;
+            for (int32_t t = 0; t < filled; t++) {
+                const float w = val[t];
+                r += (w > v) | ((w == v) & (t < s_));
+            }
+            sp[r] = v;
+            si[r] = sx[q];
+        }
+    }
+    __syncthreads();
+    float sq[SMP_Q];
+#pragma unroll
+    for (int q = 0; q < SMP_Q; q++) sq[q] = q * 64 + lane < filled ? sp[q * 64 + lane] : 0.0f;
+    // top-p, min-p, renormalized roulette pick (slm/sampler.c:150-178); the
+    // sorted probability j is register j / 64 of lane j % 64
+    int32_t cutoff = filled;
+    if (a.top_p > 0.0f && a.top_p < 1.0f) {
+        float acc = 0.0f;
+        bool done = false;
+#pragma unroll
+        for (int q = 0; q < SMP_Q; q++)
+            for (int32_t l = 0; l < 64 && !done && q * 64 + l < filled; l++) {
+                acc = __fadd_rn(acc, readlane_f(sq[q], l));
+                if (acc >= a.top_p) {
+                    cutoff = q * 64 + l + 1;
+                    done = true;
+                }
+            }
+    }
+    if (a.min_p > 0.0f) {
+        const float thresh = __fmul_rn(a.min_p, readlane_f(sq[0], 0));
+        int32_t j = 1;
+        bool done = false;
+#pragma unroll
+        for (int q = 0; q < SMP_Q; q++)
+            for (int32_t l = q == 0 ? 1 : 0; l < 64 && !done; l++) {
+                if (j < cutoff && readlane_f(sq[q], l) >= thresh) j++;
+                else done = true;
+            }
+        cutoff = j;
+    }
+    float tot = 0.0f;
+#pragma unroll
+    for (int q = 0; q < SMP_Q; q++)
+        for (int32_t l = 0; l < 64 && q * 64 + l < cutoff; l++) tot = __fadd_rn(tot, readlane_f(sq[q], l));
+    uint64_t st[2] = {rng[0], rng[1]};
+    const float u = __fmul_rn(rng_uniform_dev(st), tot);
+    float c = 0.0f;
+    int32_t picked = 0;
+    bool done = false;
+#pragma unroll
+    for (int q = 0; q < SMP_Q; q++)
+        for (int32_t l = 0; l < 64 && !done && q * 64 + l < cutoff; l++) {
+            c = __fadd_rn(c, readlane_f(sq[q], l));
+            if (u <= c) {
+                picked = q * 64 + l;
+                done = true;
+            }
+        }
+    if (lane == 0) {
+        rng[0] = st[0];
+        rng[1] = st[1];
+        *token = si[picked];
+    }
+}
+
+// ---- launcher -------------------------------------------------------------------
+// Block size: the smallest power of two >= 1024 with nblk * k within the
+// LDS list budget (n <= QK_SAMPLE_MAX_N keeps it <= 4096 and nblk <= 256).
+static int32_t sample_block(int64_t n, int32_t k) {
+    int32_t sb = 1024;
+    while (((n + sb - 1) / sb) * k > SMP_LIST_MAX) sb <<= 1;
+    return sb;
+}
+
+size_t sample_scratch_bytes(int64_t n, int32_t k) {
+    const int32_t sb = sample_block(n, k);
+    const int64_t nblk = (n + sb - 1) / sb;
+    return (size_t)nblk * sb * 8                       // event indices and values
+           + (size_t)nblk * (size_t)k * 4              // per-block top-k lists
+           + (size_t)nblk * 4 * 2                      // event counts, NaN flags
+           + (size_t)((n + SMP_BLOCK - 1) / SMP_BLOCK) * sizeof(ArgPart) + 256;   // greedy partials
+}
+
+hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k, float top_p, float min_p,
+                         float penalty, int32_t window, uint64_t *rng, const int32_t *history, int32_t hist_n,
+                         const int32_t *mask, int32_t n_mask, int32_t *token, void *scratch, hipStream_t s) {
+    const int32_t start = (window > 0 && window < hist_n) ? hist_n - window : 0;
+    hipLaunchKernelGGL(k_smp_penalty, dim3(1), dim3(256), 0, s, logits, n, history, start, hist_n, penalty,
+                       n_mask > 0 ? mask[0] : -1, n_mask > 1 ? mask[1] : -1, n_mask);
+    const int32_t sb = sample_block(n, k);
+    const int32_t nblk = (int32_t)((n + sb - 1) / sb);
+    if (nblk > SMP_KMAX || sb > 4096) return hipErrorInvalidValue;   // the caller's n limit keeps both
+    uint8_t *p = static_cast<uint8_t *>(scratch);
+    int32_t *ev_idx = reinterpret_cast<int32_t *>(p);
+    p += (size_t)nblk * sb * 4;
+    float *ev_val = reinterpret_cast<float *>(p);
+    p += (size_t)nblk * sb * 4;
+    float *tops = reinterpret_cast<float *>(p);
+    p += (size_t)nblk * (size_t)k * 4;
+    int32_t *ev_n = reinterpret_cast<int32_t *>(p);
+    p += (size_t)nblk * 4;
+    int32_t *nan_flag = reinterpret_cast<int32_t *>(p);
+    p += (size_t)nblk * 4;
+    ArgPart *part = reinterpret_cast<ArgPart *>((reinterpret_cast<uintptr_t>(p) + 15) & ~(uintptr_t)15);
+    if (temperature <= 0.0f) {
+        const int32_t ablk = (int32_t)((n + SMP_BLOCK - 1) / SMP_BLOCK);
+        hipLaunchKernelGGL(k_smp_argmax_part, dim3(ablk), dim3(256), 0, s, logits, n, part);
+        hipLaunchKernelGGL(k_smp_argmax_final, dim3(1), dim3(256), 0, s, logits, part, ablk, token);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(k_smp_blocks, dim3(nblk), dim3(256), (size_t)sb * 4, s, logits, n, k, sb, tops, nan_flag);
+    const int32_t lcap = ((nblk - 1) * k + 3) & ~3;   // the last block's prefix lists
+    const size_t ev_lds = (size_t)lcap * 4 + (size_t)sb * 8 + (size_t)k * 4;
+    hipLaunchKernelGGL(k_smp_events, dim3(nblk), dim3(256), ev_lds, s, logits, n, k, sb, lcap, tops, ev_idx,
+                       ev_val, ev_n);
+    SmpArgs a{temperature, top_p, min_p, k, sb, nblk};
+    hipLaunchKernelGGL(k_smp_finish, dim3(1), dim3(64), 0, s, logits, n, a, ev_idx, ev_val, ev_n, nan_flag, rng,
+                       token);
+    return hipGetLastError();
+}
+
+}  // namespace qk

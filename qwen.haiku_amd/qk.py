@@ -35,6 +35,12 @@ class QKError(RuntimeError):
         self.rc = rc
 
 
+class Sampler(C.Structure):
+    """struct slm_sampler (qk_sampler in include/qk.h)."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float), ("min_p", C.c_float),
+                ("repetition_penalty", C.c_float), ("repetition_window", C.c_int32)]
+
+
 class GemvDesc(C.Structure):
     _fields_ = [("type", C.c_int32), ("pad_", C.c_int32), ("n", C.c_int64), ("k", C.c_int64),
                 ("w", C.c_void_p), ("xq", C.c_void_p), ("y", C.c_void_p)]
@@ -99,6 +105,7 @@ class QK:
         L.hip_add_rmsnorm_q8k.argtypes = [_vp, _vp, _vp, C.c_float, _i64, _i64, _vp, _vp, _vp, _vp]
         L.hip_silu_f32.argtypes = [_vp, _i64, _vp, _vp]
         L.hip_swiglu_q8k.argtypes = [_vp, _vp, _i64, _i64, _vp, _vp, _vp]
+        L.hip_sample.argtypes = [_vp, _i64, C.POINTER(Sampler), _vp, _vp, C.c_int32, _vp, C.c_int32, _vp, _vp]
         L.hip_qk_register_weight.argtypes = [_vp, C.c_int, _i64, _i64]
         L.hip_qk_unregister_weight.argtypes = [_vp]
         L.hip_qk_device_weight.argtypes = [_vp]
@@ -259,6 +266,26 @@ class QK:
         _need(act, 4 * m * k, "act")
         _need(xq, m * (k // 256) * Q8K_BYTES, "xq")
         self._ck(self.L.hip_swiglu_q8k(_dp(gate), _dp(up), m, k, _dp(act), _dp(xq), self._stream()))
+
+    def sample(self, logits, sp, rng, history=None, hist_n=None, mask=(), token=None):
+        """One sampling step on device logits (modified in place): sp is a
+        dict of slm_sampler fields, rng a device uint64[2] (advanced),
+        history a device int32 tensor whose first hist_n ids count.
+        Returns the device int32 token tensor."""
+        import torch
+        if token is None:
+            token = torch.empty(1, dtype=torch.int32, device=logits.device)
+        if history is not None and hist_n is None:
+            hist_n = history.numel()
+        hist_n = hist_n or 0
+        _need(history, 4 * hist_n, "history")
+        s = Sampler(sp["temperature"], sp["top_k"], sp["top_p"], sp["min_p"], sp["repetition_penalty"],
+                    sp["repetition_window"])
+        m = (C.c_int32 * max(1, len(mask)))(*mask) if len(mask) else None
+        self._ck(self.L.hip_sample(_dp(logits), logits.numel(), C.byref(s), _dp(rng),
+                                   _dp(history) if hist_n else None, hist_n, m, len(mask), _dp(token),
+                                   self._stream()))
+        return token
 
     # -- host seam --------------------------------------------------------------
     def matmul_host(self, wtype, w_np, out_f, k, x_np):
