@@ -469,7 +469,9 @@ def e2e(prompt=512, gen=256, seed=0, timeout=600):
     runs."""
     out = {}
     runs = (("gpu_chain", E2E_GPU, ["--decode", "chain"]), ("gpu_dropin", E2E_GPU, ["--decode", "seam"]),
-            ("cpu_reference", E2E_CPU, []))
+            ("cpu_reference", E2E_CPU, []),
+            ("gpu_chain_sampled", E2E_GPU, ["--decode", "chain", "--sample", "11"]),
+            ("cpu_reference_sampled", E2E_CPU, ["--sample", "11"]))
     keys = ("prefill_tok_s", "decode_tok_s", "prefill_s", "decode_s", "tier", "host_syncs_per_token")
     for name, path, extra in runs:
         if not os.path.exists(path):
@@ -484,19 +486,23 @@ def e2e(prompt=512, gen=256, seed=0, timeout=600):
         out[name]["tokens"] = j["tokens"]
         if name == "gpu_chain":
             out[name]["prefetch_misses"] = j["prefetch_misses"]
-    cpu = out.get("cpu_reference")
-    if isinstance(cpu, dict):
-        cpu["cores"] = 1
-        cpu.pop("host_syncs_per_token", None)
-        for name in ("gpu_chain", "gpu_dropin"):
-            if isinstance(out.get(name), dict):
-                out[name]["tokens_identical"] = out[name]["tokens"] == cpu["tokens"]
-        out["tokens_identical"] = all(out[n]["tokens_identical"] for n in ("gpu_chain", "gpu_dropin")
-                                      if isinstance(out.get(n), dict))
+    pairs = (("gpu_chain", "cpu_reference"), ("gpu_dropin", "cpu_reference"),
+             ("gpu_chain_sampled", "cpu_reference_sampled"))
+    for gname, cname in pairs:
+        g, c = out.get(gname), out.get(cname)
+        if isinstance(g, dict) and isinstance(c, dict):
+            g["tokens_identical"] = g["tokens"] == c["tokens"]
+    for cname in ("cpu_reference", "cpu_reference_sampled"):
+        if isinstance(out.get(cname), dict):
+            out[cname]["cores"] = 1
+            out[cname].pop("host_syncs_per_token", None)
+    out["tokens_identical"] = all(out[g]["tokens_identical"] for g, _ in pairs
+                                  if isinstance(out.get(g), dict) and "tokens_identical" in out[g])
     for v in out.values():
         if isinstance(v, dict):
             v.pop("tokens", None)
-    out["workload"] = f"random Qwen3.5-0.8B-shaped Q4_K_M model, {prompt}-token prompt, {gen} greedy decode steps"
+    out["workload"] = (f"random Qwen3.5-0.8B-shaped Q4_K_M model, {prompt}-token prompt, {gen} decode steps: "
+                       f"greedy, and *_sampled with slm_sampler_defaults and rng seed 11")
     return out
 
 

@@ -57,6 +57,11 @@ typedef struct {
     int32_t *am_host;
     qk_dec_proj proj[QK_DEC_MAX_PROJ];
     long long syncs;
+    /* sampling (slm_generate_raw, slm/slm.c:255-325): the rng's two words
+       and the repetition history (prompt, then every pick), on the device */
+    uint64_t *rng;
+    int32_t *hist;
+    int32_t hist_n, hist_cap;
 } qk_dec;
 
 static void qk_dec_ck(hipError_t e, const char *what) {
@@ -162,6 +167,18 @@ static void qk_dec_init(qk_dec *D, const struct slm_model *m) {
     qk_dec_weight(&m->W.output);
 }
 
+/* Sampled decoding from the reference's rng state and a history holding
+ * the prompt (slm/slm.c:251-263); room for cap ids in all. */
+static void qk_dec_sampling(qk_dec *D, const struct rng *r, const int32_t *prompt, int32_t n, int32_t cap) {
+    uint64_t st[2] = {r->s0, r->s1};
+    D->rng = qk_dec_alloc(sizeof(st));
+    D->hist = qk_dec_alloc((size_t)cap * sizeof(int32_t));
+    qk_dec_ck(hipMemcpy(D->rng, st, sizeof(st), hipMemcpyHostToDevice), "upload rng");
+    qk_dec_ck(hipMemcpy(D->hist, prompt, (size_t)n * sizeof(int32_t), hipMemcpyHostToDevice), "upload history");
+    D->hist_n = n;
+    D->hist_cap = cap;
+}
+
 /* One grouped launch of n GEMVs over the normalized row: from its Q8_K
  * copy when every weight is a K-quant, else from the fp32 row (each
  * workgroup quantizes it for its own weight type). */
@@ -201,9 +218,13 @@ static void qk_dec_sync(qk_dec *D) {
     D->syncs++;
 }
 
-/* slm_forward_step + sample_argmax for token tok at position pos; the
- * logits are copied into logits_host when it is not NULL. */
-static int32_t qk_decode_step(struct slm_ctx *c, qk_dec *D, int32_t tok, int32_t pos, float *logits_host) {
+/* slm_forward_step for token tok at position pos, then the pick: with
+ * sp NULL sample_argmax fused into the LM head, else sample_with
+ * (hip_sample) on the device logits with the device rng and history, the
+ * pick appended to the history. The logits as the forward pass left them
+ * are copied into logits_host when it is not NULL. */
+static int32_t qk_decode_step(struct slm_ctx *c, qk_dec *D, int32_t tok, int32_t pos, float *logits_host,
+                              const struct slm_sampler *sp) {
     struct arena *a = c->arena;
     arena_reset(a);
     const struct slm_model *m = c->model;
@@ -275,13 +296,26 @@ static int32_t qk_decode_step(struct slm_ctx *c, qk_dec *D, int32_t tok, int32_t
     }
     /* h += ffn_out; output_norm; LM head + greedy pick */
     qk_dec_lib(hip_add_rmsnorm_q8k(D->h, delta, D->out_norm, D->eps, 1, H, D->h, NULL, D->xq, s), "output_norm");
+    const int sampled = sp != NULL;
     qk_dec_lib(hip_lmhead_q6k_argmax_topk(hip_qk_device_weight(m->W.output.data), D->vocab, H, D->xq, 0,
-                                          logits_host ? D->logits : NULL, D->am, NULL, NULL, s),
+                                          (logits_host || sampled) ? D->logits : NULL, D->am, NULL, NULL, s),
                "LM head");
-    qk_dec_ck(hipMemcpyAsync(D->am_host, D->am, sizeof(int32_t), hipMemcpyDeviceToHost, s), "token to host");
     if (logits_host)
         qk_dec_ck(hipMemcpyAsync(logits_host, D->logits, (size_t)D->vocab * 4, hipMemcpyDeviceToHost, s),
                   "logits to host");
+    int32_t *pick = D->am;
+    if (sampled) {
+        if (D->hist_n >= D->hist_cap) {
+            fprintf(stderr, "qk_decode: history full\n");
+            abort();
+        }
+        qk_sampler q = {sp->temperature, sp->top_k, sp->top_p, sp->min_p, sp->repetition_penalty,
+                        sp->repetition_window};
+        pick = D->hist + D->hist_n;
+        qk_dec_lib(hip_sample(D->logits, D->vocab, &q, D->rng, D->hist, D->hist_n, NULL, 0, pick, s), "sample");
+        D->hist_n++;
+    }
+    qk_dec_ck(hipMemcpyAsync(D->am_host, pick, sizeof(int32_t), hipMemcpyDeviceToHost, s), "token to host");
     qk_dec_sync(D);
     return *D->am_host;
 }

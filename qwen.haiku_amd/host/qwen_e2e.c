@@ -47,8 +47,16 @@
  * reference's slm_forward_step unchanged, every matmul a round trip
  * through the seam. Both report their host synchronisations per token.
  *
+ * --sample SEED (non-zero) replaces the greedy pick with the reference's
+ * default sampler chain (slm_sampler_defaults, slm/sampler.c:22-31):
+ * rng_seed(SEED) and a history holding the prompt, as slm_generate_raw
+ * does (slm/slm.c:251-325). The CPU build and --decode seam call the
+ * reference's sample_with on the host; --decode chain calls hip_sample on
+ * the device logits.
+ *
  * Usage: qwen_e2e [--prompt P] [--gen G] [--seed S] [--layers L]
  *                 [--write-gguf PATH | --gguf PATH] [--decode chain|seam]
+ *                 [--sample SEED]
  */
 #if defined(QK_E2E_GPU)
 #include "qk_seam.c"
@@ -258,7 +266,7 @@ static double e2e_now(void) {
 
 int main(int argc, char **argv) {
     int32_t n_prompt = 512, n_gen = 256, n_layers = 24;
-    uint64_t seed = 0;
+    uint64_t seed = 0, sample_seed = 0;
     const char *write_path = NULL, *load_path = NULL, *decode_mode = "chain";
     for (int i = 1; i + 1 < argc; i += 2) {
         if (strcmp(argv[i], "--prompt") == 0) n_prompt = atoi(argv[i + 1]);
@@ -268,12 +276,13 @@ int main(int argc, char **argv) {
         else if (strcmp(argv[i], "--write-gguf") == 0) write_path = argv[i + 1];
         else if (strcmp(argv[i], "--gguf") == 0) load_path = argv[i + 1];
         else if (strcmp(argv[i], "--decode") == 0) decode_mode = argv[i + 1];
+        else if (strcmp(argv[i], "--sample") == 0) sample_seed = (uint64_t)strtoull(argv[i + 1], NULL, 10);
     }
     const int chain = strcmp(decode_mode, "chain") == 0;
     if (n_prompt < 2 || n_gen < 1 || n_layers < 1 || (write_path && load_path) ||
         (!chain && strcmp(decode_mode, "seam") != 0)) {
         fprintf(stderr, "usage: %s [--prompt P>=2] [--gen G>=1] [--seed S] [--layers L>=1] "
-                        "[--write-gguf PATH | --gguf PATH] [--decode chain|seam]\n", argv[0]);
+                        "[--write-gguf PATH | --gguf PATH] [--decode chain|seam] [--sample SEED]\n", argv[0]);
         return 2;
     }
     simd_init();
@@ -413,9 +422,19 @@ int main(int argc, char **argv) {
     const int64_t nvocab = cfg.vocab_size;
     float *lbuf = (float *)oom(malloc((size_t)nvocab * sizeof(float)));
     long long syncs0 = 0, hits0 = 0, miss0 = 0;
+    /* sampling state (slm/slm.c:251-263) */
+    struct slm_sampler sp = slm_sampler_defaults();
+    const struct slm_sampler *spp = sample_seed ? &sp : NULL;
+    int32_t *history = (int32_t *)oom(calloc((size_t)(n_prompt + n_gen + 1), sizeof(int32_t)));
+    int32_t hist_n = 0;
+    for (int32_t i = 0; i < n_prompt; i++) history[hist_n++] = prompt[i];
+    if (sample_seed) rng_seed(&c->rng, sample_seed);
 #if defined(QK_E2E_GPU)
     qk_dec D;
-    if (chain) qk_dec_init(&D, m);
+    if (chain) {
+        qk_dec_init(&D, m);
+        if (sample_seed) qk_dec_sampling(&D, &c->rng, history, hist_n, n_prompt + n_gen + 1);
+    }
     syncs0 = qk_seam_gpu_calls;
     hits0 = qk_seam_pf_hits;
     miss0 = qk_seam_pf_misses;
@@ -429,15 +448,20 @@ int main(int argc, char **argv) {
         const float *lv = NULL;
 #if defined(QK_E2E_GPU)
         if (chain) {
-            next = qk_decode_step(c, &D, last, pos, stats ? lbuf : NULL);
+            next = qk_decode_step(c, &D, last, pos, stats ? lbuf : NULL, spp);
             lv = lbuf;
         } else
 #endif
         {
             logits = slm_forward_step(c, last, pos);
-            next = sample_argmax(logits);
             lv = logits->data;
+            if (spp && stats) {            /* sample_with penalizes in place: keep the raw logits */
+                memcpy(lbuf, lv, (size_t)nvocab * sizeof(float));
+                lv = lbuf;
+            }
+            next = spp ? sample_with(logits, spp, &c->rng, history, hist_n) : sample_argmax(logits);
         }
+        history[hist_n++] = next;
         if (stats) {
             lmin = lmax = lv[0];
             lsum = lsq = 0;
@@ -476,7 +500,7 @@ int main(int argc, char **argv) {
     const double nv = (double)cfg.vocab_size;
     printf("{\"mode\": \"%s\", \"source\": \"%s\", \"tier\": \"%s\", \"layers\": %d, \"prompt\": %d, \"gen\": %d, \"seed\": %llu, "
            "\"prefill_s\": %.6f, \"decode_s\": %.6f, \"prefill_tok_s\": %.3f, \"decode_tok_s\": %.3f, "
-           "\"decode_path\": \"%s\", \"host_syncs_per_token\": %.2f, \"prefetch_hits\": %.0f, \"prefetch_misses\": %.0f, "
+           "\"decode_path\": \"%s\", \"sampler\": \"%s\", \"host_syncs_per_token\": %.2f, \"prefetch_hits\": %.0f, \"prefetch_misses\": %.0f, "
            "\"distinct_tokens\": %d, \"nonfinite_logits\": %lld, \"last_logits\": {\"min\": %.6g, \"max\": %.6g, "
            "\"mean\": %.6g, \"std\": %.6g}, \"tokens\": [",
 #if defined(QK_E2E_GPU)
@@ -491,7 +515,7 @@ int main(int argc, char **argv) {
 #else
            "cpu",
 #endif
-           syncs_per_tok, pf_hits, pf_misses, distinct, (long long)nonfinite, lmin, lmax, lsum / nv,
+           spp ? "slm_sampler_defaults" : "greedy", syncs_per_tok, pf_hits, pf_misses, distinct, (long long)nonfinite, lmin, lmax, lsum / nv,
            sqrt(lsq / nv - (lsum / nv) * (lsum / nv)));
     for (int32_t i = 0; i < n_gen; i++) printf("%s%d", i ? ", " : "", toks[i]);
     printf("]}\n");

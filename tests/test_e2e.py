@@ -70,6 +70,23 @@ def test_e2e_greedy_tokens_identical(prompt, gen):
             assert gpu["host_syncs_per_token"] == 2 * layers + 1
 
 
+@pytest.mark.gpu
+def test_e2e_sampled_tokens_identical():
+    """The reference's default sampler chain (T 0.7, top-k 40, top-p 0.9,
+    min-p 0.05, repetition penalty 1.25 over 64) with a fixed rng seed:
+    the chain run samples on the device (hip_sample), the seam run and the
+    CPU reference with sample_with on the host; the token streams must be
+    identical."""
+    cpu = run(E2E_CPU, 240, prompt=64, gen=48, seed=0, sample=11)
+    assert cpu["sampler"] == "slm_sampler_defaults" and cpu["distinct_tokens"] >= 12
+    for mode in ("seam", "chain"):
+        gpu = run(E2E_GPU, 240, prompt=64, gen=48, seed=0, sample=11, decode=mode)
+        print(f"[e2e] sampled gpu-{mode} decode {gpu['decode_tok_s']:.1f} tok/s; cpu {cpu['decode_tok_s']:.1f}",
+              flush=True)
+        assert gpu["tokens"] == cpu["tokens"], mode
+        assert gpu["last_logits"] == cpu["last_logits"], mode
+
+
 # ---- GGUF round trip ------------------------------------------------------------
 # qwen_e2e --write-gguf writes the random model as GGUF v3 (host/gguf_write.c);
 # --gguf loads a file through the reference's own slm_model_load. The token
