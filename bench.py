@@ -35,6 +35,8 @@ import subprocess
 import sys
 import time
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 
 CONFIG1 = [(12, 3584, 1024), (12, 3584, 1024), (14, 1024, 3584), (13, 2048, 1024),
@@ -49,7 +51,9 @@ WARM_S = 0.2                      # minimum warm-up time
 # scaled by its reading for a known-size copy / fill (FETCH x2.000,
 # WRITE x1.000); the runs are recorded in profiles/k_gemv_decode_set_lmhead.md.
 # None when the kernel has changed since the last counter run.
-CONFIG1_TRAFFIC_BYTES = 11_997_184 + 55_296
+# config-1 HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
+# each scaled by its reading for a known-size copy in the same run
+CONFIG1_TRAFFIC_BYTES = 12_064_266
 E2E_GPU = os.path.join(ROOT, "qwen.haiku_amd", "host", "_build", "qwen_e2e_gpu")
 E2E_CPU = os.path.join(ROOT, "oracle", "_ref", "qwen_e2e_cpu")
 
@@ -99,6 +103,7 @@ class GraphTimer:
 
     def __init__(self, torch):
         self.torch = torch
+        self.warm_s = WARM_S
 
     def time(self, launch, R, steps, warmup):
         torch = self.torch
@@ -115,7 +120,7 @@ class GraphTimer:
                 launch(i, sp)
         with torch.cuda.stream(s):
             n, t0 = 0, time.perf_counter()
-            while n < warmup or time.perf_counter() - t0 < WARM_S:
+            while n < warmup or time.perf_counter() - t0 < self.warm_s:
                 g.replay()
                 n += 1
                 if n % 16 == 0:
@@ -334,6 +339,65 @@ def config3_extras(torch, qk, synth, lib, steps, warmup, peak_tops=None):
     return extra
 
 
+# ---- decode-chain links and the sampler -----------------------------------------
+
+CHAIN_CASES = ((1, 1024), (512, 1024))                 # add + RMSNorm -> Q8_K: decode row, prefill batch
+SWIGLU_CASES = ((1, 3584), (512, 3584))
+SAMPLERS = {"default_k40": dict(temperature=0.7, top_k=40, top_p=0.9, min_p=0.05, repetition_penalty=1.25,
+                                repetition_window=64),
+            "k256": dict(temperature=1.0, top_k=0, top_p=0.95, min_p=0.0, repetition_penalty=1.0,
+                         repetition_window=0),
+            "greedy_rep": dict(temperature=0.0, top_k=40, top_p=0.9, min_p=0.05, repetition_penalty=1.25,
+                               repetition_window=64)}
+
+
+def chain_extras(torch, qk, lib, steps, warmup):
+    """Latency of hip_add_rmsnorm_q8k and hip_swiglu_q8k (one graph replay
+    of 64 launches per step). The norm's sequential double sum of squares
+    (slm/tensor.c:357-360) is one dependent add per element on one lane."""
+    out = {}
+    gt = GraphTimer(torch)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for m, k in CHAIN_CASES:
+        h = torch.randn(m, k, device="cuda", generator=g)
+        d = torch.randn(m, k, device="cuda", generator=g)
+        w = torch.ones(k, device="cuda")
+        xq = torch.empty(m, (k // 256) * qk.Q8K_BYTES, dtype=torch.uint8, device="cuda")
+        args = (qk._dp(h), qk._dp(d), qk._dp(w), C.c_float(1e-6), m, k, None, None, qk._dp(xq))
+        secs = gt.time(lambda i, st: lib.L.hip_add_rmsnorm_q8k(*args, st), 64, steps, warmup)
+        out[f"add_rmsnorm_q8k_m{m}_k{k}"] = {"us_per_launch": round(secs / (64 * steps) * 1e6, 3)}
+    for m, k in SWIGLU_CASES:
+        a = torch.randn(m, k, device="cuda", generator=g)
+        b = torch.randn(m, k, device="cuda", generator=g)
+        xq = torch.empty(m, (k // 256) * qk.Q8K_BYTES, dtype=torch.uint8, device="cuda")
+        args = (qk._dp(a), qk._dp(b), m, k, None, qk._dp(xq))
+        secs = gt.time(lambda i, st: lib.L.hip_swiglu_q8k(*args, st), 64, steps, warmup)
+        per = 8 * m * k + m * (k // 256) * qk.Q8K_BYTES
+        us = secs / (64 * steps) * 1e6
+        out[f"swiglu_q8k_m{m}_k{k}"] = {"us_per_launch": round(us, 3), "GB/s": round(per / us / 1e3, 1)}
+    return out
+
+
+def sampler_extras(torch, qk, lib, steps, warmup, vocab=248320):
+    """hip_sample at the model's vocabulary: the default chain (top-k 40),
+    top-k 256, and greedy with the repetition penalty (16 calls per replay;
+    each call penalizes the same logits again, as a decode loop would)."""
+    out = {}
+    gt = GraphTimer(torch)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    hist = torch.randint(0, vocab, (64,), dtype=torch.int32, device="cuda", generator=g)
+    for name, sp in SAMPLERS.items():
+        lg = torch.randn(vocab, device="cuda", generator=g) * 2.5
+        st_ = torch.full((2,), 12345, dtype=torch.int64, device="cuda")
+        tok = torch.empty(1, dtype=torch.int32, device="cuda")
+        s = qk.Sampler(sp["temperature"], sp["top_k"], sp["top_p"], sp["min_p"], sp["repetition_penalty"],
+                       sp["repetition_window"])
+        args = (qk._dp(lg), vocab, C.byref(s), qk._dp(st_), qk._dp(hist), 64, None, 0, qk._dp(tok))
+        secs = gt.time(lambda i, stream: lib.L.hip_sample(*args, stream), 16, steps, warmup)
+        out[f"sample_vocab{vocab}_{name}"] = {"us_per_call": round(secs / (16 * steps) * 1e6, 1)}
+    return out
+
+
 # ---- CPU reference ------------------------------------------------------------------
 
 def host_description():
@@ -456,6 +520,19 @@ def cpu_extras(synth, seconds=2.0):
             out[f"config3_{'q4k' if t == 12 else 'q6k'}_m{m3}_{th}core"] = {
                 "TOPS": round(r / 1e9 / 1e3, 4), "sample": f"{reps} x {ms} tokens of {m3}, {dt:.1f} s"}
     stop()
+    # the sampler chain (sample_with, slm/sampler.c:134) at the model's
+    # vocabulary, one core, as slm_generate_raw runs it
+    oracle = _load("oracle/oracle.py", "qk_oracle_py")
+    smp = oracle.Ref() if oracle.Ref.available() else oracle.Oracle()
+    logits = synth.activations(1, 248320, seed=3).ravel() * np.float32(2.5)
+    hist = np.arange(64, dtype=np.int32) * 977
+    for name in ("default_k40", "k256"):
+        st_, calls, t0 = smp.rng_seed(11), 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds / 2:
+            _, _, st_ = smp.sample(logits, SAMPLERS[name], st_, hist)
+            calls += 1
+        dt = time.perf_counter() - t0
+        out[f"sample_vocab248320_{name}_1core"] = {"us_per_call": round(dt / calls * 1e6, 1), "calls": calls}
     return out
 
 
@@ -519,6 +596,7 @@ def mfma_peak():
 
 
 def main():
+    global WARM_S
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
@@ -527,12 +605,16 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
-    ap.add_argument("--only", choices=["all", "config1", "config3", "lmhead", "q4k_stream"], default="all",
+    ap.add_argument("--warm-seconds", type=float, default=WARM_S,
+                    help="minimum warm-up replay time per case (short values keep profiler traces small)")
+    ap.add_argument("--only", choices=["all", "config1", "config3", "lmhead", "q4k_stream", "chain", "sampler"],
+                    default="all",
                     help="time one case only (profiling aids)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run 8 plain device copies of MIB MiB each: the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     a = ap.parse_args()
+    WARM_S = a.warm_seconds
     if a.gpus != 1:
         print(f"bench.py measures one GPU: the quantized GEMV path runs on a single MI355X "
               f"(--gpus {a.gpus} is not supported)", file=sys.stderr)
@@ -560,6 +642,13 @@ def main():
         p2, c2, R2, s2 = bench_config2(torch, qk, synth, lib, a.steps, a.warmup)
         g, us = rate(p2, R2, a.steps, s2)
         print(json.dumps({"metric": "config2 LM head GB/s", "value": round(g, 2), "us_per_call": round(us, 3)}))
+        return
+    if a.only == "chain":
+        print(json.dumps({"metric": "decode-chain link latency", "extra": chain_extras(torch, qk, lib, a.steps,
+                                                                                         a.warmup)}))
+        return
+    if a.only == "sampler":
+        print(json.dumps({"metric": "sampler latency", "extra": sampler_extras(torch, qk, lib, a.steps, a.warmup)}))
         return
     if a.only == "q4k_stream":
         p, c, R, s = bench_gemv(torch, qk, synth, lib, a.steps, a.warmup, 12, 248320, 1024, 30.0)
@@ -630,6 +719,9 @@ def main():
             extra["mfma_int8_peak_measured"] = peak
         peak_tops = peak["mfma_i32_32x32x32_i8_tops"] if peak else None
         extra.update(config3_extras(torch, qk, synth, lib, max(10, a.steps // 10), 3, peak_tops))
+        progress("decode-chain links and sampler")
+        extra["chain_links"] = chain_extras(torch, qk, lib, max(10, a.steps // 10), 3)
+        extra["sampler"] = sampler_extras(torch, qk, lib, max(5, a.steps // 20), 2)
         if not a.no_e2e:
             progress("config 4 end to end")
             extra["config4_e2e"] = e2e()
