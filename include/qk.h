@@ -325,6 +325,24 @@ int hip_sample(float *logits, int64_t n, const qk_sampler *sp, uint64_t *rng,
                const int32_t *history, int32_t hist_n, const int32_t *mask,
                int32_t n_mask, int32_t *token, void *stream);
 
+/* ---- device layer: chunked Gated DeltaNet prefill ------------------ */
+
+/* The chunk loop of slm_forward_ssm_batch (slm/qwen.c:772-807) over one
+ * layer: n_tok tokens in chunks of 64, each chunk run through
+ * chunked_ssm_step_f32 (slm/chunked.c:287-521) for every head, the state
+ * of each head carried from chunk to chunk. q, k: [n_tok][n_heads][k_hd]
+ * (q L2-normalized and scaled, k L2-normalized); v: [n_tok][n_heads][v_hd];
+ * g_log, beta: [n_tok][n_heads]; state: [n_heads][k_hd][v_hd], updated in
+ * place; out: [n_tok][n_heads][v_hd]. Bit-exact against the reference's
+ * x86 build (sequential fp32 sums, expf of glibc's FMA build). Head dims
+ * at most QK_DELTANET_MAX_HD. Device pointers; scratch per stream, as for
+ * the LM head. */
+#define QK_DELTANET_MAX_HD 128
+int hip_deltanet_chunked(const float *q, const float *k, const float *v,
+                         const float *g_log, const float *beta, int64_t n_tok,
+                         int n_heads, int k_hd, int v_hd, float *state,
+                         float *out, void *stream);
+
 /* ---- host seam ------------------------------------------------------ */
 
 /* Upload the n x k weight matrix at host address `host_w` (GGUF type
@@ -354,6 +372,14 @@ const void *hip_qk_device_weight(const void *host_w);
 int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f,
                        int64_t k, const float *x, int64_t n_tok,
                        float *out);
+/* chunked_ssm_step_f32 (slm/chunked.c:287) for one head and one chunk of
+ * n <= 64 tokens, host buffers in and out, synchronous: the body the host
+ * seam gives the reference's chunk step (its scratch arguments are not
+ * needed). q, k: [n][k_hd]; v, out: [n][v_hd]; g_log, beta: [n];
+ * state: [k_hd][v_hd], updated in place. */
+int hip_qk_deltanet_host(int n, int k_hd, int v_hd, const float *q,
+                         const float *k, const float *v, const float *g_log,
+                         const float *beta, float *state, float *out);
 /* LM head: matmul_dispatch(&W.output, h) (slm/qwen.c:976) followed by
  * sample_argmax (slm/model.c:401). logits (n floats) may be NULL when
  * only the token is needed; topk may be 0. Host pointers. */

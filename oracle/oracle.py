@@ -94,6 +94,10 @@ class Oracle:
         L.qko_silu.restype = None
         L.qko_swiglu.argtypes = [_i64, _vp, _vp, _vp]
         L.qko_swiglu.restype = None
+        L.qko_chunked_step.argtypes = [C.c_int, C.c_int, C.c_int] + [_vp] * 7
+        L.qko_chunked_step.restype = None
+        L.qko_deltanet_chunked.argtypes = [_i64, C.c_int, C.c_int, C.c_int] + [_vp] * 7
+        L.qko_deltanet_chunked.restype = None
         L.qko_rng_seed.argtypes = [C.c_uint64, _vp]
         L.qko_rng_seed.restype = None
         L.qko_sample.argtypes = [_vp, _i64, C.c_float, C.c_int32, C.c_float, C.c_float, C.c_float, C.c_int32, _vp, _vp, C.c_int32, _vp, C.c_int32]
@@ -238,6 +242,36 @@ class Oracle:
     def _rng_seed(self, *a):
         self.L.qko_rng_seed(*a)
 
+    def _chunked_step(self, *a):
+        self.L.qko_chunked_step(*a)
+
+    def deltanet_chunked(self, q, k, v, g, beta, state):
+        """The chunk loop of a layer: q, k [n, H, kd]; v [n, H, vd]; g, beta
+        [n, H]; state [H, kd, vd]. Returns (out [n, H, vd], new state)."""
+        q = np.ascontiguousarray(q, np.float32)
+        n, H, kd = q.shape
+        vd = v.shape[2]
+        st = np.array(state, np.float32, copy=True)
+        out = np.zeros((n, H, vd), np.float32)
+        self.L.qko_deltanet_chunked(n, H, kd, vd, _ptr(q), _ptr(np.ascontiguousarray(k, np.float32)),
+                                    _ptr(np.ascontiguousarray(v, np.float32)),
+                                    _ptr(np.ascontiguousarray(g, np.float32)),
+                                    _ptr(np.ascontiguousarray(beta, np.float32)), _ptr(st), _ptr(out))
+        return out, st
+
+    # -- chunked Gated DeltaNet (shared by Oracle and Ref) ------------------
+    def chunked_step(self, q, k, v, g, beta, state):
+        """One chunk of one head: returns (out, new state)."""
+        q = np.ascontiguousarray(q, np.float32)
+        n, kd = q.shape
+        vd = v.shape[1]
+        st = np.array(state, np.float32, copy=True)
+        out = np.zeros((n, vd), np.float32)
+        self._chunked_step(n, kd, vd, _ptr(q), _ptr(np.ascontiguousarray(k, np.float32)),
+                           _ptr(np.ascontiguousarray(v, np.float32)), _ptr(np.ascontiguousarray(g, np.float32)),
+                           _ptr(np.ascontiguousarray(beta, np.float32)), _ptr(st), _ptr(out))
+        return out, st
+
     def _sample(self, *a):
         return self.L.qko_sample(*a)
 
@@ -310,6 +344,8 @@ class Ref:
         L.ref_silu.restype = None
         L.ref_swiglu.argtypes = [_i64, _vp, _vp, _vp]
         L.ref_swiglu.restype = C.c_int
+        L.ref_chunked_step.argtypes = [C.c_int, C.c_int, C.c_int] + [_vp] * 7
+        L.ref_chunked_step.restype = None
         L.ref_rng_seed.argtypes = [C.c_uint64, _vp]
         L.ref_rng_seed.restype = None
         L.ref_sample.argtypes = [_vp, _i64, C.c_float, C.c_int32, C.c_float, C.c_float, C.c_float, C.c_int32, _vp, _vp, C.c_int32, _vp, C.c_int32]
@@ -458,3 +494,19 @@ class Ref:
                            C.c_float(sp["min_p"]), C.c_float(sp["repetition_penalty"]), sp["repetition_window"],
                            _ptr(st), _ptr(h) if h.size else None, h.size, _ptr(mk) if mk.size else None, mk.size)
         return tok, lg, st
+
+    def _chunked_step(self, *a):
+        self.L.ref_chunked_step(*a)
+
+    # -- chunked Gated DeltaNet (shared by Oracle and Ref) ------------------
+    def chunked_step(self, q, k, v, g, beta, state):
+        """One chunk of one head: returns (out, new state)."""
+        q = np.ascontiguousarray(q, np.float32)
+        n, kd = q.shape
+        vd = v.shape[1]
+        st = np.array(state, np.float32, copy=True)
+        out = np.zeros((n, vd), np.float32)
+        self._chunked_step(n, kd, vd, _ptr(q), _ptr(np.ascontiguousarray(k, np.float32)),
+                           _ptr(np.ascontiguousarray(v, np.float32)), _ptr(np.ascontiguousarray(g, np.float32)),
+                           _ptr(np.ascontiguousarray(beta, np.float32)), _ptr(st), _ptr(out))
+        return out, st

@@ -660,3 +660,135 @@ int32_t qko_sample(float *logits, int64_t n, float temperature, int32_t top_k, f
     }
     return idx[picked];
 }
+
+/* ---- chunked Gated DeltaNet ------------------------------------------- */
+
+/* One chunk of n <= 64 tokens of one head (chunked_ssm_step_f32,
+ * slm/chunked.c:287-521, on an x86 host: every dot and axpy is a
+ * sequential mul-then-add, no FMA). q, k: [n][k_hd]; v: [n][v_hd];
+ * g, beta: [n]; state [k_hd][v_hd] updated in place; out [n][v_hd]. */
+void qko_chunked_step(int n, int kd, int vd, const float *q, const float *k, const float *v, const float *g,
+                      const float *beta, float *state, float *out) {
+    float gcs[64], gexp[64], dm[64 * 64], kb[64 * 128], vb[64 * 128], kkd[64 * 64], lhs[64 * 64];
+    float attn[64 * 64], x[64 * 64], veff[64 * 128], kbg[64 * 128], kcd[64 * 128], akq[64 * 64];
+    float qg[64 * 128], ainter[64 * 128], vnew[64 * 128];
+    float run = 0.0f;
+    for (int t = 0; t < n; t++) { run += g[t]; gcs[t] = run; }
+    for (int t = 0; t < n; t++) gexp[t] = expf(gcs[t]);
+    for (int i = 0; i < n; i++)
+        for (int j = 0; j < n; j++) dm[i * n + j] = i > j ? expf(gcs[i] - gcs[j]) : 0.0f;
+    for (int t = 0; t < n; t++) {
+        for (int d = 0; d < kd; d++) kb[t * kd + d] = k[t * kd + d] * beta[t];
+        for (int e = 0; e < vd; e++) vb[t * vd + e] = v[t * vd + e] * beta[t];
+    }
+    /* strictly lower: (K_j . Kbeta_i) * decay; lhs = I + that */
+    for (int i = 0; i < n; i++)
+        for (int j = 0; j < n; j++) {
+            float val = 0.0f;
+            if (i > j) {
+                float s = 0.0f;
+                for (int d = 0; d < kd; d++) s += k[j * kd + d] * kb[i * kd + d];
+                val = s * dm[i * n + j];
+            }
+            kkd[i * n + j] = val;
+            lhs[i * n + j] = i > j ? val : (i == j ? 1.0f : 0.0f);
+        }
+    for (int i = 0; i < n * n; i++) attn[i] = -kkd[i];
+    /* forward substitution, column by column (ggml's solve_tri order) */
+    for (int j = 0; j < n; j++)
+        for (int i = 0; i < n; i++) {
+            float s = 0.0f;
+            for (int t = 0; t < i; t++) s += lhs[i * n + t] * x[t * n + j];
+            x[i * n + j] = (attn[i * n + j] - s) / lhs[i * n + i];
+        }
+    for (int i = 0; i < n; i++)
+        for (int j = 0; j < n; j++) attn[i * n + j] = j < i ? x[i * n + j] : (j == i ? 1.0f : 0.0f);
+    /* attn @ v_beta, attn @ (k_beta * gexp): nonzero coefficients, j ascending */
+    for (int t = 0; t < n; t++) for (int d = 0; d < kd; d++) kbg[t * kd + d] = kb[t * kd + d] * gexp[t];
+    for (int i = 0; i < n; i++) {
+        for (int e = 0; e < vd; e++) veff[i * vd + e] = 0.0f;
+        for (int d = 0; d < kd; d++) kcd[i * kd + d] = 0.0f;
+        for (int j = 0; j <= i; j++) {
+            const float a = attn[i * n + j];
+            if (a == 0.0f) continue;
+            for (int e = 0; e < vd; e++) veff[i * vd + e] += a * vb[j * vd + e];
+        }
+        for (int j = 0; j <= i; j++) {
+            const float a = attn[i * n + j];
+            if (a == 0.0f) continue;
+            for (int d = 0; d < kd; d++) kcd[i * kd + d] += a * kbg[j * kd + d];
+        }
+    }
+    /* intra-chunk attention (K_j . Q_i) * decay, decay 1 on the diagonal */
+    for (int i = 0; i < n; i++)
+        for (int j = 0; j < n; j++) {
+            float val = 0.0f;
+            if (i >= j) {
+                float s = 0.0f;
+                for (int d = 0; d < kd; d++) s += k[j * kd + d] * q[i * kd + d];
+                val = s * (i == j ? 1.0f : dm[i * n + j]);
+            }
+            akq[i * n + j] = val;
+        }
+    for (int t = 0; t < n; t++) for (int d = 0; d < kd; d++) qg[t * kd + d] = gexp[t] * q[t * kd + d];
+    /* the carried state: state^T (q*gexp), state^T k_cumdecay; zero coefficients skipped */
+    for (int t = 0; t < n; t++) {
+        float vp[128];
+        for (int e = 0; e < vd; e++) { ainter[t * vd + e] = 0.0f; vp[e] = 0.0f; }
+        for (int d = 0; d < kd; d++) {
+            const float c = qg[t * kd + d];
+            if (c == 0.0f) continue;
+            for (int e = 0; e < vd; e++) ainter[t * vd + e] += c * state[d * vd + e];
+        }
+        for (int d = 0; d < kd; d++) {
+            const float c = kcd[t * kd + d];
+            if (c == 0.0f) continue;
+            for (int e = 0; e < vd; e++) vp[e] += c * state[d * vd + e];
+        }
+        for (int e = 0; e < vd; e++) vnew[t * vd + e] = veff[t * vd + e] - vp[e];
+    }
+    for (int t = 0; t < n; t++)
+        for (int e = 0; e < vd; e++) {
+            float s = 0.0f;
+            for (int u = 0; u < n; u++) s += akq[t * n + u] * vnew[u * vd + e];
+            out[t * vd + e] = ainter[t * vd + e] + s;
+        }
+    /* state := state * exp(g_last) + (K * exp(g_last - gcs))^T v_new */
+    const float glast = gcs[n - 1], gle = expf(glast);
+    float diff[64];
+    for (int t = 0; t < n; t++) diff[t] = expf(glast - gcs[t]);
+    for (int d = 0; d < kd; d++)
+        for (int e = 0; e < vd; e++) {
+            float s = 0.0f;
+            for (int t = 0; t < n; t++) {
+                const float kg = k[t * kd + d] * diff[t];
+                s += kg * vnew[t * vd + e];
+            }
+            const float decayed = state[d * vd + e] * gle;
+            state[d * vd + e] = decayed + s;
+        }
+}
+
+/* slm_forward_ssm_batch's chunk loop (slm/qwen.c:772-807): n_tok tokens
+ * in chunks of 64, every head per chunk, the state of each head carried.
+ * q, k: [n_tok][n_heads][kd]; v, out: [n_tok][n_heads][vd]; g, beta:
+ * [n_tok][n_heads]; state: [n_heads][kd][vd]. */
+void qko_deltanet_chunked(int64_t n_tok, int n_heads, int kd, int vd, const float *q, const float *k,
+                          const float *v, const float *g, const float *beta, float *state, float *out) {
+    float qc[64 * 128], kc[64 * 128], vc[64 * 128], gc[64], bc[64], oc[64 * 128];
+    for (int64_t c0 = 0; c0 < n_tok; c0 += 64) {
+        const int n = (int)(n_tok - c0 < 64 ? n_tok - c0 : 64);
+        for (int h = 0; h < n_heads; h++) {
+            for (int t = 0; t < n; t++) {
+                const int64_t tg = c0 + t;
+                memcpy(qc + t * kd, q + (tg * n_heads + h) * kd, (size_t)kd * 4);
+                memcpy(kc + t * kd, k + (tg * n_heads + h) * kd, (size_t)kd * 4);
+                memcpy(vc + t * vd, v + (tg * n_heads + h) * vd, (size_t)vd * 4);
+                gc[t] = g[tg * n_heads + h];
+                bc[t] = beta[tg * n_heads + h];
+            }
+            qko_chunked_step(n, kd, vd, qc, kc, vc, gc, bc, state + (int64_t)h * kd * vd, oc);
+            for (int t = 0; t < n; t++) memcpy(out + ((c0 + t) * n_heads + h) * vd, oc + t * vd, (size_t)vd * 4);
+        }
+    }
+}

@@ -66,6 +66,13 @@ void qko_swiglu(int64_t n, const float *gate, const float *up, float *act);
 
 int32_t qko_argmax(const float *v, int64_t n);
 
+/* Chunked Gated DeltaNet: one chunk of one head (n <= 64, kd, vd <= 128),
+ * and the chunk loop over all heads of a layer. */
+void qko_chunked_step(int n, int kd, int vd, const float *q, const float *k, const float *v, const float *g,
+                      const float *beta, float *state, float *out);
+void qko_deltanet_chunked(int64_t n_tok, int n_heads, int kd, int vd, const float *q, const float *k,
+                          const float *v, const float *g, const float *beta, float *state, float *out);
+
 /* Sampler chain (sample_with plus the min_new masking); st is the
  * reference's two-word rng state, advanced on the sampling path. */
 void qko_rng_seed(uint64_t seed, uint64_t *st);

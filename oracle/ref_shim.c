@@ -377,3 +377,33 @@ void ref_rng_seed(uint64_t seed, uint64_t *st) {
     st[0] = r.s0;
     st[1] = r.s1;
 }
+
+/* chunked_ssm_step_f32 (slm/chunked.c:287) with scratch of its own. */
+void ref_chunked_step(int n, int kd, int vd, const float *q, const float *k, const float *v, const float *g,
+                      const float *beta, float *state, float *out) {
+    const size_t C = CHUNK_SIZE, NK = C * (size_t)kd, NV = C * (size_t)vd, CC = C * C;
+    float *buf = (float *)calloc(2 * C + 6 * CC + 6 * NK + 8 * NV + (size_t)kd * vd, sizeof(float));
+    float *p = buf;
+    float *gcs = p; p += C;
+    float *gexp = p; p += C;
+    float *dm = p; p += CC;
+    float *kb = p; p += NK;
+    float *vb = p; p += NV;
+    float *kkd = p; p += CC;
+    float *lhs = p; p += CC;
+    float *attn = p; p += CC;
+    float *veff = p; p += NV > CC ? NV : CC;
+    float *kbg = p; p += NK;
+    float *kcd = p; p += NK;
+    float *akq = p; p += CC;
+    float *qg = p; p += NK;
+    float *ai = p; p += NV;
+    float *vp = p; p += NV;
+    float *vn = p; p += NV;
+    float *va = p; p += NV;
+    float *kgd = p; p += NK;
+    float *kv = p;
+    chunked_ssm_step_f32(n, kd, vd, q, k, v, g, beta, state, out, gcs, gexp, dm, kb, vb, kkd, lhs, attn, veff,
+                         kbg, kcd, akq, qg, ai, vp, vn, va, kgd, kv);
+    free(buf);
+}

@@ -621,6 +621,27 @@ int hip_sample(float *logits, int64_t n, const qk_sampler *sp, uint64_t *rng, co
     return QK_OK;
 }
 
+int hip_deltanet_chunked(const float *q, const float *k, const float *v, const float *g_log, const float *beta,
+                         int64_t n_tok, int n_heads, int k_hd, int v_hd, float *state, float *out, void *stream) {
+    int rc = require_init();
+    if (rc) return rc;
+    if (!q || !k || !v || !g_log || !beta || !state || !out) return fail(QK_ERR_ARG, "null pointer");
+    if (n_tok < 1 || n_tok > 0x7fffffffLL || n_heads < 1 || n_heads > 1024 || k_hd < 1 || v_hd < 1 ||
+        k_hd > QK_DELTANET_MAX_HD || v_hd > QK_DELTANET_MAX_HD)
+        return fail(QK_ERR_ARG, "bad shape n_tok=%lld heads=%d k_hd=%d v_hd=%d (head dims 1..%d)", (long long)n_tok,
+                    n_heads, k_hd, v_hd, QK_DELTANET_MAX_HD);
+    if (!aligned(q, 4) || !aligned(k, 4) || !aligned(v, 4) || !aligned(g_log, 4) || !aligned(beta, 4) ||
+        !aligned(state, 4) || !aligned(out, 4))
+        return fail(QK_ERR_ARG, "misaligned float arrays");
+    void *scratch = nullptr;
+    if ((rc = stream_scratch(stream_of(stream), qk::deltanet_scratch_bytes(n_heads, k_hd, v_hd), &scratch)))
+        return rc;
+    HIP_OK(qk::launch_deltanet(q, k, v, g_log, beta, n_tok, n_heads, k_hd, v_hd, state, out, scratch,
+                               stream_of(stream)),
+           "deltanet launch");
+    return QK_OK;
+}
+
 int hip_lmhead_q6k_argmax_topk_noalloc(const void *w, int64_t n, int64_t k, const void *xq, int topk,
                                        float *logits, int32_t *argmax, int32_t *topk_idx, float *topk_val,
                                        void *stream) {
@@ -875,6 +896,44 @@ int hip_qk_lmhead_host(const void *host_w, int64_t n, int64_t k, const float *x,
                "copy topk val");
     }
     HIP_OK(hipStreamSynchronize(l->stream), "hipStreamSynchronize");
+    return QK_OK;
+}
+
+int hip_qk_deltanet_host(int n, int k_hd, int v_hd, const float *q, const float *k, const float *v,
+                         const float *g_log, const float *beta, float *state, float *out) {
+    int rc = require_init();
+    if (rc) return rc;
+    if (!q || !k || !v || !g_log || !beta || !state || !out) return fail(QK_ERR_ARG, "null pointer");
+    if (n < 1 || n > 64 || k_hd < 1 || v_hd < 1 || k_hd > QK_DELTANET_MAX_HD || v_hd > QK_DELTANET_MAX_HD)
+        return fail(QK_ERR_ARG, "bad chunk n=%d k_hd=%d v_hd=%d (n 1..64, head dims 1..%d)", n, k_hd, v_hd,
+                    QK_DELTANET_MAX_HD);
+    Lane *l = nullptr;
+    if ((rc = my_lane(&l))) return rc;
+    // one buffer: q | k | v | g | beta | state, then out
+    const size_t nq = (size_t)n * k_hd, nv = (size_t)n * v_hd, ns = (size_t)k_hd * v_hd;
+    const size_t in_floats = 2 * nq + nv + 2 * (size_t)n + ns;
+    const size_t all = (in_floats + nv) * sizeof(float);
+    if ((rc = grow(&l->dx, &l->dx_cap, all)) || (rc = grow_host(&l->hx, &l->hx_cap, all))) return rc;
+    float *h = static_cast<float *>(l->hx);
+    std::memcpy(h, q, nq * 4);
+    std::memcpy(h + nq, k, nq * 4);
+    std::memcpy(h + 2 * nq, v, nv * 4);
+    std::memcpy(h + 2 * nq + nv, g_log, (size_t)n * 4);
+    std::memcpy(h + 2 * nq + nv + n, beta, (size_t)n * 4);
+    std::memcpy(h + 2 * nq + nv + 2 * n, state, ns * 4);
+    float *d = static_cast<float *>(l->dx);
+    HIP_OK(hipMemcpyAsync(d, h, in_floats * 4, hipMemcpyHostToDevice, l->stream), "hipMemcpyAsync(chunk in)");
+    void *scratch = nullptr;
+    if ((rc = stream_scratch(l->stream, qk::deltanet_scratch_bytes(1, k_hd, v_hd), &scratch))) return rc;
+    float *dstate = d + 2 * nq + nv + 2 * n, *dout = d + in_floats;
+    HIP_OK(qk::launch_deltanet(d, d + nq, d + 2 * nq, d + 2 * nq + nv, d + 2 * nq + nv + n, n, 1, k_hd, v_hd, dstate,
+                               dout, scratch, l->stream),
+           "deltanet launch");
+    HIP_OK(hipMemcpyAsync(h + 2 * nq + nv + 2 * n, dstate, (ns + nv) * 4, hipMemcpyDeviceToHost, l->stream),
+           "hipMemcpyAsync(chunk out)");
+    HIP_OK(hipStreamSynchronize(l->stream), "hipStreamSynchronize");
+    std::memcpy(state, h + 2 * nq + nv + 2 * n, ns * 4);
+    std::memcpy(out, h + in_floats, nv * 4);
     return QK_OK;
 }
 

@@ -66,6 +66,13 @@ hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k,
                          float penalty, int32_t window, uint64_t *rng, const int32_t *history, int32_t hist_n,
                          const int32_t *mask, int32_t n_mask, int32_t *token, void *scratch, hipStream_t s);
 
+// Chunked Gated DeltaNet (qk_deltanet.hip); scratch holds
+// deltanet_scratch_bytes(H, kd, vd); kd, vd <= 128.
+size_t deltanet_scratch_bytes(int32_t H, int32_t kd, int32_t vd);
+hipError_t launch_deltanet(const float *q, const float *k, const float *v, const float *g, const float *beta,
+                           int64_t n_tok, int32_t H, int32_t kd, int32_t vd, float *state, float *out,
+                           void *scratch, hipStream_t s);
+
 // Prefill GEMM (int8 MFMA); y[t*n + j].
 hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, const uint8_t *xq,
                        int64_t m, float *y, int fused, hipStream_t s);

@@ -7,9 +7,10 @@
  * the GPU with no edit to any reference file:
  *
  *   1. the four reference definitions of tensor_matmul_q4k_f32 /
- *      _q5k_ / _q6k_ / _q8_0_ (slm/tensor.c:827, 898, 1012, 952) are
- *      compiled under other names by renaming them around
- *      `#include "tensor.c"`;
+ *      _q5k_ / _q6k_ / _q8_0_ (slm/tensor.c:827, 898, 1012, 952), and the
+ *      chunked Gated DeltaNet step chunked_ssm_step_f32 (slm/chunked.c:287,
+ *      which tensor.c includes at :783), are compiled under other names by
+ *      renaming them around `#include "tensor.c"`;
  *   2. the originals' names are then defined here with the same
  *      signatures, ownership and layout: the result tensor (out_f, n)
  *      comes from x->arena, out[t*out_f + j] is the row dot of weight
@@ -53,11 +54,13 @@
 #define tensor_matmul_q5k_f32  qk_seam_cpu_matmul_q5k_f32
 #define tensor_matmul_q6k_f32  qk_seam_cpu_matmul_q6k_f32
 #define tensor_matmul_q8_0_f32 qk_seam_cpu_matmul_q8_0_f32
+#define chunked_ssm_step_f32   qk_seam_cpu_chunked_ssm_step_f32
 #include "tensor.c"
 #undef tensor_matmul_q4k_f32
 #undef tensor_matmul_q5k_f32
 #undef tensor_matmul_q6k_f32
 #undef tensor_matmul_q8_0_f32
+#undef chunked_ssm_step_f32
 
 #include "qk.h"
 
@@ -156,6 +159,31 @@ struct tensor *tensor_matmul_q6k_f32(const q6k_block *w, int64_t out_f, int64_t 
 
 struct tensor *tensor_matmul_q8_0_f32(const q8_0_block *w, int64_t out_f, int64_t k, struct tensor *x) {
     return qk_seam_matmul(QK_TYPE_Q8_0, w, out_f, k, x);
+}
+
+/* The chunked prefill's per-head, per-chunk step (slm/chunked.c:287),
+ * called by slm_forward_ssm_batch (slm/qwen.c:803) for every head of every
+ * chunk: the same arguments; q/k/v/g/beta in, state updated in place, out
+ * written, all host buffers, through hip_qk_deltanet_host. The scratch
+ * arguments are the reference's own working memory and are not needed. */
+static void chunked_ssm_step_f32(int n, int k_hd, int v_hd, const float *q, const float *k_in,
+                                 const float *v_in, const float *g_log, const float *beta, float *state,
+                                 float *out, float *gcs, float *gexp, float *decay_mask, float *k_beta,
+                                 float *v_beta, float *kk_dot, float *lhs, float *attn, float *v_eff,
+                                 float *kbeta_gexp, float *k_cumdecay, float *attn_kq, float *q_g_exp,
+                                 float *attn_inter, float *v_prime, float *v_new, float *v_attn,
+                                 float *key_gdiff, float *kgd_vnew) {
+    (void)gcs; (void)gexp; (void)decay_mask; (void)k_beta; (void)v_beta; (void)kk_dot; (void)lhs; (void)attn;
+    (void)v_eff; (void)kbeta_gexp; (void)k_cumdecay; (void)attn_kq; (void)q_g_exp; (void)attn_inter;
+    (void)v_prime; (void)v_new; (void)v_attn; (void)key_gdiff; (void)kgd_vnew;
+    qk_seam_init();
+    qk_seam_gpu_calls++;
+    int rc = hip_qk_deltanet_host(n, k_hd, v_hd, q, k_in, v_in, g_log, beta, state, out);
+    if (rc != QK_OK) {
+        fprintf(stderr, "qk_seam: chunked DeltaNet step (n=%d, %dx%d) failed (%d): %s\n", n, k_hd, v_hd, rc,
+                hip_qk_last_error());
+        abort();
+    }
 }
 
 /* Device copies are keyed by host address, and the reference borrows its

@@ -106,6 +106,8 @@ class QK:
         L.hip_silu_f32.argtypes = [_vp, _i64, _vp, _vp]
         L.hip_swiglu_q8k.argtypes = [_vp, _vp, _i64, _i64, _vp, _vp, _vp]
         L.hip_sample.argtypes = [_vp, _i64, C.POINTER(Sampler), _vp, _vp, C.c_int32, _vp, C.c_int32, _vp, _vp]
+        L.hip_deltanet_chunked.argtypes = [_vp] * 5 + [_i64, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp]
+        L.hip_qk_deltanet_host.argtypes = [C.c_int, C.c_int, C.c_int] + [_vp] * 7
         L.hip_qk_register_weight.argtypes = [_vp, C.c_int, _i64, _i64]
         L.hip_qk_unregister_weight.argtypes = [_vp]
         L.hip_qk_device_weight.argtypes = [_vp]
@@ -286,6 +288,33 @@ class QK:
                                    _dp(history) if hist_n else None, hist_n, m, len(mask), _dp(token),
                                    self._stream()))
         return token
+
+    def deltanet_chunked(self, q, k, v, g, beta, state, out=None):
+        """q, k: (n, H, kd); v: (n, H, vd); g, beta: (n, H); state (H, kd, vd)
+        updated in place; returns out (n, H, vd). Device tensors."""
+        import torch
+        n, H, kd = q.shape
+        vd = v.shape[2]
+        if out is None:
+            out = torch.empty((n, H, vd), dtype=torch.float32, device=q.device)
+        for t, want in ((k, n * H * kd), (v, n * H * vd), (g, n * H), (beta, n * H), (state, H * kd * vd),
+                        (out, n * H * vd)):
+            _need(t, 4 * want, "deltanet operand")
+        self._ck(self.L.hip_deltanet_chunked(_dp(q), _dp(k), _dp(v), _dp(g), _dp(beta), n, H, kd, vd, _dp(state),
+                                             _dp(out), self._stream()))
+        return out
+
+    def deltanet_host(self, q, k, v, g, beta, state):
+        """One head, one chunk, numpy in and out: returns (out, new state)."""
+        q = np.ascontiguousarray(q, np.float32)
+        n, kd = q.shape
+        vd = v.shape[1]
+        st = np.array(state, np.float32, copy=True)
+        out = np.empty((n, vd), np.float32)
+        arrs = [np.ascontiguousarray(a, np.float32) for a in (k, v, g, beta)]
+        self._ck(self.L.hip_qk_deltanet_host(n, kd, vd, q.ctypes.data_as(_vp), *[a.ctypes.data_as(_vp) for a in arrs],
+                                             st.ctypes.data_as(_vp), out.ctypes.data_as(_vp)))
+        return out, st
 
     # -- host seam --------------------------------------------------------------
     def matmul_host(self, wtype, w_np, out_f, k, x_np):
