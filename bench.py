@@ -398,6 +398,27 @@ def sampler_extras(torch, qk, lib, steps, warmup, vocab=248320):
     return out
 
 
+def deltanet_extras(torch, lib, steps, warmup, n_tok=512, heads=16, hd=128):
+    """hip_deltanet_chunked over one Gated DeltaNet layer of the model: 16
+    heads of 128, a 512-token prompt in 8 chunks of 64 (56 kernel launches),
+    inputs resident, the state carried in place from call to call."""
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.nn.functional.normalize(torch.randn(n_tok, heads, hd, device="cuda", generator=g), dim=2) / hd ** 0.5
+    k = torch.nn.functional.normalize(torch.randn(n_tok, heads, hd, device="cuda", generator=g), dim=2)
+    v = torch.nn.functional.silu(torch.randn(n_tok, heads, hd, device="cuda", generator=g))
+    gl = -torch.nn.functional.softplus(torch.randn(n_tok, heads, device="cuda", generator=g))
+    beta = torch.sigmoid(torch.randn(n_tok, heads, device="cuda", generator=g))
+    state = torch.zeros(heads, hd, hd, device="cuda")
+    out = torch.empty(n_tok, heads, hd, device="cuda")
+    args = tuple(C.c_void_p(t.data_ptr()) for t in (q, k, v, gl, beta)) + (n_tok, heads, hd, hd,
+                                                                            C.c_void_p(state.data_ptr()),
+                                                                            C.c_void_p(out.data_ptr()))
+    secs = GraphTimer(torch).time(lambda i, st: lib.L.hip_deltanet_chunked(*args, st), 2, steps, warmup)
+    us = secs / (2 * steps) * 1e6
+    return {f"deltanet_layer_{heads}x{hd}_n{n_tok}": {"us_per_layer": round(us, 1),
+                                                     "tok_s_per_layer": round(n_tok / us * 1e6, 1)}}
+
+
 # ---- CPU reference ------------------------------------------------------------------
 
 def host_description():
@@ -533,6 +554,23 @@ def cpu_extras(synth, seconds=2.0):
             calls += 1
         dt = time.perf_counter() - t0
         out[f"sample_vocab248320_{name}_1core"] = {"us_per_call": round(dt / calls * 1e6, 1), "calls": calls}
+    # the chunked DeltaNet step (chunked_ssm_step_f32, slm/chunked.c:287):
+    # one head, one chunk of 64, scaled to a 16-head 512-token layer
+    rng = np.random.default_rng(0)
+    qd = rng.standard_normal((64, 128)).astype(np.float32) * np.float32(0.01)
+    kd_ = rng.standard_normal((64, 128)).astype(np.float32) * np.float32(0.08)
+    vd_ = rng.standard_normal((64, 128)).astype(np.float32)
+    gd = -np.abs(rng.standard_normal(64)).astype(np.float32)
+    bd = np.full(64, 0.5, np.float32)
+    stt = np.zeros((128, 128), np.float32)
+    calls, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds / 2:
+        smp.chunked_step(qd, kd_, vd_, gd, bd, stt)
+        calls += 1
+    dt = time.perf_counter() - t0
+    out["deltanet_layer_16x128_n512_1core"] = {"us_per_layer": round(dt / calls * 128 * 1e6, 1),
+                                               "sample": f"{calls} chunk steps of 64 tokens x 1 head, "
+                                                         f"x 128 for 16 heads x 8 chunks"}
     return out
 
 
@@ -607,7 +645,8 @@ def main():
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--warm-seconds", type=float, default=WARM_S,
                     help="minimum warm-up replay time per case (short values keep profiler traces small)")
-    ap.add_argument("--only", choices=["all", "config1", "config3", "lmhead", "q4k_stream", "chain", "sampler"],
+    ap.add_argument("--only", choices=["all", "config1", "config3", "lmhead", "q4k_stream", "chain", "sampler",
+                                       "deltanet"],
                     default="all",
                     help="time one case only (profiling aids)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -646,6 +685,10 @@ def main():
     if a.only == "chain":
         print(json.dumps({"metric": "decode-chain link latency", "extra": chain_extras(torch, qk, lib, a.steps,
                                                                                          a.warmup)}))
+        return
+    if a.only == "deltanet":
+        print(json.dumps({"metric": "chunked DeltaNet layer", "extra": deltanet_extras(torch, lib, a.steps,
+                                                                                       a.warmup)}))
         return
     if a.only == "sampler":
         print(json.dumps({"metric": "sampler latency", "extra": sampler_extras(torch, qk, lib, a.steps, a.warmup)}))
@@ -722,6 +765,7 @@ def main():
         progress("decode-chain links and sampler")
         extra["chain_links"] = chain_extras(torch, qk, lib, max(10, a.steps // 10), 3)
         extra["sampler"] = sampler_extras(torch, qk, lib, max(5, a.steps // 20), 2)
+        extra["deltanet"] = deltanet_extras(torch, lib, max(5, a.steps // 20), 2)
         if not a.no_e2e:
             progress("config 4 end to end")
             extra["config4_e2e"] = e2e()

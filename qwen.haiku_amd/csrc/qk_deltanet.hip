@@ -61,42 +61,54 @@ __device__ __forceinline__ const float *row_of(const float *base, const DnArgs &
     return base + ((a.c0 + t) * a.H + h) * (int64_t)dim;
 }
 
-// 1. one workgroup per head
+// 1. grid (DN_PREP parts, H): every part rebuilds the cumulative gate of
+// its head (the g row staged in LDS by 64 lanes at once, then the serial
+// sum) and takes every DN_PREP-th slice of the elementwise work; part 0
+// writes the gate vectors.
+constexpr int DN_PREP = 8;
+
 __global__ __launch_bounds__(256) void k_dn_prep(DnArgs a, DnScratch s) {
-    const int h = blockIdx.x, n = a.n, kd = a.kd, vd = a.vd;
-    __shared__ float gcs[DN_C];
+    const int h = blockIdx.y, part = blockIdx.x, n = a.n, kd = a.kd, vd = a.vd;
+    __shared__ float gcs[DN_C], gex[DN_C];
     float *gv = s.gv + (int64_t)h * (3 * DN_C + 1);
+    if (threadIdx.x < n) gcs[threadIdx.x] = a.g[(a.c0 + threadIdx.x) * a.H + h];
+    __syncthreads();
     if (threadIdx.x == 0) {
         float run = 0.0f;
         for (int t = 0; t < n; t++) {
-            run = __fadd_rn(run, a.g[(a.c0 + t) * a.H + h]);
+            run = __fadd_rn(run, gcs[t]);
             gcs[t] = run;
         }
     }
     __syncthreads();
     const float glast = gcs[n - 1];
     for (int t = threadIdx.x; t < n; t += 256) {
-        gv[t] = gcs[t];
-        gv[DN_C + t] = qk_expf(gcs[t]);
-        gv[2 * DN_C + t] = qk_expf(__fsub_rn(glast, gcs[t]));
+        gex[t] = qk_expf(gcs[t]);
+        if (part == 0) {
+            gv[t] = gcs[t];
+            gv[DN_C + t] = gex[t];
+            gv[2 * DN_C + t] = qk_expf(__fsub_rn(glast, gcs[t]));
+        }
     }
-    if (threadIdx.x == 0) gv[3 * DN_C] = qk_expf(glast);
+    if (part == 0 && threadIdx.x == 0) gv[3 * DN_C] = qk_expf(glast);
+    __syncthreads();
+    const int first = part * 256 + threadIdx.x, stride = 256 * DN_PREP;
     float *dm = s.dm + (int64_t)h * DN_C * DN_C;
-    for (int p = threadIdx.x; p < n * n; p += 256) {
+    for (int p = first; p < n * n; p += stride) {
         const int i = p / n, j = p % n;
         dm[i * DN_C + j] = i > j ? qk_expf(__fsub_rn(gcs[i], gcs[j])) : 0.0f;
     }
     const int64_t ho = (int64_t)h * DN_C;
-    for (int p = threadIdx.x; p < n * kd; p += 256) {
+    for (int p = first; p < n * kd; p += stride) {
         const int t = p / kd, d = p % kd;
         const float b = a.beta[(a.c0 + t) * a.H + h];
         const float kbv = __fmul_rn(row_of(a.k, a, t, h, kd)[d], b);
-        const float ge = qk_expf(gcs[t]);
+        const float ge = gex[t];
         s.kb[(ho + t) * kd + d] = kbv;
         s.kbg[(ho + t) * kd + d] = __fmul_rn(kbv, ge);
         s.qg[(ho + t) * kd + d] = __fmul_rn(ge, row_of(a.q, a, t, h, kd)[d]);
     }
-    for (int p = threadIdx.x; p < n * vd; p += 256) {
+    for (int p = first; p < n * vd; p += stride) {
         const int t = p / vd, e = p % vd;
         s.vb[(ho + t) * vd + e] = __fmul_rn(row_of(a.v, a, t, h, vd)[e], a.beta[(a.c0 + t) * a.H + h]);
     }
@@ -111,13 +123,25 @@ __global__ __launch_bounds__(256) void k_dn_dots(DnArgs a, DnScratch s) {
     if (i0 >= n || j0 >= n) return;                   // whole workgroup: tile outside the chunk
     // tiles above the diagonal still run: they write the zeros the later
     // phases read there (the reference's matrices hold 0.0f above it)
-    __shared__ float kj[16][DN_D], kbi[16][DN_D], qi[16][DN_D];
+    __shared__ float kj[16][DN_D + 1], kbi[16][DN_D + 1], qi[16][DN_D + 1];   // padded: row r on bank r
     const int64_t ho = (int64_t)h * DN_C;
-    for (int p = threadIdx.x; p < 16 * kd; p += 256) {
-        const int r = p / kd, d = p % kd;
-        kj[r][d] = j0 + r < n ? row_of(a.k, a, j0 + r, h, kd)[d] : 0.0f;
-        kbi[r][d] = i0 + r < n ? s.kb[(ho + i0 + r) * kd + d] : 0.0f;
-        qi[r][d] = i0 + r < n ? row_of(a.q, a, i0 + r, h, kd)[d] : 0.0f;
+    {
+        float vk[8], vb[8], vq[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {                  // 8 * 256 = 16 rows of DN_D
+            const int p = u * 256 + threadIdx.x, r = p / DN_D, d = p % DN_D;
+            const bool jin = d < kd && j0 + r < n, iin = d < kd && i0 + r < n;
+            vk[u] = jin ? row_of(a.k, a, j0 + r, h, kd)[d] : 0.0f;
+            vb[u] = iin ? s.kb[(ho + i0 + r) * kd + d] : 0.0f;
+            vq[u] = iin ? row_of(a.q, a, i0 + r, h, kd)[d] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int p = u * 256 + threadIdx.x, r = p / DN_D, d = p % DN_D;
+            kj[r][d] = vk[u];
+            kbi[r][d] = vb[u];
+            qi[r][d] = vq[u];
+        }
     }
     __syncthreads();
     const int i = i0 + (threadIdx.x >> 4), j = j0 + (threadIdx.x & 15);
@@ -138,80 +162,179 @@ __global__ __launch_bounds__(256) void k_dn_dots(DnArgs a, DnScratch s) {
     s.akq[(ho + i) * DN_C + j] = kq;
 }
 
-// 3. one workgroup of 64 lanes per head, lane j solves column j:
-// X[i][j] = (B[i][j] - sum_{t<i} A[i][t] X[t][j]) / A[i][i] with A = I +
-// strict-lower kkd, B = -kkd (slm/chunked.c:196-213), then attn = X below
-// the diagonal, 1 on it, 0 above.
+// 3. one wave per head, lane j solves column j of (I + L) X = -L, L the
+// strictly lower kkd (slm/chunked.c:196-213): X[i][j] = (-L[i][j] -
+// sum_{t<i} L[i][t] X[t][j]) / 1. The order is right-looking: as soon as
+// X[k][j] is known every later row adds its term k, so each row's sum
+// still runs t = 0, 1, 2, ... in the reference's order while the
+// dependent path is a few operations per row. The sums sit in registers
+// (both loops unrolled) and LT = L transposed in LDS supplies row k's
+// broadcast coefficients. Dividing by the unit diagonal returns its
+// operand unchanged (a quiet NaN included), so the division is left out.
+// Rows and columns past the chunk run on stale scratch and are not
+// stored; then attn = X below the diagonal, 1 on it, 0 above.
 __global__ __launch_bounds__(64) void k_dn_solve(DnArgs a, DnScratch s) {
     const int h = blockIdx.x, n = a.n, j = threadIdx.x;
-    __shared__ float A[DN_C][DN_C + 1];
-    __shared__ float X[DN_C][DN_C + 1];
+    __shared__ float L[DN_C][DN_C + 1];                // lane j reads column j: no bank conflicts
+    __shared__ float LT[DN_C][DN_C];                   // LT[t][i] = L[i][t], read as broadcasts
     const int64_t ho = (int64_t)h * DN_C;
-    for (int p = threadIdx.x; p < n * n; p += 64) {
-        const int i = p / n, t = p % n;
-        A[i][t] = s.kkd[(ho + i) * DN_C + t];
+    {   // the whole 64x64 tile, sixteen 16-byte loads in flight per lane
+        const float4 *src = reinterpret_cast<const float4 *>(s.kkd + ho * DN_C);
+        float4 v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = src[u * 64 + j];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int p = (u * 64 + j) * 4, i = p / DN_C, t = p % DN_C;
+            L[i][t] = v[u].x;
+            L[i][t + 1] = v[u].y;
+            L[i][t + 2] = v[u].z;
+            L[i][t + 3] = v[u].w;
+            LT[t][i] = v[u].x;
+            LT[t + 1][i] = v[u].y;
+            LT[t + 2][i] = v[u].z;
+            LT[t + 3][i] = v[u].w;
+        }
     }
     __syncthreads();
-    if (j < n) {
-        for (int i = 0; i < n; i++) {
-            float acc = 0.0f;
-            for (int t = 0; t < i; t++) acc = __fadd_rn(acc, __fmul_rn(A[i][t], X[t][j]));
-            const float b = -A[i][j];                  // the negated kkd (zero on and above the diagonal: -0)
-            X[i][j] = __fdiv_rn(__fsub_rn(b, acc), 1.0f);   // lhs has a unit diagonal
-        }
-        for (int i = 0; i < n; i++)
-            s.attn[(ho + i) * DN_C + j] = j < i ? X[i][j] : (j == i ? 1.0f : 0.0f);
+    float *attn = s.attn + ho * DN_C;
+    float acc[DN_C];
+#pragma unroll
+    for (int i = 0; i < DN_C; i++) acc[i] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < DN_C; k++) {
+        const float x = __fsub_rn(-L[k][j], acc[k]);   // -L is -0 on and above the diagonal
+        if (k < n && j < n) attn[k * DN_C + j] = j < k ? x : (j == k ? 1.0f : 0.0f);
+#pragma unroll
+        for (int i = k + 1; i < DN_C; i++) acc[i] = __fadd_rn(acc[i], __fmul_rn(LT[k][i], x));
+        // keep one row's coefficients live at a time: the updates happen
+        // here, and the next row's loads stay below
+#pragma unroll
+        for (int i = k + 1; i < DN_C; i++) asm volatile("" : "+v"(acc[i]));
+        asm volatile("" ::: "memory");
     }
 }
 
-// 4. grid (n*max(kd,vd)/256 workgroups, H): lane (i, e)
+// Phases 4, 6 and 7 read DN_B operands ahead of the dependent adds: every
+// scratch row index below stays under DN_C (rows past the chunk hold stale
+// data and meet a zero coefficient), and reads of the caller's arrays stop
+// at the chunk's last row.
+constexpr int DN_R = 4;                                // rows per lane in phase 4
+constexpr int DN_B = 8;                                // loads in flight per chain
+
+// 4. grid (ceil(n/8) row blocks, 2, H): a workgroup computes eight rows
+// of attn @ V*beta (y = 0) or attn @ K*beta*exp(gcs) (y = 1). The rows of
+// the right-hand matrix up to the block's last row and the block's eight
+// attn rows are staged in LDS with every load in flight at once; lane
+// (row group, e) then runs four rows' chains in the reference's j order
+// from LDS. A zero coefficient leaves a chain unchanged (the reference
+// skips it), and j runs past a row's end only over zeros.
+constexpr int DN_RB = 8;                               // rows per workgroup
+
 __global__ __launch_bounds__(256) void k_dn_apply(DnArgs a, DnScratch s) {
-    const int h = blockIdx.y, n = a.n, kd = a.kd, vd = a.vd;
-    const int w = kd > vd ? kd : vd;
-    const int p = blockIdx.x * 256 + threadIdx.x;
-    if (p >= n * w) return;
-    const int i = p / w, e = p % w;
+    const int h = blockIdx.z, n = a.n, r0 = blockIdx.x * DN_RB;
+    const int w = blockIdx.y ? a.kd : a.vd;
     const int64_t ho = (int64_t)h * DN_C;
-    const float *arow = s.attn + (ho + i) * DN_C;
-    if (e < vd) {
-        float acc = 0.0f;
-        for (int j = 0; j <= i; j++) {
-            const float c = arow[j];
-            if (c == 0.0f) continue;
-            acc = __fadd_rn(acc, __fmul_rn(c, s.vb[(ho + j) * vd + e]));
+    const float *src = blockIdx.y ? s.kbg + ho * a.kd : s.vb + ho * a.vd;
+    float *dst = blockIdx.y ? s.kcd + ho * a.kd : s.veff + ho * a.vd;
+    __shared__ float M[DN_C * DN_D];
+    __shared__ float C[DN_RB][DN_C];
+    const int rows = r0 + DN_RB < n ? r0 + DN_RB : n;  // right-hand rows 0 .. rows-1
+    const int total = rows * w;                        // <= 64 * 128 = 32 * 256
+    {
+        float v[32];
+#pragma unroll
+        for (int u = 0; u < 32; u++) {
+            const int p = u * 256 + threadIdx.x;
+            v[u] = p < total ? src[p] : 0.0f;
         }
-        s.veff[(ho + i) * vd + e] = acc;
-    }
-    if (e < kd) {
-        float acc = 0.0f;
-        for (int j = 0; j <= i; j++) {
-            const float c = arow[j];
-            if (c == 0.0f) continue;
-            acc = __fadd_rn(acc, __fmul_rn(c, s.kbg[(ho + j) * kd + e]));
+#pragma unroll
+        for (int u = 0; u < 32; u++) {
+            const int p = u * 256 + threadIdx.x;
+            if (p < total) M[p] = v[u];
         }
-        s.kcd[(ho + i) * kd + e] = acc;
+        const float *arow = s.attn + (ho + r0) * DN_C;   // rows r0 .. r0+7 <= 63
+        const float c0 = arow[threadIdx.x], c1 = arow[256 + threadIdx.x];
+        (&C[0][0])[threadIdx.x] = c0;
+        (&C[0][0])[256 + threadIdx.x] = c1;
     }
+    __syncthreads();
+    const int rg = threadIdx.x / w, e = threadIdx.x % w;
+    const int i0 = r0 + rg * DN_R;
+    if (rg >= DN_RB / DN_R || i0 >= n) return;
+    const int last = i0 + DN_R - 1 < n - 1 ? i0 + DN_R - 1 : n - 1;
+    const float (*cr)[DN_C] = C + rg * DN_R;
+    float acc[DN_R] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j0 = 0; j0 <= last; j0 += DN_B) {         // j0 + DN_B - 1 <= 63
+        float xv[DN_B], cf[DN_R][DN_B];
+#pragma unroll
+        for (int u = 0; u < DN_B; u++) xv[u] = M[(j0 + u) * w + e];
+#pragma unroll
+        for (int r = 0; r < DN_R; r++)
+#pragma unroll
+            for (int u = 0; u < DN_B; u++)
+                cf[r][u] = (i0 + r <= last && j0 + u <= i0 + r) ? cr[r][j0 + u] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < DN_B; u++)
+#pragma unroll
+            for (int r = 0; r < DN_R; r++)
+                acc[r] = cf[r][u] != 0.0f ? __fadd_rn(acc[r], __fmul_rn(cf[r][u], xv[u])) : acc[r];
+    }
+#pragma unroll
+    for (int r = 0; r < DN_R; r++)
+        if (i0 + r <= last) dst[(i0 + r) * w + e] = acc[r];
 }
 
-// 5. grid (n*vd/256, H): lane (t, e) against the state carried in
+// 5. grid (ceil(n/4), ceil(vd/64), H): a workgroup takes four rows t and
+// 64 columns of the state carried in, both staged in LDS with every load
+// in flight at once; wave r runs row t0 + r, lane e its column, the two
+// chains (Q*exp(gcs) and the decayed keys against the state) in the
+// reference's d order.
+constexpr int DN_T = 4;                                // rows per workgroup in phase 5
+
 __global__ __launch_bounds__(256) void k_dn_state_in(DnArgs a, DnScratch s) {
-    const int h = blockIdx.y, n = a.n, kd = a.kd, vd = a.vd;
-    const int p = blockIdx.x * 256 + threadIdx.x;
-    if (p >= n * vd) return;
-    const int t = p / vd, e = p % vd;
+    const int h = blockIdx.z, n = a.n, kd = a.kd, vd = a.vd;
+    const int t0 = blockIdx.x * DN_T, e0 = blockIdx.y * 64;
     const int64_t ho = (int64_t)h * DN_C;
-    const float *st = a.state + (int64_t)h * kd * vd;
-    const float *qg = s.qg + (ho + t) * kd, *kc = s.kcd + (ho + t) * kd;
-    float ai = 0.0f, vp = 0.0f;
-    for (int d = 0; d < kd; d++) {
-        const float c = qg[d];
-        if (c == 0.0f) continue;
-        ai = __fadd_rn(ai, __fmul_rn(c, st[(int64_t)d * vd + e]));
+    __shared__ float S[DN_D][64];
+    __shared__ float Q[DN_T][DN_D], K[DN_T][DN_D];
+    {
+        const float *st = a.state + (int64_t)h * kd * vd;
+        float v[32];
+#pragma unroll
+        for (int u = 0; u < 32; u++) {                 // 32 * 256 = 128 rows of 64 columns
+            const int p = u * 256 + threadIdx.x, d = p >> 6, c = p & 63;
+            v[u] = d < kd && e0 + c < vd ? st[(int64_t)d * vd + e0 + c] : 0.0f;
+        }
+        float cq[2], ck[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {                  // 2 * 256 = DN_T rows of DN_D
+            const int p = u * 256 + threadIdx.x, r = p / DN_D, d = p % DN_D;
+            const bool in = d < kd && t0 + r < n;
+            cq[u] = in ? s.qg[(ho + t0 + r) * kd + d] : 0.0f;
+            ck[u] = in ? s.kcd[(ho + t0 + r) * kd + d] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 32; u++) {
+            const int p = u * 256 + threadIdx.x;
+            S[p >> 6][p & 63] = v[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int p = u * 256 + threadIdx.x;
+            Q[p / DN_D][p % DN_D] = cq[u];
+            K[p / DN_D][p % DN_D] = ck[u];
+        }
     }
+    __syncthreads();
+    const int r = threadIdx.x >> 6, c = threadIdx.x & 63, t = t0 + r, e = e0 + c;
+    if (t >= n || e >= vd) return;
+    float ai = 0.0f, vp = 0.0f;
+#pragma unroll 8
     for (int d = 0; d < kd; d++) {
-        const float c = kc[d];
-        if (c == 0.0f) continue;
-        vp = __fadd_rn(vp, __fmul_rn(c, st[(int64_t)d * vd + e]));
+        const float x = S[d][c], q = Q[r][d], k = K[r][d];
+        ai = q != 0.0f ? __fadd_rn(ai, __fmul_rn(q, x)) : ai;
+        vp = k != 0.0f ? __fadd_rn(vp, __fmul_rn(k, x)) : vp;
     }
     s.ainter[(ho + t) * vd + e] = ai;
     s.vnew[(ho + t) * vd + e] = __fsub_rn(s.veff[(ho + t) * vd + e], vp);
@@ -225,8 +348,20 @@ __global__ __launch_bounds__(256) void k_dn_out(DnArgs a, DnScratch s) {
     const int t = p / vd, e = p % vd;
     const int64_t ho = (int64_t)h * DN_C;
     const float *kq = s.akq + (ho + t) * DN_C;
+    const float *vn = s.vnew + ho * vd;
     float acc = 0.0f;
-    for (int u = 0; u < n; u++) acc = __fadd_rn(acc, __fmul_rn(kq[u], s.vnew[(ho + u) * vd + e]));
+    int u = 0;
+    for (; u + DN_B <= n; u += DN_B) {
+        float c[DN_B], x[DN_B];
+#pragma unroll
+        for (int w = 0; w < DN_B; w++) {
+            c[w] = kq[u + w];
+            x[w] = vn[(u + w) * vd + e];
+        }
+#pragma unroll
+        for (int w = 0; w < DN_B; w++) acc = __fadd_rn(acc, __fmul_rn(c[w], x[w]));
+    }
+    for (; u < n; u++) acc = __fadd_rn(acc, __fmul_rn(kq[u], vn[u * vd + e]));
     a.out[((a.c0 + t) * a.H + h) * (int64_t)vd + e] = __fadd_rn(s.ainter[(ho + t) * vd + e], acc);
 }
 
@@ -238,10 +373,22 @@ __global__ __launch_bounds__(256) void k_dn_state_out(DnArgs a, DnScratch s) {
     const int d = p / vd, e = p % vd;
     const int64_t ho = (int64_t)h * DN_C;
     const float *gv = s.gv + (int64_t)h * (3 * DN_C + 1);
+    const float *vn = s.vnew + ho * vd;
     float acc = 0.0f;
-    for (int t = 0; t < n; t++) {
+    int t = 0;
+    for (; t + DN_B <= n; t += DN_B) {
+        float kg[DN_B], x[DN_B];
+#pragma unroll
+        for (int w = 0; w < DN_B; w++) {
+            kg[w] = __fmul_rn(row_of(a.k, a, t + w, h, kd)[d], gv[2 * DN_C + t + w]);
+            x[w] = vn[(t + w) * vd + e];
+        }
+#pragma unroll
+        for (int w = 0; w < DN_B; w++) acc = __fadd_rn(acc, __fmul_rn(kg[w], x[w]));
+    }
+    for (; t < n; t++) {
         const float kg = __fmul_rn(row_of(a.k, a, t, h, kd)[d], gv[2 * DN_C + t]);
-        acc = __fadd_rn(acc, __fmul_rn(kg, s.vnew[(ho + t) * vd + e]));
+        acc = __fadd_rn(acc, __fmul_rn(kg, vn[t * vd + e]));
     }
     float *st = a.state + (int64_t)h * kd * vd + p;
     *st = __fadd_rn(__fmul_rn(*st, gv[3 * DN_C]), acc);
@@ -278,15 +425,14 @@ hipError_t launch_deltanet(const float *q, const float *k, const float *v, const
     s.veff = take((size_t)H * DN_C * vd);
     s.ainter = take((size_t)H * DN_C * vd);
     s.vnew = take((size_t)H * DN_C * vd);
-    const int w = kd > vd ? kd : vd;
     for (int64_t c0 = 0; c0 < n_tok; c0 += DN_C) {
         DnArgs a{q, k, v, g, beta, state, out, c0, (int32_t)(n_tok - c0 < DN_C ? n_tok - c0 : DN_C), H, kd, vd};
         const int n = a.n;
-        hipLaunchKernelGGL(k_dn_prep, dim3(H), dim3(256), 0, st, a, s);
+        hipLaunchKernelGGL(k_dn_prep, dim3(DN_PREP, H), dim3(256), 0, st, a, s);
         hipLaunchKernelGGL(k_dn_dots, dim3(4, 4, H), dim3(256), 0, st, a, s);
         hipLaunchKernelGGL(k_dn_solve, dim3(H), dim3(64), 0, st, a, s);
-        hipLaunchKernelGGL(k_dn_apply, dim3((n * w + 255) / 256, H), dim3(256), 0, st, a, s);
-        hipLaunchKernelGGL(k_dn_state_in, dim3((n * vd + 255) / 256, H), dim3(256), 0, st, a, s);
+        hipLaunchKernelGGL(k_dn_apply, dim3((n + DN_RB - 1) / DN_RB, 2, H), dim3(256), 0, st, a, s);
+        hipLaunchKernelGGL(k_dn_state_in, dim3((n + DN_T - 1) / DN_T, (vd + 63) / 64, H), dim3(256), 0, st, a, s);
         hipLaunchKernelGGL(k_dn_out, dim3((n * vd + 255) / 256, H), dim3(256), 0, st, a, s);
         hipLaunchKernelGGL(k_dn_state_out, dim3((kd * vd + 255) / 256, H), dim3(256), 0, st, a, s);
     }
