@@ -610,12 +610,14 @@ void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb, const uint8_t *__r
             }
         }
 
+        // non-temporal stores: the outputs are not read again by this
+        // kernel, and every workgroup's stores leave at about the same time
         const int64_t row = r0 + tn + col;
         if (row < n) {
 #pragma unroll
             for (int v = 0; v < VPW; v++) {
                 const int64_t t = t0 + tm + tok_of(VPW * g + v, h);
-                if (t < m) y[t * n + row] = FUSED ? bcast8(sum[v]) : sum[v];
+                if (t < m) __builtin_nontemporal_store(FUSED ? bcast8(sum[v]) : sum[v], &y[t * n + row]);
             }
         }
     };
