@@ -634,7 +634,7 @@ int hip_deltanet_chunked(const float *q, const float *k, const float *v, const f
         !aligned(state, 4) || !aligned(out, 4))
         return fail(QK_ERR_ARG, "misaligned float arrays");
     void *scratch = nullptr;
-    if ((rc = stream_scratch(stream_of(stream), qk::deltanet_scratch_bytes(n_heads, k_hd, v_hd), &scratch)))
+    if ((rc = stream_scratch(stream_of(stream), qk::deltanet_scratch_bytes(n_heads, k_hd, v_hd, n_tok), &scratch)))
         return rc;
     HIP_OK(qk::launch_deltanet(q, k, v, g_log, beta, n_tok, n_heads, k_hd, v_hd, state, out, scratch,
                                stream_of(stream)),
@@ -924,7 +924,7 @@ int hip_qk_deltanet_host(int n, int k_hd, int v_hd, const float *q, const float 
     float *d = static_cast<float *>(l->dx);
     HIP_OK(hipMemcpyAsync(d, h, in_floats * 4, hipMemcpyHostToDevice, l->stream), "hipMemcpyAsync(chunk in)");
     void *scratch = nullptr;
-    if ((rc = stream_scratch(l->stream, qk::deltanet_scratch_bytes(1, k_hd, v_hd), &scratch))) return rc;
+    if ((rc = stream_scratch(l->stream, qk::deltanet_scratch_bytes(1, k_hd, v_hd, n), &scratch))) return rc;
     float *dstate = d + 2 * nq + nv + 2 * n, *dout = d + in_floats;
     HIP_OK(qk::launch_deltanet(d, d + nq, d + 2 * nq, d + 2 * nq + nv, d + 2 * nq + nv + n, n, 1, k_hd, v_hd, dstate,
                                dout, scratch, l->stream),

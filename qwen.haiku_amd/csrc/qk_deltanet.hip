@@ -9,10 +9,12 @@
 // sums (no FMA in its build), and its result depends on that order. Here
 // every output element is one lane that runs its reduction in exactly the
 // reference's order, skipping the zero coefficients the reference skips;
-// the parallelism is across outputs and heads. A chunk is seven launches,
-// one per phase, each reading the previous phases' results from the
-// per-head scratch below (this file is built with -ffp-contract=off; the
-// only fused multiply-adds are inside qk_expf):
+// the parallelism is across outputs, heads and chunks. There are seven
+// phases, one launch each, each reading the previous phases' results from
+// the per-(chunk, head) scratch below; phases 1-4 do not depend on the
+// carried state and run for a group of chunks at once (this file is built
+// with -ffp-contract=off; the only fused multiply-adds are inside
+// qk_expf):
 //
 //   1 cumulative gate, exps, decay mask; K*beta, V*beta, K*beta*exp(gcs),
 //     Q*exp(gcs)
@@ -23,6 +25,7 @@
 //     v_new
 //   6 the intra-chunk attention on v_new; the output rows
 //   7 state := state * exp(g_last) + (K * exp(g_last - gcs))^T v_new
+//     (6 and 7 in one launch)
 #include "qk_dev.h"
 #include "qk_expf.h"
 #include "qk_kernels.h"
@@ -32,7 +35,7 @@ namespace qk {
 constexpr int DN_C = 64;                               // chunk size (CHUNK_SIZE)
 constexpr int DN_D = 128;                              // largest head dim handled
 
-// Per-head scratch of one chunk (floats).
+// Scratch of one group of chunks (floats), one slot per (chunk, head).
 struct DnScratch {
     float *gv;      // [H][3*64 + 1]: gcs | exp(gcs) | exp(glast - gcs) | exp(glast)
     float *dm;      // [H][64][64] decay mask
@@ -53,25 +56,45 @@ struct DnArgs {
     const float *q, *k, *v, *g, *beta;   // [n_tok][H][...]
     float *state;                        // [H][kd][vd]
     float *out;                          // [n_tok][H][vd]
-    int64_t c0;                          // first token of the chunk
-    int32_t n, H, kd, vd;
+    int64_t n_tok;                       // tokens of the call
+    int64_t g0;                          // first chunk of the group in flight
+    int32_t H, kd, vd;
+    int32_t c;                           // phases 5-7: the chunk of the group they run
 };
 
-__device__ __forceinline__ const float *row_of(const float *base, const DnArgs &a, int t, int h, int dim) {
-    return base + ((a.c0 + t) * a.H + h) * (int64_t)dim;
+// A scratch slot is one (chunk of the group, head): slot = c * H + h.
+struct DnChunk {
+    int slot, h, n;                      // slot, head, tokens of the chunk (1..64)
+    int64_t c0;                          // first token of the chunk
+};
+
+__device__ __forceinline__ DnChunk dn_chunk(const DnArgs &a, int slot) {
+    DnChunk ck;
+    ck.slot = slot;
+    ck.h = slot % a.H;
+    ck.c0 = (a.g0 + slot / a.H) * DN_C;
+    const int64_t rest = a.n_tok - ck.c0;
+    ck.n = rest < DN_C ? (int)rest : DN_C;
+    return ck;
 }
 
-// 1. grid (DN_PREP parts, H): every part rebuilds the cumulative gate of
-// its head (the g row staged in LDS by 64 lanes at once, then the serial
+__device__ __forceinline__ const float *row_of(const float *base, const DnArgs &a, int64_t c0, int t, int h,
+                                               int dim) {
+    return base + ((c0 + t) * a.H + h) * (int64_t)dim;
+}
+
+// 1. grid (DN_PREP parts, slots): every part rebuilds the cumulative gate
+// of its slot (the g row staged in LDS by 64 lanes at once, then the serial
 // sum) and takes every DN_PREP-th slice of the elementwise work; part 0
 // writes the gate vectors.
 constexpr int DN_PREP = 8;
 
 __global__ __launch_bounds__(256) void k_dn_prep(DnArgs a, DnScratch s) {
-    const int h = blockIdx.y, part = blockIdx.x, n = a.n, kd = a.kd, vd = a.vd;
+    const DnChunk ck = dn_chunk(a, blockIdx.y);
+    const int h = ck.h, part = blockIdx.x, n = ck.n, kd = a.kd, vd = a.vd;
     __shared__ float gcs[DN_C], gex[DN_C];
-    float *gv = s.gv + (int64_t)h * (3 * DN_C + 1);
-    if (threadIdx.x < n) gcs[threadIdx.x] = a.g[(a.c0 + threadIdx.x) * a.H + h];
+    float *gv = s.gv + (int64_t)ck.slot * (3 * DN_C + 1);
+    if (threadIdx.x < n) gcs[threadIdx.x] = a.g[(ck.c0 + threadIdx.x) * a.H + h];
     __syncthreads();
     if (threadIdx.x == 0) {
         float run = 0.0f;
@@ -93,47 +116,48 @@ __global__ __launch_bounds__(256) void k_dn_prep(DnArgs a, DnScratch s) {
     if (part == 0 && threadIdx.x == 0) gv[3 * DN_C] = qk_expf(glast);
     __syncthreads();
     const int first = part * 256 + threadIdx.x, stride = 256 * DN_PREP;
-    float *dm = s.dm + (int64_t)h * DN_C * DN_C;
+    float *dm = s.dm + (int64_t)ck.slot * DN_C * DN_C;
     for (int p = first; p < n * n; p += stride) {
         const int i = p / n, j = p % n;
         dm[i * DN_C + j] = i > j ? qk_expf(__fsub_rn(gcs[i], gcs[j])) : 0.0f;
     }
-    const int64_t ho = (int64_t)h * DN_C;
+    const int64_t ho = (int64_t)ck.slot * DN_C;
     for (int p = first; p < n * kd; p += stride) {
         const int t = p / kd, d = p % kd;
-        const float b = a.beta[(a.c0 + t) * a.H + h];
-        const float kbv = __fmul_rn(row_of(a.k, a, t, h, kd)[d], b);
+        const float b = a.beta[(ck.c0 + t) * a.H + h];
+        const float kbv = __fmul_rn(row_of(a.k, a, ck.c0, t, h, kd)[d], b);
         const float ge = gex[t];
         s.kb[(ho + t) * kd + d] = kbv;
         s.kbg[(ho + t) * kd + d] = __fmul_rn(kbv, ge);
-        s.qg[(ho + t) * kd + d] = __fmul_rn(ge, row_of(a.q, a, t, h, kd)[d]);
+        s.qg[(ho + t) * kd + d] = __fmul_rn(ge, row_of(a.q, a, ck.c0, t, h, kd)[d]);
     }
     for (int p = first; p < n * vd; p += stride) {
         const int t = p / vd, e = p % vd;
-        s.vb[(ho + t) * vd + e] = __fmul_rn(row_of(a.v, a, t, h, vd)[e], a.beta[(a.c0 + t) * a.H + h]);
+        s.vb[(ho + t) * vd + e] = __fmul_rn(row_of(a.v, a, ck.c0, t, h, vd)[e], a.beta[(ck.c0 + t) * a.H + h]);
     }
 }
 
-// 2. grid (4 j-tiles, 4 i-tiles, H); a 16x16 tile of (query i, key j) per
+// 2. grid (4 j-tiles, 4 i-tiles, slots); a 16x16 tile of (query i, key j) per
 // workgroup, the 16 K rows of its keys and the 16 Kbeta / Q rows of its
 // queries in LDS
 __global__ __launch_bounds__(256) void k_dn_dots(DnArgs a, DnScratch s) {
-    const int h = blockIdx.z, n = a.n, kd = a.kd;
+    const DnChunk ck = dn_chunk(a, blockIdx.z);
+    const int h = ck.h, n = ck.n, kd = a.kd;
     const int i0 = blockIdx.y * 16, j0 = blockIdx.x * 16;
     if (i0 >= n || j0 >= n) return;                   // whole workgroup: tile outside the chunk
     // tiles above the diagonal still run: they write the zeros the later
     // phases read there (the reference's matrices hold 0.0f above it)
     __shared__ float kj[16][DN_D + 1], kbi[16][DN_D + 1], qi[16][DN_D + 1];   // padded: row r on bank r
-    const int64_t ho = (int64_t)h * DN_C;
+    const int64_t ho = (int64_t)ck.slot * DN_C;
     {
         float vk[8], vb[8], vq[8];
 #pragma unroll
         for (int u = 0; u < 8; u++) {                  // 8 * 256 = 16 rows of DN_D
             const int p = u * 256 + threadIdx.x, r = p / DN_D, d = p % DN_D;
             const bool jin = d < kd && j0 + r < n, iin = d < kd && i0 + r < n;
-            vk[u] = jin ? row_of(a.k, a, j0 + r, h, kd)[d] : 0.0f;
+            vk[u] = jin ? row_of(a.k, a, ck.c0, j0 + r, h, kd)[d] : 0.0f;
             vb[u] = iin ? s.kb[(ho + i0 + r) * kd + d] : 0.0f;
-            vq[u] = iin ? row_of(a.q, a, i0 + r, h, kd)[d] : 0.0f;
+            vq[u] = iin ? row_of(a.q, a, ck.c0, i0 + r, h, kd)[d] : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
@@ -146,7 +170,7 @@ __global__ __launch_bounds__(256) void k_dn_dots(DnArgs a, DnScratch s) {
     __syncthreads();
     const int i = i0 + (threadIdx.x >> 4), j = j0 + (threadIdx.x & 15);
     if (i >= n || j >= n) return;
-    const float *dm = s.dm + (int64_t)h * DN_C * DN_C;
+    const float *dm = s.dm + (int64_t)ck.slot * DN_C * DN_C;
     float kk = 0.0f, kq = 0.0f;
     if (i > j) {
         float acc = 0.0f;
@@ -162,56 +186,76 @@ __global__ __launch_bounds__(256) void k_dn_dots(DnArgs a, DnScratch s) {
     s.akq[(ho + i) * DN_C + j] = kq;
 }
 
-// 3. one wave per head, lane j solves column j of (I + L) X = -L, L the
+// 3. one wave per slot, lane j solves column j of (I + L) X = -L, L the
 // strictly lower kkd (slm/chunked.c:196-213): X[i][j] = (-L[i][j] -
 // sum_{t<i} L[i][t] X[t][j]) / 1. The order is right-looking: as soon as
 // X[k][j] is known every later row adds its term k, so each row's sum
 // still runs t = 0, 1, 2, ... in the reference's order while the
 // dependent path is a few operations per row. The sums sit in registers
-// (both loops unrolled) and LT = L transposed in LDS supplies row k's
-// broadcast coefficients. Dividing by the unit diagonal returns its
-// operand unchanged (a quiet NaN included), so the division is left out.
-// Rows and columns past the chunk run on stale scratch and are not
-// stored; then attn = X below the diagonal, 1 on it, 0 above.
+// (both loops unrolled). LS[k] holds column k of L below the diagonal,
+// L[k+1 .. 63][k], from its first element, so row k's broadcast
+// coefficients arrive as a few aligned 16-byte reads issued together.
+// Dividing by the unit diagonal returns its operand unchanged (a quiet NaN
+// included), so the division is left out. Rows and columns past the chunk
+// run on stale scratch and are not stored; attn = X below the diagonal,
+// 1 on it, 0 above.
 __global__ __launch_bounds__(64) void k_dn_solve(DnArgs a, DnScratch s) {
-    const int h = blockIdx.x, n = a.n, j = threadIdx.x;
+    const DnChunk ck = dn_chunk(a, blockIdx.x);
+    const int n = ck.n, j = threadIdx.x;
     __shared__ float L[DN_C][DN_C + 1];                // lane j reads column j: no bank conflicts
-    __shared__ float LT[DN_C][DN_C];                   // LT[t][i] = L[i][t], read as broadcasts
-    const int64_t ho = (int64_t)h * DN_C;
+    __shared__ float4 LS[DN_C][DN_C / 4];              // LS[k][q] = L[k+1+4q .. k+4+4q][k]
+    const int64_t ho = (int64_t)ck.slot * DN_C;
     {   // the whole 64x64 tile, sixteen 16-byte loads in flight per lane
         const float4 *src = reinterpret_cast<const float4 *>(s.kkd + ho * DN_C);
         float4 v[16];
 #pragma unroll
         for (int u = 0; u < 16; u++) v[u] = src[u * 64 + j];
+        float *ls = &LS[0][0].x;
 #pragma unroll
         for (int u = 0; u < 16; u++) {
             const int p = (u * 64 + j) * 4, i = p / DN_C, t = p % DN_C;
-            L[i][t] = v[u].x;
-            L[i][t + 1] = v[u].y;
-            L[i][t + 2] = v[u].z;
-            L[i][t + 3] = v[u].w;
-            LT[t][i] = v[u].x;
-            LT[t + 1][i] = v[u].y;
-            LT[t + 2][i] = v[u].z;
-            LT[t + 3][i] = v[u].w;
+            const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                L[i][t + c] = e[c];
+                if (i > t + c) ls[(t + c) * DN_C + (i - t - c - 1)] = e[c];
+            }
         }
     }
     __syncthreads();
-    float *attn = s.attn + ho * DN_C;
-    float acc[DN_C];
+    float acc[DN_C], xs[DN_C];
 #pragma unroll
     for (int i = 0; i < DN_C; i++) acc[i] = 0.0f;
 #pragma unroll
     for (int k = 0; k < DN_C; k++) {
         const float x = __fsub_rn(-L[k][j], acc[k]);   // -L is -0 on and above the diagonal
-        if (k < n && j < n) attn[k * DN_C + j] = j < k ? x : (j == k ? 1.0f : 0.0f);
+        xs[k] = x;
+        constexpr int nq_max = DN_C / 4;
+        const int nq = (DN_C - 1 - k + 3) / 4;          // compile-time after unrolling
+        float cf[DN_C];
 #pragma unroll
-        for (int i = k + 1; i < DN_C; i++) acc[i] = __fadd_rn(acc[i], __fmul_rn(LT[k][i], x));
+        for (int q = 0; q < nq_max; q++) {
+            if (q < nq) {
+                const float4 c4 = LS[k][q];
+                cf[4 * q] = c4.x;
+                cf[4 * q + 1] = c4.y;
+                cf[4 * q + 2] = c4.z;
+                cf[4 * q + 3] = c4.w;
+            }
+        }
+#pragma unroll
+        for (int i = k + 1; i < DN_C; i++) acc[i] = __fadd_rn(acc[i], __fmul_rn(cf[i - k - 1], x));
         // keep one row's coefficients live at a time: the updates happen
-        // here, and the next row's loads stay below
+        // here, and the next row's reads stay below
 #pragma unroll
         for (int i = k + 1; i < DN_C; i++) asm volatile("" : "+v"(acc[i]));
         asm volatile("" ::: "memory");
+    }
+    if (j < n) {
+        float *attn = s.attn + ho * DN_C;
+#pragma unroll
+        for (int k = 0; k < DN_C; k++)
+            if (k < n) attn[k * DN_C + j] = j < k ? xs[k] : (j == k ? 1.0f : 0.0f);
     }
 }
 
@@ -222,23 +266,28 @@ __global__ __launch_bounds__(64) void k_dn_solve(DnArgs a, DnScratch s) {
 constexpr int DN_R = 4;                                // rows per lane in phase 4
 constexpr int DN_B = 8;                                // loads in flight per chain
 
-// 4. grid (ceil(n/8) row blocks, 2, H): a workgroup computes eight rows
-// of attn @ V*beta (y = 0) or attn @ K*beta*exp(gcs) (y = 1). The rows of
-// the right-hand matrix up to the block's last row and the block's eight
-// attn rows are staged in LDS with every load in flight at once; lane
-// (row group, e) then runs four rows' chains in the reference's j order
-// from LDS. A zero coefficient leaves a chain unchanged (the reference
-// skips it), and j runs past a row's end only over zeros.
+// 4. grid (8 row blocks, 2, slots), blocks past the chunk exit: a
+// workgroup computes eight rows of attn @ V*beta (y = 0) or
+// attn @ K*beta*exp(gcs) (y = 1). The rows of the right-hand matrix up to
+// the block's last row and the block's eight attn rows (j-major, so one
+// 16-byte read gives a lane its four rows' coefficients) are staged in LDS
+// with every load in flight at once; lane (row group, e) then runs four
+// rows' chains in the reference's j order from LDS. A zero coefficient
+// leaves a chain unchanged (the reference skips it). Columns j below the
+// group's first row belong to all four rows; the last few columns are
+// gated by j <= i. Rows past the chunk are computed and not stored.
 constexpr int DN_RB = 8;                               // rows per workgroup
 
 __global__ __launch_bounds__(256) void k_dn_apply(DnArgs a, DnScratch s) {
-    const int h = blockIdx.z, n = a.n, r0 = blockIdx.x * DN_RB;
+    const DnChunk ck = dn_chunk(a, blockIdx.z);
+    const int n = ck.n, r0 = blockIdx.x * DN_RB;
+    if (r0 >= n) return;                               // whole workgroup: rows past the chunk
     const int w = blockIdx.y ? a.kd : a.vd;
-    const int64_t ho = (int64_t)h * DN_C;
+    const int64_t ho = (int64_t)ck.slot * DN_C;
     const float *src = blockIdx.y ? s.kbg + ho * a.kd : s.vb + ho * a.vd;
     float *dst = blockIdx.y ? s.kcd + ho * a.kd : s.veff + ho * a.vd;
     __shared__ float M[DN_C * DN_D];
-    __shared__ float C[DN_RB][DN_C];
+    __shared__ float4 Ct[DN_C][DN_RB / DN_R];          // Ct[j][g]: rows r0+4g .. r0+4g+3 at column j
     const int rows = r0 + DN_RB < n ? r0 + DN_RB : n;  // right-hand rows 0 .. rows-1
     const int total = rows * w;                        // <= 64 * 128 = 32 * 256
     {
@@ -248,44 +297,50 @@ __global__ __launch_bounds__(256) void k_dn_apply(DnArgs a, DnScratch s) {
             const int p = u * 256 + threadIdx.x;
             v[u] = p < total ? src[p] : 0.0f;
         }
+        const float *arow = s.attn + (ho + r0) * DN_C;   // rows r0 .. r0+7 <= 63
+        const float c0 = arow[threadIdx.x], c1 = arow[256 + threadIdx.x];
 #pragma unroll
         for (int u = 0; u < 32; u++) {
             const int p = u * 256 + threadIdx.x;
             if (p < total) M[p] = v[u];
         }
-        const float *arow = s.attn + (ho + r0) * DN_C;   // rows r0 .. r0+7 <= 63
-        const float c0 = arow[threadIdx.x], c1 = arow[256 + threadIdx.x];
-        (&C[0][0])[threadIdx.x] = c0;
-        (&C[0][0])[256 + threadIdx.x] = c1;
+        float *ct = &Ct[0][0].x;
+        ct[(threadIdx.x % DN_C) * DN_RB + threadIdx.x / DN_C] = c0;
+        ct[(threadIdx.x % DN_C) * DN_RB + 4 + threadIdx.x / DN_C] = c1;
     }
     __syncthreads();
     const int rg = threadIdx.x / w, e = threadIdx.x % w;
     const int i0 = r0 + rg * DN_R;
     if (rg >= DN_RB / DN_R || i0 >= n) return;
     const int last = i0 + DN_R - 1 < n - 1 ? i0 + DN_R - 1 : n - 1;
-    const float (*cr)[DN_C] = C + rg * DN_R;
     float acc[DN_R] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j0 = 0; j0 <= last; j0 += DN_B) {         // j0 + DN_B - 1 <= 63
-        float xv[DN_B], cf[DN_R][DN_B];
+    auto term = [&](int j, const float4 c, float x, bool gate) __attribute__((always_inline)) {
+        const float cf[DN_R] = {c.x, c.y, c.z, c.w};
 #pragma unroll
-        for (int u = 0; u < DN_B; u++) xv[u] = M[(j0 + u) * w + e];
+        for (int r = 0; r < DN_R; r++) {
+            const float k = (!gate || j <= i0 + r) ? cf[r] : 0.0f;
+            acc[r] = k != 0.0f ? __fadd_rn(acc[r], __fmul_rn(k, x)) : acc[r];
+        }
+    };
+    int j0 = 0;
+    for (; j0 + DN_B <= i0; j0 += DN_B) {              // j < i0: a term of every row of the group
+        float xv[DN_B];
+        float4 c4[DN_B];
 #pragma unroll
-        for (int r = 0; r < DN_R; r++)
+        for (int u = 0; u < DN_B; u++) {
+            xv[u] = M[(j0 + u) * w + e];
+            c4[u] = Ct[j0 + u][rg];
+        }
 #pragma unroll
-            for (int u = 0; u < DN_B; u++)
-                cf[r][u] = (i0 + r <= last && j0 + u <= i0 + r) ? cr[r][j0 + u] : 0.0f;
-#pragma unroll
-        for (int u = 0; u < DN_B; u++)
-#pragma unroll
-            for (int r = 0; r < DN_R; r++)
-                acc[r] = cf[r][u] != 0.0f ? __fadd_rn(acc[r], __fmul_rn(cf[r][u], xv[u])) : acc[r];
+        for (int u = 0; u < DN_B; u++) term(j0 + u, c4[u], xv[u], false);
     }
+    for (int j = j0; j <= last; j++) term(j, Ct[j][rg], M[j * w + e], true);
 #pragma unroll
     for (int r = 0; r < DN_R; r++)
         if (i0 + r <= last) dst[(i0 + r) * w + e] = acc[r];
 }
 
-// 5. grid (ceil(n/4), ceil(vd/64), H): a workgroup takes four rows t and
+// 5. grid (ceil(n/4), ceil(vd/64), H), for chunk c of the group: a workgroup takes four rows t and
 // 64 columns of the state carried in, both staged in LDS with every load
 // in flight at once; wave r runs row t0 + r, lane e its column, the two
 // chains (Q*exp(gcs) and the decayed keys against the state) in the
@@ -293,9 +348,10 @@ __global__ __launch_bounds__(256) void k_dn_apply(DnArgs a, DnScratch s) {
 constexpr int DN_T = 4;                                // rows per workgroup in phase 5
 
 __global__ __launch_bounds__(256) void k_dn_state_in(DnArgs a, DnScratch s) {
-    const int h = blockIdx.z, n = a.n, kd = a.kd, vd = a.vd;
+    const DnChunk ck = dn_chunk(a, a.c * a.H + blockIdx.z);
+    const int h = ck.h, n = ck.n, kd = a.kd, vd = a.vd;
     const int t0 = blockIdx.x * DN_T, e0 = blockIdx.y * 64;
-    const int64_t ho = (int64_t)h * DN_C;
+    const int64_t ho = (int64_t)ck.slot * DN_C;
     __shared__ float S[DN_D][64];
     __shared__ float Q[DN_T][DN_D], K[DN_T][DN_D];
     {
@@ -340,13 +396,18 @@ __global__ __launch_bounds__(256) void k_dn_state_in(DnArgs a, DnScratch s) {
     s.vnew[(ho + t) * vd + e] = __fsub_rn(s.veff[(ho + t) * vd + e], vp);
 }
 
-// 6. grid (n*vd/256, H): lane (t, e), the output row element
-__global__ __launch_bounds__(256) void k_dn_out(DnArgs a, DnScratch s) {
-    const int h = blockIdx.y, n = a.n, vd = a.vd;
-    const int p = blockIdx.x * 256 + threadIdx.x;
+// Phases 6 and 7 share one launch for chunk c of the group: grid
+// (ceil(n*vd/256) + ceil(kd*vd/256), H), the first nout blocks write the
+// output rows and the rest the state carried out. Neither reads what the
+// other writes.
+// 6. lane (t, e), the output row element
+__device__ __forceinline__ void dn_out_block(const DnArgs &a, const DnScratch &s, int bx) {
+    const DnChunk ck = dn_chunk(a, a.c * a.H + blockIdx.y);
+    const int h = ck.h, n = ck.n, vd = a.vd;
+    const int p = bx * 256 + threadIdx.x;
     if (p >= n * vd) return;
     const int t = p / vd, e = p % vd;
-    const int64_t ho = (int64_t)h * DN_C;
+    const int64_t ho = (int64_t)ck.slot * DN_C;
     const float *kq = s.akq + (ho + t) * DN_C;
     const float *vn = s.vnew + ho * vd;
     float acc = 0.0f;
@@ -362,17 +423,18 @@ __global__ __launch_bounds__(256) void k_dn_out(DnArgs a, DnScratch s) {
         for (int w = 0; w < DN_B; w++) acc = __fadd_rn(acc, __fmul_rn(c[w], x[w]));
     }
     for (; u < n; u++) acc = __fadd_rn(acc, __fmul_rn(kq[u], vn[u * vd + e]));
-    a.out[((a.c0 + t) * a.H + h) * (int64_t)vd + e] = __fadd_rn(s.ainter[(ho + t) * vd + e], acc);
+    a.out[((ck.c0 + t) * a.H + h) * (int64_t)vd + e] = __fadd_rn(s.ainter[(ho + t) * vd + e], acc);
 }
 
-// 7. grid (kd*vd/256, H): lane (d, e), the state carried out
-__global__ __launch_bounds__(256) void k_dn_state_out(DnArgs a, DnScratch s) {
-    const int h = blockIdx.y, n = a.n, kd = a.kd, vd = a.vd;
-    const int p = blockIdx.x * 256 + threadIdx.x;
+// 7. lane (d, e), the state carried out
+__device__ __forceinline__ void dn_state_out_block(const DnArgs &a, const DnScratch &s, int bx) {
+    const DnChunk ck = dn_chunk(a, a.c * a.H + blockIdx.y);
+    const int h = ck.h, n = ck.n, kd = a.kd, vd = a.vd;
+    const int p = bx * 256 + threadIdx.x;
     if (p >= kd * vd) return;
     const int d = p / vd, e = p % vd;
-    const int64_t ho = (int64_t)h * DN_C;
-    const float *gv = s.gv + (int64_t)h * (3 * DN_C + 1);
+    const int64_t ho = (int64_t)ck.slot * DN_C;
+    const float *gv = s.gv + (int64_t)ck.slot * (3 * DN_C + 1);
     const float *vn = s.vnew + ho * vd;
     float acc = 0.0f;
     int t = 0;
@@ -380,31 +442,52 @@ __global__ __launch_bounds__(256) void k_dn_state_out(DnArgs a, DnScratch s) {
         float kg[DN_B], x[DN_B];
 #pragma unroll
         for (int w = 0; w < DN_B; w++) {
-            kg[w] = __fmul_rn(row_of(a.k, a, t + w, h, kd)[d], gv[2 * DN_C + t + w]);
+            kg[w] = __fmul_rn(row_of(a.k, a, ck.c0, t + w, h, kd)[d], gv[2 * DN_C + t + w]);
             x[w] = vn[(t + w) * vd + e];
         }
 #pragma unroll
         for (int w = 0; w < DN_B; w++) acc = __fadd_rn(acc, __fmul_rn(kg[w], x[w]));
     }
     for (; t < n; t++) {
-        const float kg = __fmul_rn(row_of(a.k, a, t, h, kd)[d], gv[2 * DN_C + t]);
+        const float kg = __fmul_rn(row_of(a.k, a, ck.c0, t, h, kd)[d], gv[2 * DN_C + t]);
         acc = __fadd_rn(acc, __fmul_rn(kg, vn[t * vd + e]));
     }
     float *st = a.state + (int64_t)h * kd * vd + p;
     *st = __fadd_rn(__fmul_rn(*st, gv[3 * DN_C]), acc);
 }
 
+__global__ __launch_bounds__(256) void k_dn_out_state(DnArgs a, DnScratch s, int nout) {
+    if ((int)blockIdx.x < nout) dn_out_block(a, s, blockIdx.x);
+    else dn_state_out_block(a, s, blockIdx.x - nout);
+}
+
 // ---- launcher -----------------------------------------------------------------
-size_t deltanet_scratch_bytes(int32_t H, int32_t kd, int32_t vd) {
+// Phases 1-4 read only their chunk's own inputs, so they run for a group
+// of chunks at once (one launch per phase over every (chunk, head) slot of
+// the group); phases 5-7 carry the state and run chunk after chunk. A
+// group holds at most DN_SLOTS slots (one head's slot is about 330 KB of
+// scratch at head dims 128), and at least one chunk.
+constexpr int DN_SLOTS = 256;
+
+static int dn_group(int32_t H, int64_t n_tok) {
+    const int64_t chunks = (n_tok + DN_C - 1) / DN_C;
+    const int64_t g = DN_SLOTS / H > 1 ? DN_SLOTS / H : 1;
+    return (int)(g < chunks ? g : chunks);
+}
+
+size_t deltanet_scratch_bytes(int32_t H, int32_t kd, int32_t vd, int64_t n_tok) {
+    const size_t slots = (size_t)dn_group(H, n_tok) * (size_t)H;
     const size_t per = (size_t)(3 * DN_C + 1) + 4 * (size_t)DN_C * DN_C + 4 * (size_t)DN_C * kd +
                        4 * (size_t)DN_C * vd;
-    return (per * (size_t)H + 13 * 64) * sizeof(float) + 256;   // 13 arrays, each rounded up to 64 floats
+    return (per * slots + 13 * 64) * sizeof(float) + 256;   // 13 arrays, each rounded up to 64 floats
 }
 
 hipError_t launch_deltanet(const float *q, const float *k, const float *v, const float *g, const float *beta,
                            int64_t n_tok, int32_t H, int32_t kd, int32_t vd, float *state, float *out,
                            void *scratch, hipStream_t st) {
-    if (kd > DN_D || vd > DN_D) return hipErrorInvalidValue;
+    if (kd > DN_D || vd > DN_D || n_tok < 1 || H < 1) return hipErrorInvalidValue;
+    const int G = dn_group(H, n_tok);
+    const size_t slots = (size_t)G * (size_t)H;
     float *p = static_cast<float *>(scratch);
     auto take = [&](size_t n_floats) {
         float *r = p;
@@ -412,29 +495,37 @@ hipError_t launch_deltanet(const float *q, const float *k, const float *v, const
         return r;
     };
     DnScratch s;
-    s.gv = take((size_t)H * (3 * DN_C + 1));
-    s.dm = take((size_t)H * DN_C * DN_C);
-    s.kkd = take((size_t)H * DN_C * DN_C);
-    s.akq = take((size_t)H * DN_C * DN_C);
-    s.attn = take((size_t)H * DN_C * DN_C);
-    s.kb = take((size_t)H * DN_C * kd);
-    s.kbg = take((size_t)H * DN_C * kd);
-    s.qg = take((size_t)H * DN_C * kd);
-    s.kcd = take((size_t)H * DN_C * kd);
-    s.vb = take((size_t)H * DN_C * vd);
-    s.veff = take((size_t)H * DN_C * vd);
-    s.ainter = take((size_t)H * DN_C * vd);
-    s.vnew = take((size_t)H * DN_C * vd);
-    for (int64_t c0 = 0; c0 < n_tok; c0 += DN_C) {
-        DnArgs a{q, k, v, g, beta, state, out, c0, (int32_t)(n_tok - c0 < DN_C ? n_tok - c0 : DN_C), H, kd, vd};
-        const int n = a.n;
-        hipLaunchKernelGGL(k_dn_prep, dim3(DN_PREP, H), dim3(256), 0, st, a, s);
-        hipLaunchKernelGGL(k_dn_dots, dim3(4, 4, H), dim3(256), 0, st, a, s);
-        hipLaunchKernelGGL(k_dn_solve, dim3(H), dim3(64), 0, st, a, s);
-        hipLaunchKernelGGL(k_dn_apply, dim3((n + DN_RB - 1) / DN_RB, 2, H), dim3(256), 0, st, a, s);
-        hipLaunchKernelGGL(k_dn_state_in, dim3((n + DN_T - 1) / DN_T, (vd + 63) / 64, H), dim3(256), 0, st, a, s);
-        hipLaunchKernelGGL(k_dn_out, dim3((n * vd + 255) / 256, H), dim3(256), 0, st, a, s);
-        hipLaunchKernelGGL(k_dn_state_out, dim3((kd * vd + 255) / 256, H), dim3(256), 0, st, a, s);
+    s.gv = take(slots * (3 * DN_C + 1));
+    s.dm = take(slots * DN_C * DN_C);
+    s.kkd = take(slots * DN_C * DN_C);
+    s.akq = take(slots * DN_C * DN_C);
+    s.attn = take(slots * DN_C * DN_C);
+    s.kb = take(slots * DN_C * kd);
+    s.kbg = take(slots * DN_C * kd);
+    s.qg = take(slots * DN_C * kd);
+    s.kcd = take(slots * DN_C * kd);
+    s.vb = take(slots * DN_C * vd);
+    s.veff = take(slots * DN_C * vd);
+    s.ainter = take(slots * DN_C * vd);
+    s.vnew = take(slots * DN_C * vd);
+    const int64_t chunks = (n_tok + DN_C - 1) / DN_C;
+    for (int64_t g0 = 0; g0 < chunks; g0 += G) {
+        const int gc = (int)(chunks - g0 < G ? chunks - g0 : G);   // chunks in this group
+        const unsigned gs = (unsigned)(gc * H);                     // slots in this group
+        DnArgs a{q, k, v, g, beta, state, out, n_tok, g0, H, kd, vd, 0};
+        hipLaunchKernelGGL(k_dn_prep, dim3(DN_PREP, gs), dim3(256), 0, st, a, s);
+        hipLaunchKernelGGL(k_dn_dots, dim3(4, 4, gs), dim3(256), 0, st, a, s);
+        hipLaunchKernelGGL(k_dn_solve, dim3(gs), dim3(64), 0, st, a, s);
+        hipLaunchKernelGGL(k_dn_apply, dim3(DN_C / DN_RB, 2, gs), dim3(256), 0, st, a, s);
+        for (int c = 0; c < gc; c++) {
+            a.c = c;
+            const int64_t rest = n_tok - (g0 + c) * DN_C;
+            const int n = (int)(rest < DN_C ? rest : DN_C);
+            hipLaunchKernelGGL(k_dn_state_in, dim3((n + DN_T - 1) / DN_T, (vd + 63) / 64, H), dim3(256), 0, st, a,
+                               s);
+            const int nout = (n * vd + 255) / 256;
+            hipLaunchKernelGGL(k_dn_out_state, dim3(nout + (kd * vd + 255) / 256, H), dim3(256), 0, st, a, s, nout);
+        }
     }
     return hipGetLastError();
 }

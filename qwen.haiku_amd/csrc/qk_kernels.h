@@ -67,8 +67,8 @@ hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k,
                          const int32_t *mask, int32_t n_mask, int32_t *token, void *scratch, hipStream_t s);
 
 // Chunked Gated DeltaNet (qk_deltanet.hip); scratch holds
-// deltanet_scratch_bytes(H, kd, vd); kd, vd <= 128.
-size_t deltanet_scratch_bytes(int32_t H, int32_t kd, int32_t vd);
+// deltanet_scratch_bytes(H, kd, vd, n_tok); kd, vd <= 128.
+size_t deltanet_scratch_bytes(int32_t H, int32_t kd, int32_t vd, int64_t n_tok);
 hipError_t launch_deltanet(const float *q, const float *k, const float *v, const float *g, const float *beta,
                            int64_t n_tok, int32_t H, int32_t kd, int32_t vd, float *state, float *out,
                            void *scratch, hipStream_t s);

@@ -64,6 +64,8 @@
 
 #include "qk.h"
 
+#include <time.h>
+
 /* Device used by the seam (QK_DEVICE in the environment, default 0);
  * initialised on the first matmul. */
 static void qk_seam_init(void) {
@@ -98,6 +100,14 @@ typedef struct {
 static _Thread_local qk_seam_prefetch qk_seam_pf[QK_SEAM_PREFETCH_MAX];
 static _Thread_local int qk_seam_pf_n;
 static _Thread_local long long qk_seam_pf_hits, qk_seam_pf_misses, qk_seam_gpu_calls;
+/* wall time inside the GPU calls of this thread, by kind (seconds) */
+static _Thread_local double qk_seam_matmul_s, qk_seam_deltanet_s;
+
+static double qk_seam_now(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
 
 static void qk_seam_prefetch_clear(void) { qk_seam_pf_n = 0; }
 
@@ -136,7 +146,9 @@ static struct tensor *qk_seam_matmul(int type, const void *w, int64_t out_f, int
     struct tensor *out = tensor_new_2d(x->arena, out_f, n);
     if (qk_seam_prefetched(w, out_f, k, x, out->data)) return out;
     qk_seam_gpu_calls++;
+    const double t = qk_seam_now();
     int rc = hip_qk_matmul_host(w, type, out_f, k, x->data, n, out->data);
+    qk_seam_matmul_s += qk_seam_now() - t;
     if (rc != QK_OK) {
         fprintf(stderr, "qk_seam: matmul type %d (%lld x %lld, %lld tokens) failed (%d): %s\n", type,
                 (long long)out_f, (long long)k, (long long)n, rc, hip_qk_last_error());
@@ -178,7 +190,9 @@ static void chunked_ssm_step_f32(int n, int k_hd, int v_hd, const float *q, cons
     (void)v_prime; (void)v_new; (void)v_attn; (void)key_gdiff; (void)kgd_vnew;
     qk_seam_init();
     qk_seam_gpu_calls++;
+    const double t = qk_seam_now();
     int rc = hip_qk_deltanet_host(n, k_hd, v_hd, q, k_in, v_in, g_log, beta, state, out);
+    qk_seam_deltanet_s += qk_seam_now() - t;
     if (rc != QK_OK) {
         fprintf(stderr, "qk_seam: chunked DeltaNet step (n=%d, %dx%d) failed (%d): %s\n", n, k_hd, v_hd, rc,
                 hip_qk_last_error());

@@ -413,6 +413,11 @@ int main(int argc, char **argv) {
     (void)logits;
     int32_t pos = n_prompt;
     double t1 = e2e_now();
+    double pf_mm = 0.0, pf_dn = 0.0;   /* prefill seconds inside the GPU matmul / DeltaNet calls */
+#if defined(QK_E2E_GPU)
+    pf_mm = qk_seam_matmul_s;
+    pf_dn = qk_seam_deltanet_s;
+#endif
     fprintf(stderr, "[e2e] prefill %.3f s\n", t1 - t0);
 
     /* decode (slm/slm.c:307-358): the first step re-feeds the last prompt token */
@@ -499,7 +504,8 @@ int main(int argc, char **argv) {
     }
     const double nv = (double)cfg.vocab_size;
     printf("{\"mode\": \"%s\", \"source\": \"%s\", \"tier\": \"%s\", \"layers\": %d, \"prompt\": %d, \"gen\": %d, \"seed\": %llu, "
-           "\"prefill_s\": %.6f, \"decode_s\": %.6f, \"prefill_tok_s\": %.3f, \"decode_tok_s\": %.3f, "
+           "\"prefill_s\": %.6f, \"prefill_gpu_matmul_s\": %.6f, \"prefill_gpu_deltanet_s\": %.6f, "
+           "\"decode_s\": %.6f, \"prefill_tok_s\": %.3f, \"decode_tok_s\": %.3f, "
            "\"decode_path\": \"%s\", \"sampler\": \"%s\", \"host_syncs_per_token\": %.2f, \"prefetch_hits\": %.0f, \"prefetch_misses\": %.0f, "
            "\"distinct_tokens\": %d, \"nonfinite_logits\": %lld, \"last_logits\": {\"min\": %.6g, \"max\": %.6g, "
            "\"mean\": %.6g, \"std\": %.6g}, \"tokens\": [",
@@ -508,7 +514,7 @@ int main(int argc, char **argv) {
 #else
            "cpu",
 #endif
-           load_path ? "gguf" : "built", simd_dispatch_label(), n_layers, n_prompt, n_gen, (unsigned long long)seed, t1 - t0, t2 - td,
+           load_path ? "gguf" : "built", simd_dispatch_label(), n_layers, n_prompt, n_gen, (unsigned long long)seed, t1 - t0, pf_mm, pf_dn, t2 - td,
            n_prompt / (t1 - t0), n_gen / (t2 - td),
 #if defined(QK_E2E_GPU)
            chain ? "gpu-chain" : "gpu-seam",
