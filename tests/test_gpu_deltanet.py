@@ -60,6 +60,21 @@ def test_deltanet_layer(lib, orc, n_tok):
     assert_bits_equal(host(dst), want_s, "state")
 
 
+@pytest.mark.parametrize("H,dim,n_tok", [(64, 32, 300), (300, 16, 130), (16, 128, 1100)])
+def test_deltanet_chunk_groups(lib, orc, H, dim, n_tok):
+    """Calls whose chunks span several groups of the state-free phases
+    (at most 256 (chunk, head) slots per group): 64 heads run 5 chunks as
+    4 + 1, 300 heads one chunk per group, 16 heads 18 chunks as 16 + 2."""
+    step(f"deltanet chunk groups H={H} dim={dim} n_tok={n_tok}")
+    q, k, v, g, b = ssm_inputs(n_tok, H=H, kd=dim, vd=dim, seed=H + n_tok)
+    st = state0(H, dim, dim, H)
+    want_o, want_s = orc.deltanet_chunked(q, k, v, g, b, st)
+    dst = dev(st)
+    out = lib.deltanet_chunked(dev(q), dev(k), dev(v), dev(g), dev(b), dst)
+    assert_bits_equal(host(out), want_o, "out")
+    assert_bits_equal(host(dst), want_s, "state")
+
+
 def test_deltanet_other_head_dims(lib, orc):
     step("deltanet kd=64 vd=96 heads=3")
     q, k, v, g, b = ssm_inputs(100, H=3, kd=64, vd=96, seed=5)
