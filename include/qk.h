@@ -380,6 +380,19 @@ int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f,
 int hip_qk_deltanet_host(int n, int k_hd, int v_hd, const float *q,
                          const float *k, const float *v, const float *g_log,
                          const float *beta, float *state, float *out);
+/* The chunk loop of slm_forward_ssm_batch over one layer
+ * (slm/qwen.c:772-807) from host buffers, synchronous: what
+ * hip_deltanet_chunked computes, on the reference's own arrays. q, k:
+ * Q_all, K_all [n_tok][n_heads][k_hd]; v: V_all [n_tok][n_heads][v_hd];
+ * g_log, beta: g_log_all, beta_all [n_tok][n_heads]; state: the layer's
+ * state_base [n_heads][k_hd][v_hd], updated in place; out: out_flat
+ * [n_tok][n_heads][v_hd]. All staged at once: at most
+ * QK_DELTANET_HOST_MAX_BYTES of them per call. */
+#define QK_DELTANET_HOST_MAX_BYTES (4.0 * 1024 * 1024 * 1024)
+int hip_qk_deltanet_layer_host(int64_t n_tok, int n_heads, int k_hd,
+                               int v_hd, const float *q, const float *k,
+                               const float *v, const float *g_log,
+                               const float *beta, float *state, float *out);
 /* LM head: matmul_dispatch(&W.output, h) (slm/qwen.c:976) followed by
  * sample_argmax (slm/model.c:401). logits (n floats) may be NULL when
  * only the token is needed; topk may be 0. Host pointers. */

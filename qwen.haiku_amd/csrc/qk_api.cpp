@@ -580,6 +580,43 @@ int stream_scratch(hipStream_t stream, size_t need, void **out) {
     return QK_OK;
 }
 
+// Host buffers in and out: q | k | v | g | beta | state staged in this
+// thread's pinned buffer, one copy each way, the launch on its stream,
+// synchronous. State and out come back in one copy (they are adjacent on
+// the device).
+int deltanet_host(int64_t n_tok, int H, int k_hd, int v_hd, const float *q, const float *k, const float *v,
+                  const float *g_log, const float *beta, float *state, float *out) {
+    int rc;
+    Lane *l = nullptr;
+    if ((rc = my_lane(&l))) return rc;
+    const size_t nq = (size_t)n_tok * H * k_hd, nv = (size_t)n_tok * H * v_hd, ng = (size_t)n_tok * H;
+    const size_t ns = (size_t)H * k_hd * v_hd;
+    const size_t in_floats = 2 * nq + nv + 2 * ng + ns;
+    const size_t all = (in_floats + nv) * sizeof(float);
+    if ((rc = grow(&l->dx, &l->dx_cap, all)) || (rc = grow_host(&l->hx, &l->hx_cap, all))) return rc;
+    float *h = static_cast<float *>(l->hx);
+    std::memcpy(h, q, nq * 4);
+    std::memcpy(h + nq, k, nq * 4);
+    std::memcpy(h + 2 * nq, v, nv * 4);
+    std::memcpy(h + 2 * nq + nv, g_log, ng * 4);
+    std::memcpy(h + 2 * nq + nv + ng, beta, ng * 4);
+    std::memcpy(h + 2 * nq + nv + 2 * ng, state, ns * 4);
+    float *d = static_cast<float *>(l->dx);
+    HIP_OK(hipMemcpyAsync(d, h, in_floats * 4, hipMemcpyHostToDevice, l->stream), "hipMemcpyAsync(deltanet in)");
+    void *scratch = nullptr;
+    if ((rc = stream_scratch(l->stream, qk::deltanet_scratch_bytes(H, k_hd, v_hd, n_tok), &scratch))) return rc;
+    float *dstate = d + 2 * nq + nv + 2 * ng, *dout = d + in_floats;
+    HIP_OK(qk::launch_deltanet(d, d + nq, d + 2 * nq, d + 2 * nq + nv, d + 2 * nq + nv + ng, n_tok, H, k_hd, v_hd,
+                               dstate, dout, scratch, l->stream),
+           "deltanet launch");
+    HIP_OK(hipMemcpyAsync(h + 2 * nq + nv + 2 * ng, dstate, (ns + nv) * 4, hipMemcpyDeviceToHost, l->stream),
+           "hipMemcpyAsync(deltanet out)");
+    HIP_OK(hipStreamSynchronize(l->stream), "hipStreamSynchronize");
+    std::memcpy(state, h + 2 * nq + nv + 2 * ng, ns * 4);
+    std::memcpy(out, h + in_floats, nv * 4);
+    return QK_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -907,34 +944,24 @@ int hip_qk_deltanet_host(int n, int k_hd, int v_hd, const float *q, const float 
     if (n < 1 || n > 64 || k_hd < 1 || v_hd < 1 || k_hd > QK_DELTANET_MAX_HD || v_hd > QK_DELTANET_MAX_HD)
         return fail(QK_ERR_ARG, "bad chunk n=%d k_hd=%d v_hd=%d (n 1..64, head dims 1..%d)", n, k_hd, v_hd,
                     QK_DELTANET_MAX_HD);
-    Lane *l = nullptr;
-    if ((rc = my_lane(&l))) return rc;
-    // one buffer: q | k | v | g | beta | state, then out
-    const size_t nq = (size_t)n * k_hd, nv = (size_t)n * v_hd, ns = (size_t)k_hd * v_hd;
-    const size_t in_floats = 2 * nq + nv + 2 * (size_t)n + ns;
-    const size_t all = (in_floats + nv) * sizeof(float);
-    if ((rc = grow(&l->dx, &l->dx_cap, all)) || (rc = grow_host(&l->hx, &l->hx_cap, all))) return rc;
-    float *h = static_cast<float *>(l->hx);
-    std::memcpy(h, q, nq * 4);
-    std::memcpy(h + nq, k, nq * 4);
-    std::memcpy(h + 2 * nq, v, nv * 4);
-    std::memcpy(h + 2 * nq + nv, g_log, (size_t)n * 4);
-    std::memcpy(h + 2 * nq + nv + n, beta, (size_t)n * 4);
-    std::memcpy(h + 2 * nq + nv + 2 * n, state, ns * 4);
-    float *d = static_cast<float *>(l->dx);
-    HIP_OK(hipMemcpyAsync(d, h, in_floats * 4, hipMemcpyHostToDevice, l->stream), "hipMemcpyAsync(chunk in)");
-    void *scratch = nullptr;
-    if ((rc = stream_scratch(l->stream, qk::deltanet_scratch_bytes(1, k_hd, v_hd, n), &scratch))) return rc;
-    float *dstate = d + 2 * nq + nv + 2 * n, *dout = d + in_floats;
-    HIP_OK(qk::launch_deltanet(d, d + nq, d + 2 * nq, d + 2 * nq + nv, d + 2 * nq + nv + n, n, 1, k_hd, v_hd, dstate,
-                               dout, scratch, l->stream),
-           "deltanet launch");
-    HIP_OK(hipMemcpyAsync(h + 2 * nq + nv + 2 * n, dstate, (ns + nv) * 4, hipMemcpyDeviceToHost, l->stream),
-           "hipMemcpyAsync(chunk out)");
-    HIP_OK(hipStreamSynchronize(l->stream), "hipStreamSynchronize");
-    std::memcpy(state, h + 2 * nq + nv + 2 * n, ns * 4);
-    std::memcpy(out, h + in_floats, nv * 4);
-    return QK_OK;
+    return deltanet_host(n, 1, k_hd, v_hd, q, k, v, g_log, beta, state, out);
+}
+
+int hip_qk_deltanet_layer_host(int64_t n_tok, int n_heads, int k_hd, int v_hd, const float *q, const float *k,
+                               const float *v, const float *g_log, const float *beta, float *state, float *out) {
+    int rc = require_init();
+    if (rc) return rc;
+    if (!q || !k || !v || !g_log || !beta || !state || !out) return fail(QK_ERR_ARG, "null pointer");
+    if (n_tok < 1 || n_tok > 0x7fffffffLL || n_heads < 1 || n_heads > 1024 || k_hd < 1 || v_hd < 1 ||
+        k_hd > QK_DELTANET_MAX_HD || v_hd > QK_DELTANET_MAX_HD)
+        return fail(QK_ERR_ARG, "bad shape n_tok=%lld heads=%d k_hd=%d v_hd=%d (head dims 1..%d)", (long long)n_tok,
+                    n_heads, k_hd, v_hd, QK_DELTANET_MAX_HD);
+    // q, k, v, g, beta, state and out staged at once
+    const double bytes = 4.0 * (double)n_tok * n_heads * (2.0 * k_hd + 2.0 * v_hd + 2.0) +
+                         4.0 * (double)n_heads * k_hd * v_hd;
+    if (bytes > QK_DELTANET_HOST_MAX_BYTES)
+        return fail(QK_ERR_ARG, "layer of %.0f bytes exceeds QK_DELTANET_HOST_MAX_BYTES; split the tokens", bytes);
+    return deltanet_host(n_tok, n_heads, k_hd, v_hd, q, k, v, g_log, beta, state, out);
 }
 
 }  // extern "C"

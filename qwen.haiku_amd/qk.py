@@ -108,6 +108,7 @@ class QK:
         L.hip_sample.argtypes = [_vp, _i64, C.POINTER(Sampler), _vp, _vp, C.c_int32, _vp, C.c_int32, _vp, _vp]
         L.hip_deltanet_chunked.argtypes = [_vp] * 5 + [_i64, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp]
         L.hip_qk_deltanet_host.argtypes = [C.c_int, C.c_int, C.c_int] + [_vp] * 7
+        L.hip_qk_deltanet_layer_host.argtypes = [C.c_int64, C.c_int, C.c_int, C.c_int] + [_vp] * 7
         L.hip_qk_register_weight.argtypes = [_vp, C.c_int, _i64, _i64]
         L.hip_qk_unregister_weight.argtypes = [_vp]
         L.hip_qk_device_weight.argtypes = [_vp]
@@ -314,6 +315,20 @@ class QK:
         arrs = [np.ascontiguousarray(a, np.float32) for a in (k, v, g, beta)]
         self._ck(self.L.hip_qk_deltanet_host(n, kd, vd, q.ctypes.data_as(_vp), *[a.ctypes.data_as(_vp) for a in arrs],
                                              st.ctypes.data_as(_vp), out.ctypes.data_as(_vp)))
+        return out, st
+
+    def deltanet_layer_host(self, q, k, v, g, beta, state):
+        """One layer, numpy in and out (q, k [n][H][kd], v [n][H][vd], g,
+        beta [n][H], state [H][kd][vd]): returns (out, new state)."""
+        q = np.ascontiguousarray(q, np.float32)
+        n, H, kd = q.shape
+        vd = v.shape[2]
+        st = np.array(state, np.float32, copy=True)
+        out = np.empty((n, H, vd), np.float32)
+        arrs = [np.ascontiguousarray(a, np.float32) for a in (k, v, g, beta)]
+        self._ck(self.L.hip_qk_deltanet_layer_host(n, H, kd, vd, q.ctypes.data_as(_vp),
+                                                   *[a.ctypes.data_as(_vp) for a in arrs],
+                                                   st.ctypes.data_as(_vp), out.ctypes.data_as(_vp)))
         return out, st
 
     # -- host seam --------------------------------------------------------------

@@ -75,6 +75,19 @@ def test_deltanet_chunk_groups(lib, orc, H, dim, n_tok):
     assert_bits_equal(host(dst), want_s, "state")
 
 
+@pytest.mark.parametrize("n_tok", [1, 200])
+def test_deltanet_layer_host(lib, orc, n_tok):
+    """hip_qk_deltanet_layer_host: the layer from host buffers laid out as
+    slm_forward_ssm_batch holds them."""
+    step(f"deltanet layer host n_tok={n_tok}")
+    q, k, v, g, b = ssm_inputs(n_tok, H=16, seed=n_tok + 3, zero_rows=n_tok > 3)
+    st = state0(16, 128, 128, n_tok + 3)
+    want_o, want_s = orc.deltanet_chunked(q, k, v, g, b, st)
+    out, new_st = lib.deltanet_layer_host(q, k, v, g, b, st)
+    assert_bits_equal(out, want_o, "out")
+    assert_bits_equal(new_st, want_s, "state")
+
+
 def test_deltanet_other_head_dims(lib, orc):
     step("deltanet kd=64 vd=96 heads=3")
     q, k, v, g, b = ssm_inputs(100, H=3, kd=64, vd=96, seed=5)
@@ -111,3 +124,6 @@ def test_deltanet_rejects_bad_shapes(lib):
     with pytest.raises(qk.QKError):                    # a chunk holds at most 64 tokens
         lib.deltanet_host(np.zeros((65, 128)), np.zeros((65, 128)), np.zeros((65, 128)), np.zeros(65),
                           np.zeros(65), np.zeros((128, 128)))
+    with pytest.raises(qk.QKError):                    # head dim past QK_DELTANET_MAX_HD, host layer
+        lib.deltanet_layer_host(np.zeros((4, 2, 129)), np.zeros((4, 2, 129)), np.zeros((4, 2, 128)),
+                                np.zeros((4, 2)), np.zeros((4, 2)), np.zeros((2, 129, 128)))
