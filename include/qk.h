@@ -225,7 +225,7 @@ int hip_dequant_q6k(const void *w, int64_t nblocks, float *y, void *stream);
  * h_out (may be NULL, may equal h) receives r, x_out (may be NULL) x,
  * xq (may be NULL, needs k % 256 == 0) the Q8_K row for the next GEMV;
  * one of x_out / xq is required. w holds k floats shared by every row.
- * k is a multiple of 4, at most QK_NORM_MAX_K. Bit-exact. Device
+ * k is a multiple of 4, at most QK_NORM_MAX_K; m at most 2^24. Bit-exact. Device
  * pointers; float rows 16-byte aligned. The decode chain between two
  * matmuls: slm/qwen.c:936-948 (h = h + mix; ffn_norm) and the norm that
  * opens each layer's mixer (slm/qwen.c:332-334). */
@@ -242,7 +242,8 @@ int hip_silu_f32(const float *x, int64_t n, float *y, void *stream);
 /* The FFN's SwiGLU link (slm/qwen.c:949-954): act = silu(gate) * up over
  * m rows of k floats (simd_silu_f32 then tensor_mul, slm/tensor.c:293),
  * written to act (may be NULL) and/or quantized to Q8_K rows in xq (may
- * be NULL, needs k % 256 == 0) for the down projection. Bit-exact. */
+ * be NULL, needs k % 256 == 0) for the down projection; m*k at most
+ * 2^33. Bit-exact. */
 int hip_swiglu_q8k(const float *gate, const float *up, int64_t m, int64_t k,
                    float *act, void *xq, void *stream);
 

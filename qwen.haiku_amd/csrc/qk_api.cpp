@@ -477,9 +477,9 @@ int hip_add_rmsnorm_q8k(const float *h, const float *delta, const float *w, floa
     if (rc) return rc;
     if (!h || !w) return fail(QK_ERR_ARG, "null pointer");
     if (!x_out && !xq) return fail(QK_ERR_ARG, "x_out and xq are both NULL");
-    if (m < 1 || m > 0x7fffffffLL || k < 4 || k % 4 || k > QK_NORM_MAX_K)
-        return fail(QK_ERR_ARG, "bad shape m=%lld k=%lld (k a multiple of 4, at most %d)", (long long)m,
-                    (long long)k, QK_NORM_MAX_K);
+    if (m < 1 || m > ((int64_t)1 << 24) || k < 4 || k % 4 || k > QK_NORM_MAX_K)   // one workgroup per row
+        return fail(QK_ERR_ARG, "bad shape m=%lld k=%lld (m at most 2^24, k a multiple of 4, at most %d)",
+                    (long long)m, (long long)k, QK_NORM_MAX_K);
     if (xq && k % QK_K) return fail(QK_ERR_ARG, "k=%lld: a Q8_K row needs a multiple of 256", (long long)k);
     if (!aligned(h, 16) || !aligned(delta, 16) || !aligned(w, 16) || !aligned(h_out, 16) || !aligned(x_out, 16) ||
         !aligned(xq, 4))
@@ -505,8 +505,9 @@ int hip_swiglu_q8k(const float *gate, const float *up, int64_t m, int64_t k, flo
     if (rc) return rc;
     if (!gate || !up) return fail(QK_ERR_ARG, "null pointer");
     if (!act && !xq) return fail(QK_ERR_ARG, "act and xq are both NULL");
-    if (m < 1 || k < 4 || k % 4 || m > ((int64_t)1 << 40) / k)
-        return fail(QK_ERR_ARG, "bad shape m=%lld k=%lld (k a multiple of 4)", (long long)m, (long long)k);
+    if (m < 1 || k < 4 || k % 4 || m > ((int64_t)1 << 33) / k)    // one wave per 256 elements
+        return fail(QK_ERR_ARG, "bad shape m=%lld k=%lld (k a multiple of 4, m*k at most 2^33)", (long long)m,
+                    (long long)k);
     if (xq && k % QK_K) return fail(QK_ERR_ARG, "k=%lld: a Q8_K row needs a multiple of 256", (long long)k);
     if (!aligned(gate, 16) || !aligned(up, 16) || !aligned(act, 16) || !aligned(xq, 4))
         return fail(QK_ERR_ARG, "float rows must be 16-byte and xq 4-byte aligned");

@@ -76,6 +76,24 @@ __device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
 // thread owning a token's first occurrence applies its count in turn.
 constexpr int SMP_HIST_LDS = 4096;                    // window entries staged in LDS
 
+// Window entry i of h[0..w): the owner of its token's first occurrence
+// applies the token's count of repeats in turn.
+__device__ __forceinline__ void penalty_entry(float *logits, int64_t n, const int32_t *h, int32_t w, int32_t i,
+                                              float penalty) {
+    const int32_t t = h[i];
+    if (t < 0 || t >= n) return;
+    bool first = true;
+    for (int32_t j = 0; j < i && first; j++) first = h[j] != t;
+    if (!first) return;
+    int32_t reps = 1;
+    for (int32_t j = i + 1; j < w; j++) reps += h[j] == t;
+    float v = logits[t];
+    for (int32_t r = 0; r < reps; r++) v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
+    logits[t] = v;
+}
+
+// One workgroup: the masks, then (windows of at most SMP_HIST_LDS ids,
+// staged in LDS) the penalty.
 __global__ __launch_bounds__(256) void k_smp_penalty(float *logits, int64_t n, const int32_t *history,
                                                      int32_t start, int32_t hist_n, float penalty, int32_t m0,
                                                      int32_t m1, int32_t n_mask) {
@@ -85,24 +103,19 @@ __global__ __launch_bounds__(256) void k_smp_penalty(float *logits, int64_t n, c
         if (t >= 0 && t < n) logits[t] = -__builtin_inff();
     }
     const int32_t w = hist_n - start;
-    const bool staged = w <= SMP_HIST_LDS;
-    if (staged)
-        for (int32_t i = threadIdx.x; i < w; i += 256) hw[i] = history[start + i];
+    if (w > SMP_HIST_LDS) return;                      // k_smp_penalty_wide takes it
+    for (int32_t i = threadIdx.x; i < w; i += 256) hw[i] = history[start + i];
     __syncthreads();
-    if (penalty == 1.0f || hist_n == 0) return;
-    const int32_t *h = staged ? hw : history + start;
-    for (int32_t i = threadIdx.x; i < w; i += 256) {
-        const int32_t t = h[i];
-        if (t < 0 || t >= n) continue;
-        bool first = true;
-        for (int32_t j = 0; j < i && first; j++) first = h[j] != t;
-        if (!first) continue;
-        int32_t reps = 1;
-        for (int32_t j = i + 1; j < w; j++) reps += h[j] == t;
-        float v = logits[t];
-        for (int32_t r = 0; r < reps; r++) v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
-        logits[t] = v;
-    }
+    if (penalty == 1.0f || w == 0) return;
+    for (int32_t i = threadIdx.x; i < w; i += 256) penalty_entry(logits, n, hw, w, i, penalty);
+}
+
+// Windows longer than SMP_HIST_LDS: one thread per entry over as many
+// workgroups as the window needs, after k_smp_penalty has set the masks.
+__global__ __launch_bounds__(256) void k_smp_penalty_wide(float *logits, int64_t n, const int32_t *history,
+                                                          int32_t w, float penalty) {
+    const int32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < w) penalty_entry(logits, n, history, w, i, penalty);
 }
 
 // ---- greedy: sample_argmax (slm/model.c:401-412) ---------------------------
@@ -697,6 +710,10 @@ hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k,
     const int32_t start = (window > 0 && window < hist_n) ? hist_n - window : 0;
     hipLaunchKernelGGL(k_smp_penalty, dim3(1), dim3(256), 0, s, logits, n, history, start, hist_n, penalty,
                        n_mask > 0 ? mask[0] : -1, n_mask > 1 ? mask[1] : -1, n_mask);
+    const int32_t w = hist_n - start;
+    if (w > SMP_HIST_LDS && penalty != 1.0f)
+        hipLaunchKernelGGL(k_smp_penalty_wide, dim3((unsigned)((w + 255) / 256)), dim3(256), 0, s, logits, n,
+                           history + start, w, penalty);
     const int32_t sb = sample_block(n, k);
     const int32_t nblk = (int32_t)((n + sb - 1) / sb);
     if (nblk > SMP_KMAX || sb > 4096) return hipErrorInvalidValue;   // the caller's n limit keeps both

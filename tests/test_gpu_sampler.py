@@ -51,6 +51,27 @@ def test_sample_matches_oracle(lib, orc, n):
             check(lib, orc, logits, sp, st, hist, mask, f"n={n} row={li} sampler={si}")
 
 
+@pytest.mark.parametrize("window", [0, 5000, 4096, 64])
+def test_sample_long_history_windows(lib, orc, window):
+    """Windows past the 4096 ids the penalty stages in LDS run over many
+    workgroups after the masks: a 12000-id history full of repeats and
+    out-of-range ids, masks that are also in the history, and penalties
+    that compound (1.3), shrink (0.7) and zero (0: -inf * 0 is NaN, so the
+    mask has to land before the penalty)."""
+    step(f"sample long history window={window}")
+    n = 9000
+    rng = np.random.default_rng(window + 1)
+    hist = rng.integers(-3, n + 3, 12000).astype(np.int32)
+    hist[::7] = 17                                     # one token repeated about 1700 times
+    for pen in (1.3, 0.7, 0.0):
+        sp = dict(temperature=0.8, top_k=40, top_p=0.9, min_p=0.05, repetition_penalty=pen,
+                  repetition_window=window)
+        logits = (rng.standard_normal(n) * 2).astype(np.float32)
+        logits[17] = 0.5
+        check(lib, orc, logits, sp, orc.rng_seed(window + 3), hist, np.array([17, int(hist[5]) % n], np.int32),
+              f"window={window} penalty={pen}")
+
+
 def test_sample_vocab_sequence_on_device(lib, orc):
     """64 steps at vocabulary 248320 with the default sampler: logits from
     a random walk (so later steps see repeated tokens in the window), the
