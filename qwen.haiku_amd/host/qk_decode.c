@@ -48,6 +48,7 @@ typedef struct {
 typedef struct {
     hipStream_t s;
     int64_t hidden, ffn, vocab;
+    int32_t n_layers;
     float eps;
     float *h, *mix, *xn, *gate, *up, *act, *ffn_out, *logits;   /* device */
     void *xq, *aq;                                              /* device Q8_K rows */
@@ -118,6 +119,7 @@ static void qk_dec_init(qk_dec *D, const struct slm_model *m) {
     D->hidden = cfg->hidden_dim;
     D->ffn = cfg->ffn_dim;
     D->vocab = cfg->vocab_size;
+    D->n_layers = cfg->n_layers;
     D->eps = cfg->norm_eps;
     if (m->W.output.type != GGUF_TT_Q6_K || m->W.tok_embd.type != GGUF_TT_Q6_K || D->hidden % QK_K ||
         D->ffn % QK_K) {
@@ -165,6 +167,32 @@ static void qk_dec_init(qk_dec *D, const struct slm_model *m) {
     }
     D->out_norm = qk_dec_vec(&m->W.output_norm, D->hidden);
     qk_dec_weight(&m->W.output);
+}
+
+/* Everything qk_dec_init and qk_dec_sampling allocated; the weights stay
+ * with the seam's registry. */
+static void qk_dec_free(qk_dec *D) {
+    if (!D->s) return;
+    qk_dec_ck(hipStreamSynchronize(D->s), "hipStreamSynchronize");
+    void *dev[] = {D->h, D->mix, D->xn, D->gate, D->up, D->act, D->ffn_out, D->logits, D->xq, D->aq, D->am,
+                   D->out_norm, D->rng, D->hist};
+    for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
+        if (dev[i]) qk_dec_ck(hipFree(dev[i]), "hipFree");
+    void *pin[] = {D->h_host, D->xn_host, D->mix_host, D->am_host};
+    for (size_t i = 0; i < sizeof(pin) / sizeof(pin[0]); i++)
+        if (pin[i]) qk_dec_ck(hipHostFree(pin[i]), "hipHostFree");
+    for (int i = 0; i < QK_DEC_MAX_PROJ; i++) {
+        if (D->proj[i].y_dev) qk_dec_ck(hipFree(D->proj[i].y_dev), "hipFree");
+        if (D->proj[i].y_host) qk_dec_ck(hipHostFree(D->proj[i].y_host), "hipHostFree");
+    }
+    for (int32_t L = 0; D->attn_norm && D->ffn_norm && L < D->n_layers; L++) {
+        qk_dec_ck(hipFree(D->attn_norm[L]), "hipFree");
+        qk_dec_ck(hipFree(D->ffn_norm[L]), "hipFree");
+    }
+    free(D->attn_norm);
+    free(D->ffn_norm);
+    qk_dec_ck(hipStreamDestroy(D->s), "hipStreamDestroy");
+    memset(D, 0, sizeof(*D));
 }
 
 /* Sampled decoding from the reference's rng state and a history holding

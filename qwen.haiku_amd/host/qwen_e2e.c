@@ -526,6 +526,9 @@ int main(int argc, char **argv) {
     for (int32_t i = 0; i < n_gen; i++) printf("%s%d", i ? ", " : "", toks[i]);
     printf("]}\n");
     fflush(stdout);
+#if defined(QK_E2E_GPU)
+    if (chain) qk_dec_free(&D);
+#endif
     slm_ctx_destroy(c);
     return nonfinite ? 1 : 0;
 }
