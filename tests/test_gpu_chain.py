@@ -78,6 +78,41 @@ def test_add_rmsnorm_in_place_and_partial_outputs(lib, orc):
         assert_bits_equal(host(hd), want_r, f"in-place h m={m} k={k}")
 
 
+def norm_block_rows(k, rng):
+    """Rows for the norm's block walk (64 squares per block, added in one
+    step when every add of the block is exact, else one by one): blocks
+    at scales that change by up to 2^40 from block to block (exact and
+    rounding blocks in one row), powers of two (squares with one set bit),
+    a lone huge value followed by tiny ones (the tiny squares round away),
+    and the row whose sequential sum differs from its exact and pairwise
+    sums."""
+    rows = []
+    for _ in range(6):
+        scale = np.repeat(np.exp2(rng.integers(-20, 21, (k + 63) // 64)), 64)[:k]
+        rows.append(rng.standard_normal(k) * scale)
+    rows.append(np.exp2(rng.integers(-40, 20, k)).astype(np.float64) * rng.choice([-1, 1], k))
+    tiny = rng.standard_normal(k) * 2.0 ** -20
+    tiny[k // 3] = 3.0e4
+    rows.append(tiny)
+    rows.append(rng.uniform(-1, 1, k))
+    disc = np.full(k, np.float32(2.0 ** -13))
+    disc[0] = np.array([0x46800DDC], np.uint32).view(np.float32)[0]
+    disc[min(1, k - 1)] = 4.0
+    rows.append(disc)
+    return np.asarray(rows, np.float32)
+
+
+@pytest.mark.parametrize("k", [4, 100, 256, 1000, 1024, 3584, 16384])
+def test_add_rmsnorm_block_paths(lib, orc, k):
+    step(f"add_rmsnorm block paths k={k}")
+    rng = np.random.default_rng(k + 5)
+    h = norm_block_rows(k, rng)
+    w = (1 + 0.02 * rng.standard_normal(k)).astype(np.float32)
+    xo = empty(h.shape)
+    lib.add_rmsnorm_q8k(dev(h), None, dev(w), 1e-6, x_out=xo)
+    assert_bits_equal(host(xo), orc.add_rmsnorm(h, None, w, 1e-6)[1], f"block paths k={k}")
+
+
 def test_add_rmsnorm_many_scales(lib, orc):
     """4096 constant rows spanning 60 binades: as many distinct
     rscale = 1/sqrtf(mean + eps) values, each correctly rounded."""
