@@ -359,6 +359,108 @@ __global__ __launch_bounds__(256) void k_smp_events(const float *logits, int64_t
     }
 }
 
+// ---- the final slots without a replay -------------------------------------------
+// When the k fill values and the entering events are all distinct, the
+// replay has a closed form. Each event evicts the smallest slot value,
+// and what enters is larger than what leaves, so the evicted values come
+// out strictly increasing: the j-th event (in index order) evicts the
+// element of rank j among all N = k + events elements (the N - k
+// smallest are exactly the evicted ones, the k largest the survivors).
+// That element sits in its own fill slot, or in the slot of the earlier
+// event that brought it in, so every event's slot is found by pointer
+// jumping over "evicts the element of rank j". One workgroup ranks the
+// elements (keys in LDS), resolves the chains and writes each survivor
+// into its slot; k_smp_finish then skips its replay. Ties (equal keys,
+// -0 and +0 included), a NaN in the fill or more than SMP_NMAX elements
+// leave *ok = 0 and the replay runs.
+constexpr int SMP_NMAX = 3584;
+
+__global__ __launch_bounds__(1024) void k_smp_slots(const float *logits, int64_t n, int32_t k, int32_t sb,
+                                                    int32_t nblk, const int32_t *ev_idx, const float *ev_val,
+                                                    const int32_t *ev_n, const int32_t *nan_flag, float *res_val,
+                                                    int32_t *res_idx, int32_t *ok) {
+    __shared__ uint32_t key[SMP_NMAX];                 // elements: the fill, then the events in index order
+    __shared__ float ev[SMP_NMAX];
+    __shared__ int32_t eid[SMP_NMAX];                  // logit index of each element
+    __shared__ int32_t byr[SMP_NMAX];                  // element of each rank, then resolved slots
+    __shared__ int32_t off[SMP_KMAX + 1];
+    __shared__ int32_t skip;
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        int32_t acc = 0, nf = 0;
+        for (int32_t b = 0; b < nblk; b++) {
+            off[b] = acc;
+            acc += ev_n[b];
+            nf |= nan_flag[b];
+        }
+        off[nblk] = acc;
+        skip = nf != 0 || n <= k || acc == 0 || k + acc > SMP_NMAX;
+        if (skip) *ok = 0;
+    }
+    __syncthreads();
+    if (skip) return;                                  // uniform
+    const int32_t total = off[nblk], N = k + total;
+    for (int32_t e = tid; e < N; e += 1024) {
+        float v;
+        int32_t id;
+        if (e < k) {
+            v = logits[e];
+            id = e;
+        } else {
+            const int32_t j = e - k;
+            int32_t lo = 0, hi = nblk;                 // last block with off[block] <= j
+            while (hi - lo > 1) {
+                const int32_t mid = (lo + hi) >> 1;
+                if (off[mid] <= j) lo = mid;
+                else hi = mid;
+            }
+            const int64_t at = (int64_t)lo * sb + (j - off[lo]);
+            v = ev_val[at];
+            id = ev_idx[at];
+        }
+        ev[e] = v;
+        eid[e] = id;
+        key[e] = fkey(v);
+    }
+    __syncthreads();
+    int tie = 0;
+    for (int32_t e = tid; e < N; e += 1024) {
+        const uint32_t ke = key[e];
+        int32_t r = 0, eq = 0;
+        int32_t f = 0;
+        for (; f + 4 <= N; f += 4) {
+            const uint4 q = *reinterpret_cast<const uint4 *>(&key[f]);
+            r += (q.x < ke) + (q.y < ke) + (q.z < ke) + (q.w < ke);
+            eq += (q.x == ke) + (q.y == ke) + (q.z == ke) + (q.w == ke);
+        }
+        for (; f < N; f++) {
+            r += key[f] < ke;
+            eq += key[f] == ke;
+        }
+        tie |= eq > 1;
+        byr[r < N ? r : N - 1] = e;
+    }
+    if (__syncthreads_or(tie)) {
+        if (tid == 0) *ok = 0;
+        return;
+    }
+    // event j evicts element byr[j]: a fill slot, or event byr[j] - k's slot
+    for (int32_t len = 1; len < 2 * total; len <<= 1) {
+        for (int32_t j = tid; j < total; j += 1024) {
+            const int32_t p = byr[j];
+            if (p >= k) byr[j] = byr[p - k];
+        }
+        __syncthreads();
+    }
+    for (int32_t r = total + tid; r < N; r += 1024) {    // the survivors into their slots
+        const int32_t e = byr[r];
+        const int32_t slot = e < k ? e : byr[e - k];
+        res_val[slot] = ev[e];
+        res_idx[slot] = eid[e];
+    }
+    if (tid == 0) *ok = 1;
+}
+
 // One wave: the k slots (LDS), the replay of the events, then the rest of
 // sample_with on lane 0.
 struct SmpArgs {
@@ -486,7 +588,8 @@ __device__ void chain_literal(float *val, int32_t *idx, int32_t filled, const Sm
 
 __global__ __launch_bounds__(64) void k_smp_finish(const float *logits, int64_t n, SmpArgs a, const int32_t *ev_idx,
                                                    const float *ev_val, const int32_t *ev_n, const int32_t *nan_flag,
-                                                   uint64_t *rng, int32_t *token) {
+                                                   const float *res_val, const int32_t *res_idx,
+                                                   const int32_t *res_ok, uint64_t *rng, int32_t *token) {
     __shared__ float val[SMP_KMAX];
     __shared__ int32_t idx[SMP_KMAX];
     __shared__ int32_t off[SMP_KMAX + 1];              // event offsets per block (nblk <= 256)
@@ -521,14 +624,15 @@ __global__ __launch_bounds__(64) void k_smp_finish(const float *logits, int64_t 
     if (lane == 0) off[nblk] = total;
     float sv[SMP_Q];
     int32_t sx[SMP_Q];
+    const bool resolved = *res_ok != 0;                // k_smp_slots placed the survivors
 #pragma unroll
     for (int q = 0; q < SMP_Q; q++) {
         const int32_t s_ = q * 64 + lane;
-        sv[q] = s_ < filled ? logits[s_] : 0.0f;
-        sx[q] = s_;
+        sv[q] = s_ < filled ? (resolved ? res_val[s_] : logits[s_]) : 0.0f;
+        sx[q] = resolved && s_ < filled ? res_idx[s_] : s_;
     }
     __syncthreads();
-    if (!nan_in_fill && n > k && total > 0) {
+    if (!resolved && !nan_in_fill && n > k && total > 0) {
         float mv;
         int32_t ms;
         slot_min(sv, k, mv, ms);
@@ -701,7 +805,8 @@ size_t sample_scratch_bytes(int64_t n, int32_t k) {
     return (size_t)nblk * sb * 8                       // event indices and values
            + (size_t)nblk * (size_t)k * 4              // per-block top-k lists
            + (size_t)nblk * 4 * 2                      // event counts, NaN flags
-           + (size_t)((n + SMP_BLOCK - 1) / SMP_BLOCK) * sizeof(ArgPart) + 256;   // greedy partials
+           + (size_t)((n + SMP_BLOCK - 1) / SMP_BLOCK) * sizeof(ArgPart) + 256    // greedy partials
+           + (size_t)SMP_KMAX * 8 + 16;                // resolved slots and their flag
 }
 
 hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k, float top_p, float min_p,
@@ -729,6 +834,10 @@ hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k,
     int32_t *nan_flag = reinterpret_cast<int32_t *>(p);
     p += (size_t)nblk * 4;
     ArgPart *part = reinterpret_cast<ArgPart *>((reinterpret_cast<uintptr_t>(p) + 15) & ~(uintptr_t)15);
+    uint8_t *pr = reinterpret_cast<uint8_t *>(part + (n + SMP_BLOCK - 1) / SMP_BLOCK);
+    float *res_val = reinterpret_cast<float *>(pr);
+    int32_t *res_idx = reinterpret_cast<int32_t *>(pr + (size_t)SMP_KMAX * 4);
+    int32_t *res_ok = reinterpret_cast<int32_t *>(pr + (size_t)SMP_KMAX * 8);
     if (temperature <= 0.0f) {
         const int32_t ablk = (int32_t)((n + SMP_BLOCK - 1) / SMP_BLOCK);
         hipLaunchKernelGGL(k_smp_argmax_part, dim3(ablk), dim3(256), 0, s, logits, n, part);
@@ -740,9 +849,11 @@ hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k,
     const size_t ev_lds = (size_t)lcap * 4 + (size_t)sb * 8 + (size_t)k * 4;
     hipLaunchKernelGGL(k_smp_events, dim3(nblk), dim3(256), ev_lds, s, logits, n, k, sb, lcap, tops, ev_idx,
                        ev_val, ev_n);
+    hipLaunchKernelGGL(k_smp_slots, dim3(1), dim3(1024), 0, s, logits, n, k, sb, nblk, ev_idx, ev_val, ev_n,
+                       nan_flag, res_val, res_idx, res_ok);
     SmpArgs a{temperature, top_p, min_p, k, sb, nblk};
-    hipLaunchKernelGGL(k_smp_finish, dim3(1), dim3(64), 0, s, logits, n, a, ev_idx, ev_val, ev_n, nan_flag, rng,
-                       token);
+    hipLaunchKernelGGL(k_smp_finish, dim3(1), dim3(64), 0, s, logits, n, a, ev_idx, ev_val, ev_n, nan_flag, res_val,
+                       res_idx, res_ok, rng, token);
     return hipGetLastError();
 }
 
