@@ -336,8 +336,8 @@ int hip_sample(float *logits, int64_t n, const qk_sampler *sp, uint64_t *rng,
  * g_log, beta: [n_tok][n_heads]; state: [n_heads][k_hd][v_hd], updated in
  * place; out: [n_tok][n_heads][v_hd]. Bit-exact against the reference's
  * x86 build (sequential fp32 sums, expf of glibc's FMA build). Head dims
- * at most QK_DELTANET_MAX_HD. Device pointers; scratch per stream, as for
- * the LM head. */
+ * at most QK_DELTANET_MAX_HD. Device pointers; out must not overlap the
+ * inputs or the state (rejected); scratch per stream, as for the LM head. */
 #define QK_DELTANET_MAX_HD 128
 int hip_deltanet_chunked(const float *q, const float *k, const float *v,
                          const float *g_log, const float *beta, int64_t n_tok,

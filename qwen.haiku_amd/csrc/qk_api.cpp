@@ -671,6 +671,17 @@ int hip_deltanet_chunked(const float *q, const float *k, const float *v, const f
     if (!aligned(q, 4) || !aligned(k, 4) || !aligned(v, 4) || !aligned(g_log, 4) || !aligned(beta, 4) ||
         !aligned(state, 4) || !aligned(out, 4))
         return fail(QK_ERR_ARG, "misaligned float arrays");
+    {   // out is written while later phases still read the inputs and the state
+        const size_t nq = (size_t)n_tok * n_heads * k_hd * 4, nv = (size_t)n_tok * n_heads * v_hd * 4;
+        const size_t ng = (size_t)n_tok * n_heads * 4, ns = (size_t)n_heads * k_hd * v_hd * 4;
+        auto overlap = [&](const void *a, size_t na) {
+            const uintptr_t x = reinterpret_cast<uintptr_t>(out), y = reinterpret_cast<uintptr_t>(a);
+            return x < y + na && y < x + nv;
+        };
+        if (overlap(q, nq) || overlap(k, nq) || overlap(v, nv) || overlap(g_log, ng) || overlap(beta, ng) ||
+            overlap(state, ns))
+            return fail(QK_ERR_ARG, "out overlaps an input or the state");
+    }
     void *scratch = nullptr;
     if ((rc = stream_scratch(stream_of(stream), qk::deltanet_scratch_bytes(n_heads, k_hd, v_hd, n_tok), &scratch)))
         return rc;

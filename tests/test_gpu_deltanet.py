@@ -124,6 +124,10 @@ def test_deltanet_rejects_bad_shapes(lib):
     with pytest.raises(qk.QKError):                    # a chunk holds at most 64 tokens
         lib.deltanet_host(np.zeros((65, 128)), np.zeros((65, 128)), np.zeros((65, 128)), np.zeros(65),
                           np.zeros(65), np.zeros((128, 128)))
+    q2 = torch.zeros((4, 2, 128), device="cuda")
+    g2 = torch.zeros((4, 2), device="cuda")
+    with pytest.raises(qk.QKError):                    # out written over v, which later phases still read
+        lib.deltanet_chunked(q2, q2, q2, g2, g2, torch.zeros((2, 128, 128), device="cuda"), out=q2)
     with pytest.raises(qk.QKError):                    # head dim past QK_DELTANET_MAX_HD, host layer
         lib.deltanet_layer_host(np.zeros((4, 2, 129)), np.zeros((4, 2, 129)), np.zeros((4, 2, 128)),
                                 np.zeros((4, 2)), np.zeros((4, 2)), np.zeros((2, 129, 128)))
