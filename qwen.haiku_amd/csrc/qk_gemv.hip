@@ -7,13 +7,13 @@
 //
 // Loads. All weight loads are buffer loads whose range check covers the
 // wave's current work item (rows of one tile), so no lane needs a guard.
-//  - Q4_K / Q5_K (144 / 176-byte blocks, 16-byte aligned): each lane loads
-//    the fields of its block straight into registers (3 / 5 loads).
-//  - Q6_K / Q8_0 (210 / 34-byte blocks): the wave reads its item with
-//    lane-contiguous 16-byte loads (each load instruction covers 1 KB of
-//    consecutive bytes) and passes it through a wave-private LDS window,
-//    from which lanes read their fields at any alignment. Direct loads
-//    would take 9 (Q6_K) or 24 (Q8_0) instructions per lane.
+// The wave reads its item with lane-contiguous 16-byte loads (each load
+// instruction covers 1 KB of consecutive bytes, non-temporal) and passes
+// it through a wave-private LDS window, from which lanes read their block
+// fields at any alignment (Q6_K's 210-byte and Q8_0's 34-byte blocks
+// included). For Q4_K / Q5_K this replaced per-lane loads of each block's
+// fields straight into registers: 5.89 against 5.35 TB/s on a 144 MB
+// Q4_K stream, 4.45 against 4.70 us for the config-1 set.
 // Loads run one work item ahead of the arithmetic.
 //
 // Arithmetic. An aligned group of 4 lanes owns one 256-element super-block:
@@ -172,7 +172,11 @@ __device__ __forceinline__ Span make_span(const uint8_t *w, int64_t s, int64_t e
 // Buffer loads: the range check of the buffer resource (num_records =
 // npc x 16) turns pieces past the item into zeros without a memory access,
 // so the loads need no per-lane guard. A load whose 64 pieces all lie past
-// the item is skipped (a uniform branch).
+// the item is skipped (a uniform branch). The weights are read once per
+// launch, so the loads carry the non-temporal cache policy (bit 1 of the
+// buffer instruction's cache-policy operand on gfx950): 6.36 against
+// 5.55 TB/s on the 209 MB LM head.
+constexpr int W_NT = 2;
 template <int NL>
 __device__ __forceinline__ void chunk_load(ChunkN<NL> &c, const Span &sp, int lane) {
     const __amdgpu_buffer_rsrc_t r =
@@ -180,7 +184,7 @@ __device__ __forceinline__ void chunk_load(ChunkN<NL> &c, const Span &sp, int la
 #pragma unroll
     for (int u = 0; u < NL; u++) {
         if (u * 64 < sp.npc) {
-            const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16, u * 1024, 0);
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16, u * 1024, W_NT);
             c.v[u] = make_uint4(v[0], v[1], v[2], v[3]);
         }
     }
@@ -195,7 +199,7 @@ __device__ __forceinline__ void chunk_load_all(ChunkN<NL> &c, const Span &sp, in
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(sp.base), 0, sp.npc * 16, 0x00020000);
 #pragma unroll
     for (int u = 0; u < NL; u++) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16, u * 1024, 0);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16, u * 1024, W_NT);
         c.v[u] = make_uint4(v[0], v[1], v[2], v[3]);
     }
 }
@@ -238,7 +242,7 @@ __device__ __forceinline__ void scale_min_pair(uint32_t s0, uint32_t s1, uint32_
 
 // ---- per-super-block fields and terms -------------------------------------------
 // Lane j (0..3) of a group holds its 32 quant bytes of the super-block and
-// the header (Q4_K / Q5_K: loaded directly; Q6_K: read from the window).
+// the header, read from the wave's LDS window.
 template <int T> struct Raw;
 template <> struct Raw<12> { uint4 hdr, q0, q1; };
 template <> struct Raw<13> { uint4 hdr, q0, q1, h0, h1; };
@@ -267,6 +271,21 @@ __device__ __forceinline__ void read_sb(Raw<14> &r, const uint8_t *wb, int off, 
     r.sc = lds_u16(wb + off + 192 + s);
     r.sc2 = lds_u16(wb + off + 196 + s);
     r.d = lds_u16(wb + off + 208);
+}
+
+// Q4_K / Q5_K blocks (144 / 176 bytes, so 16-byte aligned in the window):
+// the header, then lane j's 32 quant bytes (and Q5_K's 32 qh bytes).
+__device__ __forceinline__ void read_sb(Raw<12> &r, const uint8_t *wb, int off, int j) {
+    r.hdr = *(const QK_LDS uint4 *)(wb + off);
+    r.q0 = *(const QK_LDS uint4 *)(wb + off + 16 + 32 * j);
+    r.q1 = *(const QK_LDS uint4 *)(wb + off + 32 + 32 * j);
+}
+__device__ __forceinline__ void read_sb(Raw<13> &r, const uint8_t *wb, int off, int j) {
+    r.hdr = *(const QK_LDS uint4 *)(wb + off);
+    r.h0 = *(const QK_LDS uint4 *)(wb + off + 16);
+    r.h1 = *(const QK_LDS uint4 *)(wb + off + 32);
+    r.q0 = *(const QK_LDS uint4 *)(wb + off + 48 + 32 * j);
+    r.q1 = *(const QK_LDS uint4 *)(wb + off + 64 + 32 * j);
 }
 
 // ---- activation operands straight from the Q8_K row -----------------------
@@ -478,7 +497,7 @@ __device__ __forceinline__ void gather_terms(float (&tg)[P], float t, int src0) 
     }
 }
 
-// Q6_K rows handled by this workgroup (the LDS-window path): tiles
+// K-quant rows handled by this workgroup (the LDS-window path): tiles
 // lw, lw+nwg, ... of 4 waves x 16/P rows. A row's P = 2^LP groups each take
 // one super-block of a step (P super-blocks); the P terms of a step are
 // gathered into the row's first lane and added to the row sum in
@@ -535,7 +554,7 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
     const __amdgpu_buffer_rsrc_t ar = act_rsrc(D.xq, nb * Q8K_BYTES);
     // fp32 row: quantized into LDS after the first item's loads are issued
     const uint8_t *xl = XF ? lds : nullptr;
-    Act6 xa;
+    typename ActOf<TYPE>::type xa;
     if (!xl) load_act(xa, ar, g, j);
     int xit = 0;
     int tile = lw, it = 0;
@@ -645,137 +664,6 @@ __device__ __forceinline__ void run_kq(const KDesc &D, int lw, int nwg, uint8_t 
         nsp = span(ntile, nit);
     }
     finish();
-}
-
-// Q4_K / Q5_K: the same tiles and gather as run_kq, with each lane's block
-// fields loaded straight into registers (buffer loads, range-checked by
-// the item).
-__device__ __forceinline__ void load_direct(Raw<12> &r, __amdgpu_buffer_rsrc_t rs, int off, int j) {
-    r.hdr = bl128(rs, off);
-    r.q0 = bl128(rs, off + 16 + 32 * j);
-    r.q1 = bl128(rs, off + 32 + 32 * j);
-}
-__device__ __forceinline__ void load_direct(Raw<13> &r, __amdgpu_buffer_rsrc_t rs, int off, int j) {
-    r.hdr = bl128(rs, off);
-    r.h0 = bl128(rs, off + 16);
-    r.h1 = bl128(rs, off + 32);
-    r.q0 = bl128(rs, off + 48 + 32 * j);
-    r.q1 = bl128(rs, off + 64 + 32 * j);
-}
-template <int TYPE, int LP, bool FUSED, bool LM, bool XF>
-__device__ __forceinline__ void run_kqd(const KDesc &D, int lw, int nwg, uint8_t *lds, uint64_t &best, bool keys) {
-    constexpr int BB = TYPE == 12 ? Q4K_BYTES : Q5K_BYTES;
-    constexpr int P = 1 << LP;
-    constexpr int RPW = 16 >> LP;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int grp = lane >> 2, j = lane & 3;
-    const int team = grp >> LP, g = grp & (P - 1);
-    const int nb = D.nb, ntiles = D.ntiles, n = D.n;
-    const int niter = (nb + P - 1) >> LP;
-    const uint32_t rowb = (uint32_t)nb * BB;
-    const uint8_t *__restrict__ w = D.w;
-    float *__restrict__ y = D.y;
-    const int src0 = team * P * 4;
-    const int lofs = (team * nb + g) * BB;
-    auto rsrc = [&](int t, int i) -> __amdgpu_buffer_rsrc_t {
-        const int r0 = t * (4 * RPW) + wave * RPW;
-        uint32_t len;
-        if (niter == 1) {
-            const int nr = (n - r0 < RPW) ? n - r0 : RPW;
-            len = (uint32_t)nr * rowb;
-        } else {
-            const int nbl = (nb - i * P < P) ? nb - i * P : P;
-            len = (uint32_t)nbl * BB;
-        }
-        if (t >= ntiles || r0 >= n) len = 0;
-        const uint32_t s0 = (uint32_t)r0 * rowb + (uint32_t)(i * P * BB);
-        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w + s0), 0, (int)len, 0x00020000);
-    };
-    // activation operands of super-block g first (those of every item
-    // when a row is one item), then the first item's weights
-    const __amdgpu_buffer_rsrc_t ar = act_rsrc(D.xq, nb * Q8K_BYTES);
-    // fp32 row: quantized into LDS after the first item's loads are issued
-    const uint8_t *xl = XF ? lds : nullptr;
-    typename ActOf<TYPE>::type xa;
-    if (!xl) load_act(xa, ar, g, j);
-    int xit = 0;
-    int tile = lw, it = 0;
-    Raw<TYPE> cur;
-    load_direct(cur, rsrc(tile, it), lofs, j);
-    if (xl) {
-        stage_q8k_f32(reinterpret_cast<const float *>(D.xq), nb, lds);
-        lds_barrier();
-        load_act_lds(xa, xl, g, j);
-    }
-    int ntile = tile, nit = it + 1;
-    if (nit == niter) { nit = 0; ntile += nwg; }
-    float sum = 0.0f;
-    // item (tile, it) from registers c: its term, gathered into the row's
-    // first lane, which stores the row after its last item
-    auto item = [&](const Raw<TYPE> &c, int tile, int it) __attribute__((always_inline)) {
-        if (it != xit) {                               // rows of several items: next super-blocks
-            if (xl) load_act_lds(xa, xl, it * P + g, j);
-            else load_act(xa, ar, it * P + g, j);
-            xit = it;
-        }
-        // a group past the row end contributes +0.0 (as in run_kq)
-        const int lim = (nb - it * P < P) ? nb - it * P : P;
-        const float t0 = term_sb<FUSED>(c, xa, j);
-        const float t = g < lim ? t0 : 0.0f;
-        float tg[P];
-        gather_terms<P>(tg, t, src0);
-#pragma unroll
-        for (int g2 = 0; g2 < P; g2++) sum += tg[g2];
-        if (it == niter - 1) {
-            const int row = tile * (4 * RPW) + wave * RPW + team;
-            if (FUSED) sum = bcast8(sum);
-            if (row < n && g == 0 && j == 0) {
-                *(QK_GLOBAL float *)(y + row) = sum;
-                if (keys) {
-                    const uint64_t k = argkey(sum, row);
-                    best = k > best ? k : best;
-                }
-            }
-            sum = 0.0f;
-        }
-    };
-    if (ntile >= ntiles) {                             // one item (a decode launch): no look-ahead
-        item(cur, tile, it);
-        return;
-    }
-    if (LM && TYPE == 12 && niter == 1) {
-        // Q4_K rows of one item (k <= 4096), many items per wave (the
-        // streaming instantiation): two register sets in turn, so one
-        // item's loads stay in flight while the wave waits for the other's.
-        // Moving look-ahead registers into place would wait for every load
-        // at the latch.
-        Raw<TYPE> nxt;
-        while (true) {
-            load_direct(nxt, rsrc(ntile, 0), lofs, j);   // past the last tile: zeros, never stored
-            item(cur, tile, 0);
-            tile = ntile;
-            ntile += nwg;
-            if (tile >= ntiles) break;
-            load_direct(cur, rsrc(ntile, 0), lofs, j);
-            item(nxt, tile, 0);
-            tile = ntile;
-            ntile += nwg;
-            if (tile >= ntiles) break;
-        }
-        return;
-    }
-    while (tile < ntiles) {
-        Raw<TYPE> nxt;
-        load_direct(nxt, rsrc(ntile, nit), lofs, j);
-        item(cur, tile, it);
-        cur = nxt;
-        tile = ntile;
-        it = nit;
-        ntile = tile;
-        nit = it + 1;
-        if (nit == niter) { nit = 0; ntile += nwg; }
-    }
 }
 
 // Q8_0 (q8_0_dot_q8_0, simd/avx.c:65-158, simd/quants.h:244-256): one row
@@ -1079,14 +967,14 @@ __global__ __launch_bounds__(256, LM ? 4 : 5) void k_gemv(uint32_t t0, uint32_t 
     const bool keys = amax_partial != nullptr;        // argmax keys (LM head) wanted
     switch (D.type) {
         case 12:
-            if (D.p == 4) run_kqd<12, 2, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
-            else if (D.p == 8) run_kqd<12, 3, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
-            else run_kqd<12, 4, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
+            if (D.p == 4) run_kq<12, 2, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
+            else if (D.p == 8) run_kq<12, 3, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
+            else run_kq<12, 4, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
             break;
         case 13:
-            if (D.p == 4) run_kqd<13, 2, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
-            else if (D.p == 8) run_kqd<13, 3, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
-            else run_kqd<13, 4, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
+            if (D.p == 4) run_kq<13, 2, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
+            else if (D.p == 8) run_kq<13, 3, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
+            else run_kq<13, 4, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
             break;
         case 14:
             if (D.p == 4) run_kq<14, 2, FUSED, LM, XF>(D, lw, D.nwg, lds, best, keys);
