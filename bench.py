@@ -47,13 +47,11 @@ MALL_DEFEAT_BYTES = 512 << 20
 REPLAY_TARGET_S = 1.0e-3          # a graph replay (one step) lasts about this long
 WARM_S = 0.2                      # minimum warm-up time
 # HBM bytes per config-1 launch of the current k_gemv, from rocprofv3 --pmc
-# FETCH_SIZE and WRITE_SIZE runs of this script (--copy-probe 256), each
-# scaled by its reading for a known-size copy / fill (FETCH x2.000,
-# WRITE x1.000); the runs are recorded in profiles/k_gemv_decode_set_lmhead.md.
-# None when the kernel has changed since the last counter run.
-# config-1 HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
-# each scaled by its reading for a known-size copy in the same run
-CONFIG1_TRAFFIC_BYTES = 12_064_266
+# FETCH_SIZE and WRITE_SIZE runs of this script (--only config1
+# --copy-probe 256), each scaled by its reading for a known-size copy / fill
+# in the same run (FETCH x2.000: 5870.1 KiB; WRITE x1.000: 54.0 KiB). None
+# when the kernel has changed since the last counter run.
+CONFIG1_TRAFFIC_BYTES = 12_077_261
 E2E_GPU = os.path.join(ROOT, "qwen.haiku_amd", "host", "_build", "qwen_e2e_gpu")
 E2E_CPU = os.path.join(ROOT, "oracle", "_ref", "qwen_e2e_cpu")
 
