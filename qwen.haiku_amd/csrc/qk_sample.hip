@@ -242,8 +242,10 @@ __global__ __launch_bounds__(256) void k_smp_blocks(const float *logits, int64_t
 // a logit of the block can enter only if it exceeds T; for such a logit v
 // the count of earlier logits >= v is the count in R = {x in P : x > T}
 // (fewer than k elements, all inside those lists) plus the count among
-// the block's earlier candidates. Events are candidates at index >= k
-// whose count is below k, written in index order with their values.
+// the block's earlier candidates, which go in chunks of 256 with T and R
+// carried forward over each chunk (so no candidate scans more than R and
+// its own chunk). Events are candidates at index >= k whose count is below
+// k, written in index order with their values.
 __device__ __forceinline__ int32_t wg_sum(int32_t c, int32_t *wsum) {
     c = wave_sum_i(c);
     if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = c;
@@ -280,9 +282,10 @@ __global__ __launch_bounds__(256) void k_smp_events(const float *logits, int64_t
     uint32_t *keys = reinterpret_cast<uint32_t *>(lds4);
     float *cv = reinterpret_cast<float *>(keys + lcap);   // sb candidate values
     int32_t *ci = reinterpret_cast<int32_t *>(cv + sb);   // sb candidate indices
-    float *rp = reinterpret_cast<float *>(ci + sb);    // R: the prefix values above T (< k)
+    float *rp = reinterpret_cast<float *>(ci + sb);    // R: the prefix values above T (< k), then R' twice
     __shared__ int32_t wsum[4];
-    __shared__ int32_t nr_sh, ncand_sh;
+    __shared__ int32_t nr_sh, ncand_sh, nr2_sh;
+    __shared__ uint32_t tk_sh;
     const int64_t base = (int64_t)b * sb;
     const int32_t n4 = (nlist + 3) >> 2;
     for (int32_t j = threadIdx.x; j < n4 * 4; j += 256) keys[j] = j < nlist ? fkey(tops[j]) : 0u;   // 0: below all
@@ -327,19 +330,80 @@ __global__ __launch_bounds__(256) void k_smp_events(const float *logits, int64_t
         }
     __syncthreads();
     const int32_t ncand = ncand_sh, nr = nr_sh;
-    for (int32_t c = threadIdx.x; c < ncand; c += 256) {
-        if (ci[c] < k) continue;                       // the initial fill
-        const float v = cv[c];
-        int32_t cnt = 0;
-        int32_t r = 0;
-        for (; r + 4 <= nr; r += 4) cnt += (rp[r] >= v) + (rp[r + 1] >= v) + (rp[r + 2] >= v) + (rp[r + 3] >= v);
-        for (; r < nr; r++) cnt += rp[r] >= v;
-        int32_t e = 0;
-        for (; e + 8 <= c && cnt < k; e += 8)
-            cnt += (cv[e] >= v) + (cv[e + 1] >= v) + (cv[e + 2] >= v) + (cv[e + 3] >= v) + (cv[e + 4] >= v) +
-                   (cv[e + 5] >= v) + (cv[e + 6] >= v) + (cv[e + 7] >= v);
-        for (; e < c && cnt < k; e++) cnt += cv[e] >= v;
-        if (cnt < k) ci[c] |= (int32_t)0x80000000;     // indices are < 2^31
+    // The candidates in chunks of 256, in index order, with a running
+    // threshold: the top k of everything before a chunk is the multiset
+    // R' (the values above T', fewer than k, as keys in rk) plus k - |R'|
+    // copies of T' (key 0 while fewer than k values came before). A
+    // candidate at or below T' has k earlier values >= it; one above it
+    // counts those in R' and its own chunk's earlier candidates. After a
+    // chunk, T' becomes the k-th largest of R', the copies and the chunk
+    // (a bisection), and R' the values above it.
+    uint32_t *rk = reinterpret_cast<uint32_t *>(rp);  // R' (rp's values, as keys)
+    uint32_t *rk2 = rk + k;                           // the next R'
+    for (int32_t r = threadIdx.x; r < nr; r += 256) rk[r] = fkey(rp[r]);
+    if (threadIdx.x == 0) {
+        tk_sh = tkey;
+        nr2_sh = nr;
+    }
+    __syncthreads();
+    for (int32_t c0 = 0; c0 < ncand; c0 += 256) {
+        const uint32_t tk = tk_sh;
+        const int32_t nr2 = nr2_sh;                    // < k <= 256
+        const int32_t c = c0 + threadIdx.x;
+        const bool act = c < ncand;
+        const uint32_t kv = act ? fkey(cv[c]) : 0u;
+        if (act && ci[c] >= k && kv > tk) {            // the initial fill never enters
+            int32_t cnt = 0, r = 0;
+            for (; r + 8 <= nr2; r += 8) {             // eight independent reads per step
+                const uint4 a = *reinterpret_cast<const uint4 *>(&rk[r]);
+                const uint4 b2 = *reinterpret_cast<const uint4 *>(&rk[r + 4]);
+                cnt += (a.x >= kv) + (a.y >= kv) + (a.z >= kv) + (a.w >= kv) + (b2.x >= kv) + (b2.y >= kv) +
+                       (b2.z >= kv) + (b2.w >= kv);
+            }
+            for (; r < nr2; r++) cnt += rk[r] >= kv;
+            const float v = cv[c];
+            int32_t e = c0;
+            for (; e + 8 <= c && cnt < k; e += 8)
+                cnt += (cv[e] >= v) + (cv[e + 1] >= v) + (cv[e + 2] >= v) + (cv[e + 3] >= v) + (cv[e + 4] >= v) +
+                       (cv[e + 5] >= v) + (cv[e + 6] >= v) + (cv[e + 7] >= v);
+            for (; e < c && cnt < k; e++) cnt += cv[e] >= v;
+            if (cnt < k) ci[c] |= (int32_t)0x80000000;   // indices are < 2^31
+        }
+        if (c0 + 256 >= ncand) break;                  // uniform: the last chunk
+        __syncthreads();                               // every count has read rk
+        if (threadIdx.x < 64) {                        // one wave: the next T' and R'
+            const int lane = threadIdx.x;
+            const int32_t nc = ncand - c0 < 256 ? ncand - c0 : 256;
+            uint32_t key8[8];                          // R' entries l + 64m, chunk entries l + 64m
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                key8[m] = lane + 64 * m < nr2 ? rk[lane + 64 * m] : 0u;
+                key8[4 + m] = lane + 64 * m < nc ? fkey(cv[c0 + lane + 64 * m]) : 0u;
+            }
+            uint32_t t = 0;
+            for (int bit = 31; bit >= 0; bit--) {
+                const uint32_t cand = t | (1u << bit);
+                int32_t cnt = 0;
+#pragma unroll
+                for (int m = 0; m < 8; m++) cnt += key8[m] >= cand;   // 0 keys are padding: cand >= 1
+                if (lane == 0 && tk >= cand) cnt += k - nr2;
+                if (wave_sum_i(cnt) >= k) t = cand;
+            }
+            int32_t nn = 0;                            // R'' = the keys above t, compacted by the wave
+#pragma unroll
+            for (int m = 0; m < 8; m++) {
+                const bool keep = key8[m] > t;
+                const uint64_t bal = __ballot(keep);
+                if (keep) rk2[nn + __builtin_popcountll(bal & ((1ull << lane) - 1))] = key8[m];
+                nn += __builtin_popcountll(bal);
+            }
+            for (int32_t r = lane; r < nn; r += 64) rk[r] = rk2[r];   // nn < k; the wave wrote rk2 itself
+            if (lane == 0) {
+                tk_sh = t;
+                nr2_sh = nn;
+            }
+        }
+        __syncthreads();
     }
     __syncthreads();
     if (threadIdx.x < 64) {                            // compact the events in order
@@ -368,23 +432,24 @@ __global__ __launch_bounds__(256) void k_smp_events(const float *logits, int64_t
 // smallest are exactly the evicted ones, the k largest the survivors).
 // That element sits in its own fill slot, or in the slot of the earlier
 // event that brought it in, so every event's slot is found by pointer
-// jumping over "evicts the element of rank j". One workgroup ranks the
-// elements (keys in LDS), resolves the chains and writes each survivor
-// into its slot; k_smp_finish then skips its replay. Ties (equal keys,
-// -0 and +0 included), a NaN in the fill or more than SMP_NMAX elements
-// leave *ok = 0 and the replay runs.
-constexpr int SMP_NMAX = 3584;
+// jumping over "evicts the element of rank j". One workgroup sorts the
+// elements by key (a bitonic sort in LDS), resolves the chains and writes
+// each survivor into its slot; k_smp_finish then skips its replay. Ties
+// (equal keys, -0 and +0 included), a NaN in the fill or more than
+// SMP_NMAX elements leave *ok = 0 and the replay runs.
+constexpr int SMP_NMAX = 4096;
+constexpr int SMP_NSORT = 4096;                        // sort capacity: a power of two >= SMP_NMAX
 
 __global__ __launch_bounds__(1024) void k_smp_slots(const float *logits, int64_t n, int32_t k, int32_t sb,
                                                     int32_t nblk, const int32_t *ev_idx, const float *ev_val,
                                                     const int32_t *ev_n, const int32_t *nan_flag, float *res_val,
                                                     int32_t *res_idx, int32_t *ok) {
-    __shared__ uint32_t key[SMP_NMAX];                 // elements: the fill, then the events in index order
-    __shared__ float ev[SMP_NMAX];
-    __shared__ int32_t eid[SMP_NMAX];                  // logit index of each element
-    __shared__ int32_t byr[SMP_NMAX];                  // element of each rank, then resolved slots
+    // (key << 32 | element) pairs, sorted ascending; then, as 32-bit
+    // words, the element of each rank and the resolved slots
+    __shared__ uint64_t buf[SMP_NSORT];
     __shared__ int32_t off[SMP_KMAX + 1];
     __shared__ int32_t skip;
+    int32_t *byr = reinterpret_cast<int32_t *>(buf);
     const int tid = threadIdx.x;
     if (tid == 0) {
         int32_t acc = 0, nf = 0;
@@ -400,50 +465,62 @@ __global__ __launch_bounds__(1024) void k_smp_slots(const float *logits, int64_t
     __syncthreads();
     if (skip) return;                                  // uniform
     const int32_t total = off[nblk], N = k + total;
-    for (int32_t e = tid; e < N; e += 1024) {
-        float v;
-        int32_t id;
-        if (e < k) {
-            v = logits[e];
-            id = e;
-        } else {
-            const int32_t j = e - k;
-            int32_t lo = 0, hi = nblk;                 // last block with off[block] <= j
-            while (hi - lo > 1) {
-                const int32_t mid = (lo + hi) >> 1;
-                if (off[mid] <= j) lo = mid;
-                else hi = mid;
-            }
-            const int64_t at = (int64_t)lo * sb + (j - off[lo]);
-            v = ev_val[at];
-            id = ev_idx[at];
+    // element e: the fill slot e < k, or event e - k (in index order)
+    auto locate = [&](int32_t j) -> int64_t {          // scratch position of event j
+        int32_t lo = 0, hi = nblk;                     // last block with off[block] <= j
+        while (hi - lo > 1) {
+            const int32_t mid = (lo + hi) >> 1;
+            if (off[mid] <= j) lo = mid;
+            else hi = mid;
         }
-        ev[e] = v;
-        eid[e] = id;
-        key[e] = fkey(v);
+        return (int64_t)lo * sb + (j - off[lo]);
+    };
+    int32_t P = 2;
+    while (P < N) P <<= 1;                             // <= SMP_NSORT
+    for (int32_t e = tid; e < P; e += 1024) {
+        uint64_t v = ~0ull;                            // padding sorts last
+        if (e < N) {
+            const float x = e < k ? logits[e] : ev_val[locate(e - k)];
+            v = ((uint64_t)fkey(x) << 32) | (uint32_t)e;
+        }
+        buf[e] = v;
     }
     __syncthreads();
-    int tie = 0;
-    for (int32_t e = tid; e < N; e += 1024) {
-        const uint32_t ke = key[e];
-        int32_t r = 0, eq = 0;
-        int32_t f = 0;
-        for (; f + 4 <= N; f += 4) {
-            const uint4 q = *reinterpret_cast<const uint4 *>(&key[f]);
-            r += (q.x < ke) + (q.y < ke) + (q.z < ke) + (q.w < ke);
-            eq += (q.x == ke) + (q.y == ke) + (q.z == ke) + (q.w == ke);
+    for (int32_t size = 2; size <= P; size <<= 1) {    // bitonic sort, ascending
+        for (int32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int32_t i = tid; i < (P >> 1); i += 1024) {
+                const int32_t lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+                const uint64_t a = buf[lo], b = buf[hi];
+                const bool up = (lo & size) == 0;
+                if ((a > b) == up) {
+                    buf[lo] = b;
+                    buf[hi] = a;
+                }
+            }
+            __syncthreads();
         }
-        for (; f < N; f++) {
-            r += key[f] < ke;
-            eq += key[f] == ke;
-        }
-        tie |= eq > 1;
-        byr[r < N ? r : N - 1] = e;
     }
+    // ties (equal keys, -0 and +0 included) leave the order to the replay
+    int tie = 0;
+    for (int32_t r = 1 + tid; r < N; r += 1024) tie |= (buf[r] >> 32) == (buf[r - 1] >> 32);
     if (__syncthreads_or(tie)) {
         if (tid == 0) *ok = 0;
         return;
     }
+    // ranks -> elements, in place: every thread reads its entries first
+    int32_t mine[SMP_NSORT / 1024];
+#pragma unroll
+    for (int q = 0; q < SMP_NSORT / 1024; q++) {
+        const int32_t r = tid + 1024 * q;
+        mine[q] = r < N ? (int32_t)(uint32_t)buf[r] : 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < SMP_NSORT / 1024; q++) {
+        const int32_t r = tid + 1024 * q;
+        if (r < N) byr[r] = mine[q];
+    }
+    __syncthreads();
     // event j evicts element byr[j]: a fill slot, or event byr[j] - k's slot
     for (int32_t len = 1; len < 2 * total; len <<= 1) {
         for (int32_t j = tid; j < total; j += 1024) {
@@ -455,8 +532,14 @@ __global__ __launch_bounds__(1024) void k_smp_slots(const float *logits, int64_t
     for (int32_t r = total + tid; r < N; r += 1024) {    // the survivors into their slots
         const int32_t e = byr[r];
         const int32_t slot = e < k ? e : byr[e - k];
-        res_val[slot] = ev[e];
-        res_idx[slot] = eid[e];
+        if (e < k) {
+            res_val[slot] = logits[e];
+            res_idx[slot] = e;
+        } else {
+            const int64_t at = locate(e - k);
+            res_val[slot] = ev_val[at];
+            res_idx[slot] = ev_idx[at];
+        }
     }
     if (tid == 0) *ok = 1;
 }
@@ -846,7 +929,7 @@ hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k,
     }
     hipLaunchKernelGGL(k_smp_blocks, dim3(nblk), dim3(256), (size_t)sb * 4, s, logits, n, k, sb, tops, nan_flag);
     const int32_t lcap = ((nblk - 1) * k + 3) & ~3;   // the last block's prefix lists
-    const size_t ev_lds = (size_t)lcap * 4 + (size_t)sb * 8 + (size_t)k * 4;
+    const size_t ev_lds = (size_t)lcap * 4 + (size_t)sb * 8 + (size_t)k * 8;
     hipLaunchKernelGGL(k_smp_events, dim3(nblk), dim3(256), ev_lds, s, logits, n, k, sb, lcap, tops, ev_idx,
                        ev_val, ev_n);
     hipLaunchKernelGGL(k_smp_slots, dim3(1), dim3(1024), 0, s, logits, n, k, sb, nblk, ev_idx, ev_val, ev_n,
