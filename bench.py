@@ -283,18 +283,19 @@ def bench_config3(torch, qk, synth, lib, steps, warmup, wtype=12, n=3584, k=1024
     output buffers rotate through > 512 MB so each launch reads its weights
     from HBM and writes its outputs to fresh lines. Returns (copies, R,
     seconds for the GEMM alone, seconds for quantize + GEMM from fp32 x)."""
-    per = n * (k // 256) * qk.BLOCK_BYTES[wtype] + 4 * m * n
+    per = n * qk.row_bytes(wtype, k) + 4 * m * n
     copies = max(2, -(-MALL_DEFEAT_BYTES // per))
     w = torch.from_numpy(synth.blocks(wtype, n, k, seed=0)).cuda()
     ws = [w] + [w.clone() for _ in range(copies - 1)]
     ys = [torch.empty((m, n), dtype=torch.float32, device="cuda") for _ in range(copies)]
     x = torch.from_numpy(synth.activations(m, k, seed=0)).cuda()
-    xq = lib.quantize_q8k(x)
-    fn = {12: lib.L.hip_matmul_q4k, 13: lib.L.hip_matmul_q5k, 14: lib.L.hip_matmul_q6k}[wtype]
+    xq = lib.quantize_q8_0(x) if wtype == qk.Q8_0 else lib.quantize_q8k(x)
+    fn = {8: lib.L.hip_matmul_q8_0, 12: lib.L.hip_matmul_q4k, 13: lib.L.hip_matmul_q5k,
+          14: lib.L.hip_matmul_q6k}[wtype]
     wp = [C.c_void_p(t.data_ptr()) for t in ws]
     yp = [C.c_void_p(t.data_ptr()) for t in ys]
     xp, xqp = C.c_void_p(x.data_ptr()), C.c_void_p(xq.data_ptr())
-    quant = lib.L.hip_quantize_q8k
+    quant = lib.L.hip_quantize_q8_0 if wtype == qk.Q8_0 else lib.L.hip_quantize_q8k
     est = 2.0 * m * n * k / 250e12 * 1e6
     R = replays_for(copies, est)
 
@@ -311,7 +312,10 @@ def bench_config3(torch, qk, synth, lib, steps, warmup, wtype=12, n=3584, k=1024
     return copies, R, gt.time(gemm, R, steps, warmup), gt.time(both, R, steps, warmup)
 
 
-CONFIG3_CASES = ((12, 3584, 1024, 512), (12, 3584, 1024, 128), (12, 3584, 1024, 2048), (14, 1024, 3584, 512))
+# config 3 (Q4_K at three prompt lengths, the Q6_K down projection) and
+# the Q8_0 GEMM on config 1's Q8_0 matrix at a 512-token prompt
+CONFIG3_CASES = ((12, 3584, 1024, 512), (12, 3584, 1024, 128), (12, 3584, 1024, 2048), (14, 1024, 3584, 512),
+                 (8, 1024, 1024, 512))
 
 
 def config3_extras(torch, qk, synth, lib, steps, warmup, peak_tops=None):
@@ -322,9 +326,9 @@ def config3_extras(torch, qk, synth, lib, steps, warmup, peak_tops=None):
         c3, R, sg, sb = bench_config3(torch, qk, synth, lib, steps, warmup, t, n3, k3, m3)
         ops = 2.0 * m3 * n3 * k3
         launches = steps * R
-        alg = 4 * m3 * k3 + n3 * (k3 // 256) * qk.BLOCK_BYTES[t] + 4 * m3 * n3
+        alg = 4 * m3 * k3 + n3 * qk.row_bytes(t, k3) + 4 * m3 * n3
         tg, tb = ops * launches / sg, ops * launches / sb
-        name = {12: "q4k", 14: "q6k"}[t]
+        name = {8: "q80", 12: "q4k", 14: "q6k"}[t]
         e = {"TOPS_gemm": round(tg / 1e12, 2), "us_gemm": round(sg / launches * 1e6, 3),
              "TOPS_with_quantize": round(tb / 1e12, 2), "us_with_quantize": round(sb / launches * 1e6, 3),
              "frac_of_5POPS_gemm": round(tg / (MFMA_I8_PEAK_TOPS * 1e12), 4),

@@ -147,9 +147,11 @@ int hip_quantize_q8_0(const float *x, int64_t m, int64_t k, void *xq,
  * tensor_matmul_q{4k,5k,6k}_f32 / _q8_0_f32 at n_tok == 1
  * (slm/tensor.c:846-850, 912-917, 1026-1031, 974-979) and the
  * simd_q*_row_dot entry points it calls (simd/simd.c:236-250).
- * Limits: w 16-byte aligned; k <= 16384 (a Q8_0 activation row is
- * staged in LDS; the limit holds for every type); the matrix (n rows x
- * row bytes) below 4 GB (32-bit offsets). */
+ * Limits: w 16-byte aligned; k <= QK_MAX_K (a Q8_0 activation row is
+ * staged in LDS; the limit holds for every type and every matvec /
+ * matmul entry point); the matrix (n rows x row bytes) below 4 GB
+ * (32-bit offsets). */
+#define QK_MAX_K 65536
 int hip_matvec_q4k (const void *w, int64_t n, int64_t k, const void *xq,
                     float *y, void *stream);
 int hip_matvec_q5k (const void *w, int64_t n, int64_t k, const void *xq,
@@ -196,13 +198,17 @@ int hip_matvec_group_f32(const qk_gemv_desc_f32 *desc, int count, void *stream);
 
 /* y[t*n + j] = row_dot(W row j, xq row t) for t < m, j < n: the token
  * loop of tensor_matmul_q{4k,5k,6k}_f32 (slm/tensor.c:838-851) as one
- * int8-MFMA GEMM. xq holds m rows of k/256 Q8_K blocks. */
+ * int8-MFMA GEMM. xq holds m rows of k/256 Q8_K blocks (k/32 Q8_0 blocks
+ * for hip_matmul_q8_0, the token loop of tensor_matmul_q8_0_f32,
+ * slm/tensor.c:952-981). m is at most 65535 * 64. */
 int hip_matmul_q4k(const void *w, int64_t n, int64_t k, const void *xq,
                    int64_t m, float *y, void *stream);
 int hip_matmul_q5k(const void *w, int64_t n, int64_t k, const void *xq,
                    int64_t m, float *y, void *stream);
 int hip_matmul_q6k(const void *w, int64_t n, int64_t k, const void *xq,
                    int64_t m, float *y, void *stream);
+int hip_matmul_q8_0(const void *w, int64_t n, int64_t k, const void *xq,
+                    int64_t m, float *y, void *stream);
 
 /* ---- device layer: dequantization ----------------------------------- */
 

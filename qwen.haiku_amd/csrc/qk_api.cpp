@@ -160,7 +160,7 @@ int check_mat(int type, const void *w, int64_t n, int64_t k, const void *xq, con
     if (!w || !xq || !y) return fail(QK_ERR_ARG, "null pointer");
     if (n < 1 || k < 1) return fail(QK_ERR_ARG, "empty matrix (n=%lld, k=%lld)", (long long)n, (long long)k);
     if (k % block_elems(type)) return fail(QK_ERR_ARG, "k=%lld is not a multiple of %lld", (long long)k, (long long)block_elems(type));
-    if (k > 16384) return fail(QK_ERR_ARG, "k=%lld exceeds the 16384 limit", (long long)k);
+    if (k > QK_MAX_K) return fail(QK_ERR_ARG, "k=%lld exceeds the %d limit", (long long)k, QK_MAX_K);
     if (n > 0x7fffffffLL) return fail(QK_ERR_ARG, "n=%lld exceeds 2^31-1 rows", (long long)n);
     // The GEMV streams the matrix with 16-byte loads from its base and
     // addresses it with 32-bit byte offsets (buffer loads).
@@ -279,7 +279,6 @@ int matmul(int type, const void *w, int64_t n, int64_t k, const void *xq, int64_
     if (rc) return rc;
     if ((rc = check_mat(type, w, n, k, xq, y))) return rc;
     if (m < 1 || m > GEMM_MAX_M) return fail(QK_ERR_ARG, "m=%lld tokens (1..%lld)", (long long)m, GEMM_MAX_M);
-    if (type == QK_TYPE_Q8_0) return fail(QK_ERR_UNSUPPORTED, "no Q8_0 GEMM; use hip_matvec_q8_0 per token");
     HIP_OK(qk::launch_gemm(type, static_cast<const uint8_t *>(w), n, k, static_cast<const uint8_t *>(xq), m, y,
                            fused_of(st().tier.load()), stream_of(s)),
            "gemm launch");
@@ -456,6 +455,9 @@ int hip_matmul_q5k(const void *w, int64_t n, int64_t k, const void *xq, int64_t 
 }
 int hip_matmul_q6k(const void *w, int64_t n, int64_t k, const void *xq, int64_t m, float *y, void *s) {
     return matmul(QK_TYPE_Q6_K, w, n, k, xq, m, y, s);
+}
+int hip_matmul_q8_0(const void *w, int64_t n, int64_t k, const void *xq, int64_t m, float *y, void *s) {
+    return matmul(QK_TYPE_Q8_0, w, n, k, xq, m, y, s);
 }
 
 static int dequant(int type, const void *w, int64_t nblocks, float *y, void *s) {
@@ -822,7 +824,7 @@ int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f, int64_t k, c
     if (rc) return rc;
     if (!x || !out || n_tok < 1) return fail(QK_ERR_ARG, "bad activation arguments");
     if ((rc = check_weight_args(host_w, type, k, out_f))) return rc;
-    if (type != QK_TYPE_Q8_0 && n_tok > GEMM_MAX_M)
+    if (n_tok > GEMM_MAX_M)
         return fail(QK_ERR_ARG, "n_tok=%lld tokens (1..%lld)", (long long)n_tok, GEMM_MAX_M);
     Lane *l = nullptr;
     if ((rc = my_lane(&l))) return rc;
@@ -859,43 +861,23 @@ int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f, int64_t k, c
     // the same contract as the device layer, on the device copy
     if ((rc = check_mat(type, w.dev, out_f, k, dxq, dy))) return rc;
     const int fused = fused_of(st().tier.load());
-    if (type == QK_TYPE_Q8_0) {
-        HIP_OK(qk::launch_quantize_q8_0(dx, n_tok * (k / QK8_0), dxq, l->stream), "quantize");
-        // tensor_matmul_q8_0_f32 has no batched form: up to 16 tokens per launch.
-        for (int64_t t0 = 0; t0 < n_tok; t0 += QK_GROUP_MAX_DEV) {
-            qk::GemvArgs a{};
-            a.fused = fused;
-            a.count = (int32_t)((n_tok - t0) < QK_GROUP_MAX_DEV ? (n_tok - t0) : QK_GROUP_MAX_DEV);
-            for (int i = 0; i < a.count; i++) {
-                a.d[i].type = type;
-                a.d[i].n = out_f;
-                a.d[i].k = k;
-                a.d[i].w = static_cast<const uint8_t *>(w.dev);
-                a.d[i].xq = dxq + (t0 + i) * act_bytes(type, k);
-                a.d[i].y = dy + (t0 + i) * out_f;
-                qk::gemv_plan(a.d[i]);
-            }
-            HIP_OK(qk::launch_gemv(a, 1 << 20, l->stream), "gemv launch");
-        }
+    if (type == QK_TYPE_Q8_0) HIP_OK(qk::launch_quantize_q8_0(dx, n_tok * (k / QK8_0), dxq, l->stream), "quantize");
+    else HIP_OK(qk::launch_quantize_q8k(dx, n_tok * (k / QK_K), dxq, l->stream), "quantize");
+    if (n_tok == 1) {
+        qk::GemvArgs a{};
+        a.fused = fused;
+        a.count = 1;
+        a.d[0].type = type;
+        a.d[0].n = out_f;
+        a.d[0].k = k;
+        a.d[0].w = static_cast<const uint8_t *>(w.dev);
+        a.d[0].xq = dxq;
+        a.d[0].y = dy;
+        qk::gemv_plan(a.d[0]);
+        HIP_OK(qk::launch_gemv(a, st().cu_count * 8, l->stream), "gemv launch");
     } else {
-        HIP_OK(qk::launch_quantize_q8k(dx, n_tok * (k / QK_K), dxq, l->stream), "quantize");
-        if (n_tok == 1) {
-            qk::GemvArgs a{};
-            a.fused = fused;
-            a.count = 1;
-            a.d[0].type = type;
-            a.d[0].n = out_f;
-            a.d[0].k = k;
-            a.d[0].w = static_cast<const uint8_t *>(w.dev);
-            a.d[0].xq = dxq;
-            a.d[0].y = dy;
-            qk::gemv_plan(a.d[0]);
-            HIP_OK(qk::launch_gemv(a, st().cu_count * 8, l->stream), "gemv launch");
-        } else {
-            HIP_OK(qk::launch_gemm(type, static_cast<const uint8_t *>(w.dev), out_f, k, dxq, n_tok, dy, fused,
-                                   l->stream),
-                   "gemm launch");
-        }
+        HIP_OK(qk::launch_gemm(type, static_cast<const uint8_t *>(w.dev), out_f, k, dxq, n_tok, dy, fused, l->stream),
+               "gemm launch");
     }
     if (!y_direct)
         HIP_OK(hipMemcpyAsync(l->hy, dy, yb, hipMemcpyDeviceToHost, l->stream), "hipMemcpyAsync(out)");

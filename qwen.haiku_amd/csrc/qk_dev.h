@@ -20,9 +20,6 @@
 #define Q6K_BYTES 210   // u8 ql[128] | u8 qh[64] @128 | i8 scales[16] @192 | f16 d @208
 #define Q80_BYTES 34    // f16 d | i8 qs[32] @2
 
-// Upper bound on blocks per activation row staged in LDS: K <= 16384.
-#define QK_MAX_K 16384
-#define QK_NB_MAX (QK_MAX_K / QK_K)
 
 namespace qk {
 

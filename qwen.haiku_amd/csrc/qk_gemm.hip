@@ -1,5 +1,6 @@
-// qk_gemm.hip -- chunked-prefill GEMM over native GGUF K-quant blocks
-// (gfx950, int8 MFMA).
+// qk_gemm.hip -- chunked-prefill GEMM over native GGUF K-quant and Q8_0
+// blocks (gfx950, int8 MFMA). The K-quant kernel is described here; the
+// Q8_0 kernel (k_gemm_q80) has its own description further down.
 //
 // y[t*n + j] = row_dot(W row j, xq row t): the token loop of
 // tensor_matmul_q{4k,5k,6k}_f32 (slm/tensor.c:838-851, 908-918,
@@ -633,8 +634,206 @@ void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb, const uint8_t *__r
     }
 }
 
+// ---- Q8_0 x Q8_0 --------------------------------------------------------------
+// The token loop of tensor_matmul_q8_0_f32 (slm/tensor.c:952-981) over
+// q8_0_dot_q8_0 (simd/avx.c:65-158, simd/quants.h:244-256). Per 32-element
+// block the AVX2/VNNI tiers keep eight int32 slot partials p_s (bytes
+// 4s..4s+3) and eight fp32 chains acc_s = fma((float)p_s, d_w*d_x, acc_s),
+// summed at the end as ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)); the scalar
+// and AVX1 tiers add (float)(sum of the block) * (d_w*d_x) to one sum.
+//
+// One v_mfma_i32_32x32x32_i8 covers one block (K = 32) of 4 weight rows x
+// 32 tokens with every slot apart: its 32 A rows are (weight row j, slot
+// s) = 8j + s, each the weight row's block with every byte outside slot s
+// zeroed. Output v of a lane is then p_s of row j = v/4, slot
+// s = 4h + v%4 (h = lane/32) for token lane%32, so the lane runs the fp32
+// chains of four slots of four rows; the other four slots sit in lane
+// l^32. The mask selects bytes by their position in the staged block,
+// and both operands of a lane hold the same block positions, so it does
+// not depend on the MFMA's internal k order.
+//
+// A 512-thread workgroup owns RT weight rows x TT tokens (32 x 32) and
+// walks the blocks in steps of 8: the step's blocks are staged into LDS
+// (quants at a 16-byte aligned stride, d widened) while the next step's
+// raw bytes load into registers. Its RT/4 x TT/32 MFMA tiles per block are spread
+// over the eight waves; each tile is one chain of MFMA, conversion and
+// FMAs per block, so the tiles of several waves per SIMD overlap.
+#define G8_KB 8                       // blocks per step
+#define G8_LD (G8_KB * 32 + 16)       // LDS row stride of the quants
+
+template <int RT, int TT>
+struct __attribute__((aligned(16))) Gemm80Lds {
+    int8_t w[RT][G8_LD];              // weight quants of the step's blocks
+    int8_t x[TT][G8_LD];              // activation quants
+    float wd[G8_KB][RT];              // weight d, rows contiguous
+    float xd[G8_KB][TT];              // activation d
+};
+
+// One 34-byte block (d | qs[32]) at byte offset o of a buffer whose base
+// is 4-byte aligned: qs through the nine aligned dwords that contain it
+// (o is even, so the shift is 0 or 2), d as a 16-bit load.
+struct Q80Raw { uint4 a, b; uint32_t c, d, sh; };
+
+__device__ __forceinline__ void load_q80(Q80Raw &r, __amdgpu_buffer_rsrc_t rs, int o) {
+    const int q = o + 2, a = q & ~3;
+    r.sh = (uint32_t)(q & 3);
+    r.a = bl128(rs, a);
+    r.b = bl128(rs, a + 16);
+    r.c = bl32(rs, a + 32);
+    r.d = __builtin_amdgcn_raw_buffer_load_b16(rs, o, 0, 0);
+}
+
+__device__ __forceinline__ void store_q80(const Q80Raw &r, int8_t *qs, float *d) {
+    const uint32_t v[9] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c};
+    uint32_t q[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) q[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], r.sh);
+    lds_st16(qs, q[0], q[1], q[2], q[3]);
+    lds_st16(qs + 16, q[4], q[5], q[6], q[7]);
+    *d = h2f(r.d);
+}
+
+template <bool FUSED, int RT, int TT>
+__global__ __launch_bounds__(512) void k_gemm_q80(const uint8_t *__restrict__ w, int64_t n, int nb,
+                                                  const uint8_t *__restrict__ xq, int64_t m,
+                                                  float *__restrict__ y) {
+    constexpr int NRG = RT / 4, NTH = TT / 32;           // 4-row groups, 32-token halves
+    constexpr int TPW = NRG * NTH / 8;                   // MFMA tiles per wave
+    constexpr int NPAIR = (RT + TT) * G8_KB;             // (row or token, block) pairs per step
+    constexpr int NSLOT = (NPAIR + 511) / 512;           // of them per thread
+    static_assert(TPW >= 1 && NRG * NTH == 8 * TPW, "tiles split evenly over 8 waves");
+    static_assert((RT * G8_KB) % 64 == 0, "a wave stages weights or activations, not both");
+    __shared__ Gemm80Lds<RT, TT> s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, h = lane >> 5;
+    const int64_t r0 = (int64_t)blockIdx.x * RT, t0 = (int64_t)blockIdx.y * TT;
+    const int rowb = nb * Q80_BYTES;
+    // the tile's weight rows and tokens as buffers based at the 4-byte
+    // aligned address at or below their first byte, ending at the 4-byte
+    // boundary at or after their last byte (the same dwords hold both
+    // ends), so rows past n and tokens past m read zeros
+    const int nrows = (n - r0 < RT) ? (int)(n - r0) : RT;
+    const int mrows = (m - t0 < TT) ? (int)(m - t0) : TT;
+    const uint8_t *wt = w + r0 * rowb, *xt = xq + t0 * rowb;
+    const int wmis = (int)(reinterpret_cast<uintptr_t>(wt) & 3u), xmis = (int)(reinterpret_cast<uintptr_t>(xt) & 3u);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(wt - wmis), 0, (wmis + nrows * rowb + 3) & ~3, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(xt - xmis), 0, (xmis + mrows * rowb + 3) & ~3, 0x00020000);
+    // staging: pair p = tid + 512u is weight row p/8 (p < 8 RT) or token
+    // p/8 - RT, block p%8 of the step (wave-uniform: 8 RT is a multiple of 64)
+    Q80Raw raw[NSLOT];
+    int so[NSLOT];
+    auto load_step = [&](int b0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < NSLOT; u++) {
+            const int p = tid + 512 * u;
+            if (p < NPAIR) load_q80(raw[u], p < RT * G8_KB ? wr : xr, so[u] + b0 * Q80_BYTES);
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < NSLOT; u++) {
+        const int p = tid + 512 * u, r = p >> 3, kb = p & 7;
+        so[u] = p < RT * G8_KB ? wmis + r * rowb + kb * Q80_BYTES : xmis + (r - RT) * rowb + kb * Q80_BYTES;
+    }
+    load_step(0);
+    // this lane's slot (A row 8j + s, s = col % 8) as a mask of the four
+    // dwords it holds (block bytes 16h..16h+15)
+    const int sl = (col & 7) - 4 * h;
+    const uint32_t mk0 = sl == 0 ? ~0u : 0u, mk1 = sl == 1 ? ~0u : 0u;
+    const uint32_t mk2 = sl == 2 ? ~0u : 0u, mk3 = sl == 3 ? ~0u : 0u;
+    const v16i zero = {0};
+    // the wave's tiles: q = TPW * wave + i, row group q % NRG, token half q / NRG
+    float acc[TPW][16];
+#pragma unroll
+    for (int i = 0; i < TPW; i++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[i][v] = 0.0f;
+
+    for (int b0 = 0; b0 < nb; b0 += G8_KB) {
+        lds_barrier();                                   // previous step's reads done
+#pragma unroll
+        for (int u = 0; u < NSLOT; u++) {
+            const int p = tid + 512 * u, r = p >> 3, kb = p & 7;
+            if (p < RT * G8_KB) store_q80(raw[u], &s.w[r][32 * kb], &s.wd[kb][r]);
+            else if (p < NPAIR) store_q80(raw[u], &s.x[r - RT][32 * kb], &s.xd[kb][r - RT]);
+        }
+        if (b0 + G8_KB < nb) load_step(b0 + G8_KB);      // next step in flight during compute
+        lds_barrier();
+        const int kn = (nb - b0 < G8_KB) ? nb - b0 : G8_KB;
+        for (int kb = 0; kb < kn; kb++) {
+#pragma unroll
+            for (int i = 0; i < TPW; i++) {
+                const int q = TPW * wave + i, rg = q % NRG, th = q / NRG;
+                const v4i bx = *(const QK_LDS v4i *)&s.x[32 * th + col][32 * kb + 16 * h];
+                const float dx = s.xd[kb][32 * th + col];
+                const v4i aw = *(const QK_LDS v4i *)&s.w[4 * rg + (col >> 3)][32 * kb + 16 * h];
+                const v4i am = {(int32_t)((uint32_t)aw[0] & mk0), (int32_t)((uint32_t)aw[1] & mk1),
+                                (int32_t)((uint32_t)aw[2] & mk2), (int32_t)((uint32_t)aw[3] & mk3)};
+                const float4 dw = *(const QK_LDS float4 *)&s.wd[kb][4 * rg];
+                const float dwj[4] = {dw.x, dw.y, dw.z, dw.w};
+                const v16i pr = __builtin_amdgcn_mfma_i32_32x32x32_i8(FUSED ? am : aw, bx, zero, 0, 0, 0);
+                float *a = acc[i];
+                if constexpr (FUSED) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float sc = __fmul_rn(dwj[j], dx);
+#pragma unroll
+                        for (int c = 0; c < 4; c++) a[4 * j + c] = __builtin_fmaf((float)pr[4 * j + c], sc, a[4 * j + c]);
+                    }
+                } else {
+                    // unmasked A: every A row 8j + s is the whole block of row
+                    // j, so its output is the block's sum (the same for all
+                    // eight s); a[j] keeps row j's sum
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float sc = __fmul_rn(dwj[j], dx);
+                        a[j] = __fadd_rn(a[j], __fmul_rn((float)pr[4 * j], sc));
+                    }
+                }
+            }
+        }
+    }
+
+    // lane h = 0 of token col stores rows 4rg + j
+#pragma unroll
+    for (int i = 0; i < TPW; i++) {
+        const int q = TPW * wave + i, rg = q % NRG, th = q / NRG;
+        const float *a = acc[i];
+        float res[4];
+        if constexpr (FUSED) {
+            float b[16];
+#pragma unroll
+            for (int v = 0; v < 16; v++) b[v] = __fadd_rn(a[v], __shfl_xor(a[v], 32));   // a_s + a_(s+4)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                res[j] = __fadd_rn(__fadd_rn(b[4 * j], b[4 * j + 1]), __fadd_rn(b[4 * j + 2], b[4 * j + 3]));
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) res[j] = a[j];
+        }
+        const int64_t t = t0 + 32 * th + col;
+        const int64_t row = r0 + 4 * rg;
+        if (h == 0 && t < m) {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (row + j < n) __builtin_nontemporal_store(res[j], &y[t * n + row + j]);
+        }
+    }
+}
+
 hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, const uint8_t *xq, int64_t m,
                        float *y, int fused, hipStream_t s) {
+    if (type == 8) {
+        const int nb = (int)(k / QK8_0);
+        // 32 x 32 tiles: eight MFMA tiles, one per wave (measured against
+        // 32 x 64 and 16 x 64 at M = 64..2048: 14.7 / 18.2 / 15.5 us at
+        // M = 512, N = K = 1024)
+        const dim3 grid((unsigned)((n + 31) / 32), (unsigned)((m + 31) / 32));
+        if (fused) hipLaunchKernelGGL((k_gemm_q80<true, 32, 32>), grid, dim3(512), 0, s, w, n, nb, xq, m, y);
+        else hipLaunchKernelGGL((k_gemm_q80<false, 32, 32>), grid, dim3(512), 0, s, w, n, nb, xq, m, y);
+        return hipGetLastError();
+    }
     const int nb = (int)(k / QK_K);
     const unsigned mt = (unsigned)((m + GM_BM - 1) / GM_BM);
     // 64-row tiles when they alone give every CU a workgroup, else 32-row

@@ -97,7 +97,7 @@ class QK:
             getattr(L, f).argtypes = [_vp, _i64, _i64, _vp, _vp, _vp]
         L.hip_matvec_group.argtypes = [C.POINTER(GemvDesc), C.c_int, _vp]
         L.hip_matvec_group_f32.argtypes = [C.POINTER(GemvDesc), C.c_int, _vp]
-        for f in ("hip_matmul_q4k", "hip_matmul_q5k", "hip_matmul_q6k"):
+        for f in ("hip_matmul_q4k", "hip_matmul_q5k", "hip_matmul_q6k", "hip_matmul_q8_0"):
             getattr(L, f).argtypes = [_vp, _i64, _i64, _vp, _i64, _vp, _vp]
         for f in ("hip_dequant_q4k", "hip_dequant_q5k", "hip_dequant_q6k"):
             getattr(L, f).argtypes = [_vp, _i64, _vp, _vp]
@@ -208,7 +208,8 @@ class QK:
         import torch
         if y is None:
             y = torch.empty((m, n), dtype=torch.float32, device=w.device)
-        f = {Q4_K: self.L.hip_matmul_q4k, Q5_K: self.L.hip_matmul_q5k, Q6_K: self.L.hip_matmul_q6k}[wtype]
+        f = {Q4_K: self.L.hip_matmul_q4k, Q5_K: self.L.hip_matmul_q5k, Q6_K: self.L.hip_matmul_q6k,
+             Q8_0: self.L.hip_matmul_q8_0}[wtype]
         _need(w, n * row_bytes(wtype, k), "w")
         _need(xq, m * act_bytes(wtype, k), "xq")
         _need(y, 4 * m * n, "y")

@@ -74,6 +74,7 @@ SHAPES = [
     (14, 100, 2560), (12, 40, 16384), (14, 9, 16384), (8, 45, 96), (8, 3, 16384),
     (13, 21, 8192), (8, 70, 512),                          # Q5_K rows of two items; Q8_0 512 rows path
     (12, 40000, 256), (13, 40000, 256),                    # more tiles than workgroups: items in a loop
+    (12, 9, 65536), (13, 3, 25600), (14, 5, 65536), (8, 7, 65536),   # k up to the 65536 limit
 ]
 
 
@@ -114,7 +115,8 @@ def test_matvec_group_matches_single(lib, orc):
 
 F32_SHAPES = [(12, 3584, 1024), (14, 1024, 3584), (13, 2048, 1024), (13, 1024, 2048), (8, 1024, 1024),
               (8, 70, 512), (8, 45, 96), (8, 3, 16384), (12, 33, 768), (13, 21, 8192), (14, 100, 2560),
-              (12, 40, 16384), (14, 9, 16384), (12, 40000, 256), (14, 30000, 1024)]
+              (12, 40, 16384), (14, 9, 16384), (12, 40000, 256), (14, 30000, 1024),
+              (12, 9, 65536), (8, 5, 65536)]             # rows quantized into 78 / 74 KB of LDS
 
 
 @pytest.mark.parametrize("wtype,n,k", F32_SHAPES)
@@ -180,6 +182,12 @@ GEMM_SHAPES = [
     # 64-row tiles (at least 256 of them) for every type; the others run
     # 32-row tiles with a four-way k split
     (13, 4096, 1024, 512), (14, 4096, 1024, 300), (12, 4160, 512, 260),
+    (12, 40, 65536, 9), (14, 33, 25600, 3),                                  # k up to the limit
+    # Q8_0: config 1's matrix and the model's ssm_alpha / ssm_beta at a
+    # 512-token prompt; a step of one block (65 = 8 * 8 + 1); partial row
+    # and token tiles; one block; k at the limit
+    (8, 1024, 1024, 512), (8, 16, 1024, 512), (8, 33, 2080, 65), (8, 45, 96, 37),
+    (8, 100, 512, 129), (8, 1, 32, 1), (8, 70, 65536, 5),
 ]
 
 
@@ -190,10 +198,12 @@ def test_matmul_gemm(tier, orc, wtype, n, k, m, epi, t):
     step(f"matmul type={wtype} n={n} k={k} m={m} tier={t}")
     lib.set_tier(t)
     w = synth.blocks(wtype, n, k, seed=m, tag=wtype)
+    if wtype == 8:
+        w[0, 2:34] = 0x80                              # quants of -128 (a valid GGUF byte)
     x = synth.activations(m, k, seed=m + 1)
     if m >= 4:
         x[1:4] = edge_rows(k)[[0, 6, 7]]               # zero / huge / subnormal rows
-    xq = orc.quantize_q8k(x)
+    xq = orc.quantize_for(wtype, x)
     got = host(lib.matmul(wtype, dev(w), n, k, dev(xq), m))
     want = orc.matmul_xq(wtype, w, n, k, xq, m, epi)
     assert_bits_equal(got, want, f"gemm {wtype} {m}x{n}x{k}")
@@ -417,8 +427,10 @@ def test_rejects_bad_shapes(lib):
     L = lib.L
     assert L.hip_matvec_q4k(wp, 4, 1000, xp, yp, None) == 1          # k % 256
     assert L.hip_matvec_q4k(C.c_void_p(w.data_ptr() + 1), 1, 256, xp, yp, None) == 1   # misaligned
-    assert L.hip_matvec_q4k(wp, 1, 32768, xp, yp, None) == 1         # k above 16384
-    assert L.hip_matvec_q8_0(wp, 1, 32768, xp, yp, None) == 1
+    assert L.hip_matvec_q4k(wp, 1, 65536 + 256, xp, yp, None) == 1   # k above 65536
+    assert L.hip_matvec_q8_0(wp, 1, 65536 + 32, xp, yp, None) == 1
+    assert L.hip_matmul_q8_0(wp, 1, 65536 + 32, xp, 2, yp, None) == 1
+    assert L.hip_matmul_q8_0(wp, 4, 64, xp, 0, yp, None) == 1         # m = 0
     assert L.hip_matvec_q4k(wp, 0, 256, xp, yp, None) == 1           # empty
     assert L.hip_matvec_q4k(None, 1, 256, xp, yp, None) == 1         # null
     am = torch.zeros(1, dtype=torch.int32, device="cuda")
