@@ -402,7 +402,7 @@ def sampler_extras(torch, qk, lib, steps, warmup, vocab=248320):
 
 def deltanet_extras(torch, lib, steps, warmup, n_tok=512, heads=16, hd=128):
     """hip_deltanet_chunked over one Gated DeltaNet layer of the model: 16
-    heads of 128, a 512-token prompt in 8 chunks of 64 (56 kernel launches),
+    heads of 128, a 512-token prompt in 8 chunks of 64 (5 kernel launches),
     inputs resident, the state carried in place from call to call."""
     g = torch.Generator(device="cuda").manual_seed(0)
     q = torch.nn.functional.normalize(torch.randn(n_tok, heads, hd, device="cuda", generator=g), dim=2) / hd ** 0.5

@@ -10,11 +10,11 @@
 // every output element is one lane that runs its reduction in exactly the
 // reference's order, skipping the zero coefficients the reference skips;
 // the parallelism is across outputs, heads and chunks. There are seven
-// phases, one launch each, each reading the previous phases' results from
-// the per-(chunk, head) scratch below; phases 1-4 do not depend on the
-// carried state and run for a group of chunks at once (this file is built
-// with -ffp-contract=off; the only fused multiply-adds are inside
-// qk_expf):
+// phases, each reading the previous phases' results from the per-(chunk,
+// head) scratch below; phases 1-4 do not depend on the carried state and
+// run for a group of chunks at once, one launch each, and phases 5-7 run
+// chunk after chunk inside one launch (this file is built with
+// -ffp-contract=off; the only fused multiply-adds are inside qk_expf):
 //
 //   1 cumulative gate, exps, decay mask; K*beta, V*beta, K*beta*exp(gcs),
 //     Q*exp(gcs)
@@ -25,7 +25,6 @@
 //     v_new
 //   6 the intra-chunk attention on v_new; the output rows
 //   7 state := state * exp(g_last) + (K * exp(g_last - gcs))^T v_new
-//     (6 and 7 in one launch)
 #include "qk_dev.h"
 #include "qk_expf.h"
 #include "qk_kernels.h"
@@ -48,8 +47,6 @@ struct DnScratch {
     float *attn;    // [H][64][64] solved, unit diagonal
     float *veff;    // [H][64][vd]
     float *kcd;     // [H][64][kd]
-    float *ainter;  // [H][64][vd]
-    float *vnew;    // [H][64][vd]
 };
 
 struct DnArgs {
@@ -59,7 +56,6 @@ struct DnArgs {
     int64_t n_tok;                       // tokens of the call
     int64_t g0;                          // first chunk of the group in flight
     int32_t H, kd, vd;
-    int32_t c;                           // phases 5-7: the chunk of the group they run
 };
 
 // A scratch slot is one (chunk of the group, head): slot = c * H + h.
@@ -340,132 +336,119 @@ __global__ __launch_bounds__(256) void k_dn_apply(DnArgs a, DnScratch s) {
         if (i0 + r <= last) dst[(i0 + r) * w + e] = acc[r];
 }
 
-// 5. grid (ceil(n/4), ceil(vd/64), H), for chunk c of the group: a workgroup takes four rows t and
-// 64 columns of the state carried in, both staged in LDS with every load
-// in flight at once; wave r runs row t0 + r, lane e its column, the two
-// chains (Q*exp(gcs) and the decayed keys against the state) in the
-// reference's d order.
-constexpr int DN_T = 4;                                // rows per workgroup in phase 5
+// 5-7 for every chunk of the group in one launch. Each of the three is
+// local to a column e of the state: v_new[., e], the output column e and
+// the new state column e read only the state column e and per-chunk rows
+// every column shares. So a workgroup owns DN_E columns of one head, keeps
+// them in LDS and walks the group's chunks in order: grid
+// (ceil(vd / DN_E), H), no workgroup waits for another. A chunk's shared
+// rows (Q*exp(gcs), the decayed keys, K, the KQ^T decay rows and the gate
+// factors) go through registers into LDS, rows padded by one float so the
+// eight rows a wave reads sit in different banks; the next chunk's loads
+// are issued before this chunk's chains run. Each element's chains run
+// in the reference's order, as phases 5-7 above do.
+constexpr int DN_E = 8;                                // state columns per workgroup
+constexpr int DN_RS = DN_D + 1;                        // padded LDS row of DN_D floats
+constexpr int DN_CS = DN_C + 1;                        // padded LDS row of DN_C floats
 
-__global__ __launch_bounds__(256) void k_dn_state_in(DnArgs a, DnScratch s) {
-    const DnChunk ck = dn_chunk(a, a.c * a.H + blockIdx.z);
-    const int h = ck.h, n = ck.n, kd = a.kd, vd = a.vd;
-    const int t0 = blockIdx.x * DN_T, e0 = blockIdx.y * 64;
-    const int64_t ho = (int64_t)ck.slot * DN_C;
-    __shared__ float S[DN_D][64];
-    __shared__ float Q[DN_T][DN_D], K[DN_T][DN_D];
-    {
-        const float *st = a.state + (int64_t)h * kd * vd;
-        float v[32];
+// Lane (t, e) runs both chains of phase 5 and, over one loop, the output
+// chain of (t, e) and the state chains of (t, e) and (t + 64, e).
+__global__ __launch_bounds__(512) void k_dn_carry(DnArgs a, DnScratch s, int gc) {
+    constexpr int PR = DN_C * DN_D / 512, PA = DN_C * DN_C / 512;   // row / KQ^T elements per lane
+    __shared__ float Qs[DN_C * DN_RS], Ks[DN_C * DN_RS], Kr[DN_C * DN_RS], As[DN_C * DN_CS];
+    __shared__ float S[DN_D][DN_E], vn[DN_C][DN_E], gf[DN_C + 1];
+    const int h = blockIdx.y, e0 = blockIdx.x * DN_E, kd = a.kd, vd = a.vd;
+    const int tid = threadIdx.x, el = tid % DN_E, e = e0 + el, t = tid / DN_E;
+    const bool col = e < vd;
+    float *st = a.state + (int64_t)h * kd * vd;
+    for (int p = tid; p < DN_D * DN_E; p += 512) {
+        const int d = p / DN_E, c = p % DN_E;
+        S[d][c] = d < kd && e0 + c < vd ? st[(int64_t)d * vd + e0 + c] : 0.0f;
+    }
+    for (int c = 0; c < gc; c++) {
+        const DnChunk ck = dn_chunk(a, c * a.H + h);
+        const int n = ck.n;
+        const int64_t ho = (int64_t)ck.slot * DN_C;
+        // the chunk's shared rows: every load in flight, then into LDS
+        float rq[PR], rc[PR], rk[PR], ra[PA], rg;
 #pragma unroll
-        for (int u = 0; u < 32; u++) {                 // 32 * 256 = 128 rows of 64 columns
-            const int p = u * 256 + threadIdx.x, d = p >> 6, c = p & 63;
-            v[u] = d < kd && e0 + c < vd ? st[(int64_t)d * vd + e0 + c] : 0.0f;
+        for (int u = 0; u < PR; u++) {
+            const int p = tid + 512 * u, tt = p / kd, d = p - tt * kd;
+            const bool in = tt < n;
+            rq[u] = in ? s.qg[(ho + tt) * kd + d] : 0.0f;
+            rc[u] = in ? s.kcd[(ho + tt) * kd + d] : 0.0f;
+            rk[u] = in ? row_of(a.k, a, ck.c0, tt, h, kd)[d] : 0.0f;
         }
-        float cq[2], ck[2];
 #pragma unroll
-        for (int u = 0; u < 2; u++) {                  // 2 * 256 = DN_T rows of DN_D
-            const int p = u * 256 + threadIdx.x, r = p / DN_D, d = p % DN_D;
-            const bool in = d < kd && t0 + r < n;
-            cq[u] = in ? s.qg[(ho + t0 + r) * kd + d] : 0.0f;
-            ck[u] = in ? s.kcd[(ho + t0 + r) * kd + d] : 0.0f;
+        for (int u = 0; u < PA; u++) {
+            const int p = tid + 512 * u;
+            ra[u] = p / DN_C < n ? s.akq[ho * DN_C + p] : 0.0f;
+        }
+        // exp(glast - gcs[t]) for t < 64, exp(glast) at 64
+        rg = tid <= DN_C ? s.gv[(int64_t)ck.slot * (3 * DN_C + 1) + 2 * DN_C + tid] : 0.0f;
+        __syncthreads();                               // the previous chunk's reads of the rows done
+#pragma unroll
+        for (int u = 0; u < PR; u++) {
+            const int p = tid + 512 * u, tt = p / kd, d = p - tt * kd;
+            if (tt < DN_C) {
+                Qs[tt * DN_RS + d] = rq[u];
+                Ks[tt * DN_RS + d] = rc[u];
+                Kr[tt * DN_RS + d] = rk[u];
+            }
         }
 #pragma unroll
-        for (int u = 0; u < 32; u++) {
-            const int p = u * 256 + threadIdx.x;
-            S[p >> 6][p & 63] = v[u];
+        for (int u = 0; u < PA; u++) {
+            const int p = tid + 512 * u;
+            As[(p / DN_C) * DN_CS + p % DN_C] = ra[u];
         }
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int p = u * 256 + threadIdx.x;
-            Q[p / DN_D][p % DN_D] = cq[u];
-            K[p / DN_D][p % DN_D] = ck[u];
+        if (tid <= DN_C) gf[tid] = rg;
+        __syncthreads();
+        // 5: the chains against the state (Q*exp(gcs) and the decayed
+        // keys, skipping zero coefficients as the reference does); v_new
+        float ai = 0.0f;
+        if (t < n && col) {
+            float vp = 0.0f;
+            const float *qr = Qs + t * DN_RS, *kr = Ks + t * DN_RS;
+#pragma unroll 8
+            for (int d = 0; d < kd; d++) {
+                const float x = S[d][el], qv = qr[d], kv = kr[d];
+                ai = qv != 0.0f ? __fadd_rn(ai, __fmul_rn(qv, x)) : ai;
+                vp = kv != 0.0f ? __fadd_rn(vp, __fmul_rn(kv, x)) : vp;
+            }
+            vn[t][el] = __fsub_rn(s.veff[(ho + t) * vd + e], vp);
+        }
+        __syncthreads();
+        // 6 and 7 over u: the output row's chain (the intra-chunk attention
+        // on v_new) and the state's for d = t and t + 64, with
+        // K * exp(glast - gcs) rounded as the reference forms it
+        const float *kq = As + t * DN_CS;
+        const int d0 = t, d1 = t + 64;
+        float acc6 = 0.0f, acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll 4
+        for (int u = 0; u < n; u++) {
+            const float x = vn[u][el], g = gf[u];
+            acc6 = __fadd_rn(acc6, __fmul_rn(kq[u], x));
+            acc0 = __fadd_rn(acc0, __fmul_rn(__fmul_rn(Kr[u * DN_RS + d0], g), x));
+            acc1 = __fadd_rn(acc1, __fmul_rn(__fmul_rn(Kr[u * DN_RS + d1], g), x));
+        }
+        if (col) {
+            if (t < n) a.out[((ck.c0 + t) * a.H + h) * (int64_t)vd + e] = __fadd_rn(ai, acc6);
+            if (d0 < kd) S[d0][el] = __fadd_rn(__fmul_rn(S[d0][el], gf[DN_C]), acc0);
+            if (d1 < kd) S[d1][el] = __fadd_rn(__fmul_rn(S[d1][el], gf[DN_C]), acc1);
         }
     }
     __syncthreads();
-    const int r = threadIdx.x >> 6, c = threadIdx.x & 63, t = t0 + r, e = e0 + c;
-    if (t >= n || e >= vd) return;
-    float ai = 0.0f, vp = 0.0f;
-#pragma unroll 8
-    for (int d = 0; d < kd; d++) {
-        const float x = S[d][c], q = Q[r][d], k = K[r][d];
-        ai = q != 0.0f ? __fadd_rn(ai, __fmul_rn(q, x)) : ai;
-        vp = k != 0.0f ? __fadd_rn(vp, __fmul_rn(k, x)) : vp;
+    for (int p = tid; p < DN_D * DN_E; p += 512) {
+        const int d = p / DN_E, c = p % DN_E;
+        if (d < kd && e0 + c < vd) st[(int64_t)d * vd + e0 + c] = S[d][c];
     }
-    s.ainter[(ho + t) * vd + e] = ai;
-    s.vnew[(ho + t) * vd + e] = __fsub_rn(s.veff[(ho + t) * vd + e], vp);
-}
-
-// Phases 6 and 7 share one launch for chunk c of the group: grid
-// (ceil(n*vd/256) + ceil(kd*vd/256), H), the first nout blocks write the
-// output rows and the rest the state carried out. Neither reads what the
-// other writes.
-// 6. lane (t, e), the output row element
-__device__ __forceinline__ void dn_out_block(const DnArgs &a, const DnScratch &s, int bx) {
-    const DnChunk ck = dn_chunk(a, a.c * a.H + blockIdx.y);
-    const int h = ck.h, n = ck.n, vd = a.vd;
-    const int p = bx * 256 + threadIdx.x;
-    if (p >= n * vd) return;
-    const int t = p / vd, e = p % vd;
-    const int64_t ho = (int64_t)ck.slot * DN_C;
-    const float *kq = s.akq + (ho + t) * DN_C;
-    const float *vn = s.vnew + ho * vd;
-    float acc = 0.0f;
-    int u = 0;
-    for (; u + DN_B <= n; u += DN_B) {
-        float c[DN_B], x[DN_B];
-#pragma unroll
-        for (int w = 0; w < DN_B; w++) {
-            c[w] = kq[u + w];
-            x[w] = vn[(u + w) * vd + e];
-        }
-#pragma unroll
-        for (int w = 0; w < DN_B; w++) acc = __fadd_rn(acc, __fmul_rn(c[w], x[w]));
-    }
-    for (; u < n; u++) acc = __fadd_rn(acc, __fmul_rn(kq[u], vn[u * vd + e]));
-    a.out[((ck.c0 + t) * a.H + h) * (int64_t)vd + e] = __fadd_rn(s.ainter[(ho + t) * vd + e], acc);
-}
-
-// 7. lane (d, e), the state carried out
-__device__ __forceinline__ void dn_state_out_block(const DnArgs &a, const DnScratch &s, int bx) {
-    const DnChunk ck = dn_chunk(a, a.c * a.H + blockIdx.y);
-    const int h = ck.h, n = ck.n, kd = a.kd, vd = a.vd;
-    const int p = bx * 256 + threadIdx.x;
-    if (p >= kd * vd) return;
-    const int d = p / vd, e = p % vd;
-    const int64_t ho = (int64_t)ck.slot * DN_C;
-    const float *gv = s.gv + (int64_t)ck.slot * (3 * DN_C + 1);
-    const float *vn = s.vnew + ho * vd;
-    float acc = 0.0f;
-    int t = 0;
-    for (; t + DN_B <= n; t += DN_B) {
-        float kg[DN_B], x[DN_B];
-#pragma unroll
-        for (int w = 0; w < DN_B; w++) {
-            kg[w] = __fmul_rn(row_of(a.k, a, ck.c0, t + w, h, kd)[d], gv[2 * DN_C + t + w]);
-            x[w] = vn[(t + w) * vd + e];
-        }
-#pragma unroll
-        for (int w = 0; w < DN_B; w++) acc = __fadd_rn(acc, __fmul_rn(kg[w], x[w]));
-    }
-    for (; t < n; t++) {
-        const float kg = __fmul_rn(row_of(a.k, a, ck.c0, t, h, kd)[d], gv[2 * DN_C + t]);
-        acc = __fadd_rn(acc, __fmul_rn(kg, vn[t * vd + e]));
-    }
-    float *st = a.state + (int64_t)h * kd * vd + p;
-    *st = __fadd_rn(__fmul_rn(*st, gv[3 * DN_C]), acc);
-}
-
-__global__ __launch_bounds__(256) void k_dn_out_state(DnArgs a, DnScratch s, int nout) {
-    if ((int)blockIdx.x < nout) dn_out_block(a, s, blockIdx.x);
-    else dn_state_out_block(a, s, blockIdx.x - nout);
 }
 
 // ---- launcher -----------------------------------------------------------------
 // Phases 1-4 read only their chunk's own inputs, so they run for a group
 // of chunks at once (one launch per phase over every (chunk, head) slot of
 // the group); phases 5-7 carry the state and run chunk after chunk. A
-// group holds at most DN_SLOTS slots (one head's slot is about 330 KB of
+// group holds at most DN_SLOTS slots (one head's slot is about 263 KB of
 // scratch at head dims 128), and at least one chunk.
 constexpr int DN_SLOTS = 256;
 
@@ -478,8 +461,8 @@ static int dn_group(int32_t H, int64_t n_tok) {
 size_t deltanet_scratch_bytes(int32_t H, int32_t kd, int32_t vd, int64_t n_tok) {
     const size_t slots = (size_t)dn_group(H, n_tok) * (size_t)H;
     const size_t per = (size_t)(3 * DN_C + 1) + 4 * (size_t)DN_C * DN_C + 4 * (size_t)DN_C * kd +
-                       4 * (size_t)DN_C * vd;
-    return (per * slots + 13 * 64) * sizeof(float) + 256;   // 13 arrays, each rounded up to 64 floats
+                       2 * (size_t)DN_C * vd;
+    return (per * slots + 11 * 64) * sizeof(float) + 256;   // 11 arrays, each rounded up to 64 floats
 }
 
 hipError_t launch_deltanet(const float *q, const float *k, const float *v, const float *g, const float *beta,
@@ -506,26 +489,16 @@ hipError_t launch_deltanet(const float *q, const float *k, const float *v, const
     s.kcd = take(slots * DN_C * kd);
     s.vb = take(slots * DN_C * vd);
     s.veff = take(slots * DN_C * vd);
-    s.ainter = take(slots * DN_C * vd);
-    s.vnew = take(slots * DN_C * vd);
     const int64_t chunks = (n_tok + DN_C - 1) / DN_C;
     for (int64_t g0 = 0; g0 < chunks; g0 += G) {
         const int gc = (int)(chunks - g0 < G ? chunks - g0 : G);   // chunks in this group
         const unsigned gs = (unsigned)(gc * H);                     // slots in this group
-        DnArgs a{q, k, v, g, beta, state, out, n_tok, g0, H, kd, vd, 0};
+        DnArgs a{q, k, v, g, beta, state, out, n_tok, g0, H, kd, vd};
         hipLaunchKernelGGL(k_dn_prep, dim3(DN_PREP, gs), dim3(256), 0, st, a, s);
         hipLaunchKernelGGL(k_dn_dots, dim3(4, 4, gs), dim3(256), 0, st, a, s);
         hipLaunchKernelGGL(k_dn_solve, dim3(gs), dim3(64), 0, st, a, s);
         hipLaunchKernelGGL(k_dn_apply, dim3(DN_C / DN_RB, 2, gs), dim3(256), 0, st, a, s);
-        for (int c = 0; c < gc; c++) {
-            a.c = c;
-            const int64_t rest = n_tok - (g0 + c) * DN_C;
-            const int n = (int)(rest < DN_C ? rest : DN_C);
-            hipLaunchKernelGGL(k_dn_state_in, dim3((n + DN_T - 1) / DN_T, (vd + 63) / 64, H), dim3(256), 0, st, a,
-                               s);
-            const int nout = (n * vd + 255) / 256;
-            hipLaunchKernelGGL(k_dn_out_state, dim3(nout + (kd * vd + 255) / 256, H), dim3(256), 0, st, a, s, nout);
-        }
+        hipLaunchKernelGGL(k_dn_carry, dim3((vd + DN_E - 1) / DN_E, H), dim3(512), 0, st, a, s, gc);
     }
     return hipGetLastError();
 }
