@@ -200,7 +200,8 @@ int hip_matvec_group_f32(const qk_gemv_desc_f32 *desc, int count, void *stream);
  * loop of tensor_matmul_q{4k,5k,6k}_f32 (slm/tensor.c:838-851) as one
  * int8-MFMA GEMM. xq holds m rows of k/256 Q8_K blocks (k/32 Q8_0 blocks
  * for hip_matmul_q8_0, the token loop of tensor_matmul_q8_0_f32,
- * slm/tensor.c:952-981). m is at most 65535 * 64. */
+ * slm/tensor.c:952-981). m is at most 65535 * 64 (65535 * 32 for
+ * hip_matmul_q8_0); so is n_tok of hip_qk_matmul_host. */
 int hip_matmul_q4k(const void *w, int64_t n, int64_t k, const void *xq,
                    int64_t m, float *y, void *stream);
 int hip_matmul_q5k(const void *w, int64_t n, int64_t k, const void *xq,

@@ -271,14 +271,16 @@ int matvec(int type, const void *w, int64_t n, int64_t k, const void *xq, float 
     return QK_OK;
 }
 
-// Token bound of the GEMM (grid.y = token tiles of 64).
-constexpr int64_t GEMM_MAX_M = 65535LL * 64;
+// Token bound of the GEMM: grid.y = token tiles of 64 (K-quants) or 32
+// (Q8_0), at most 65535 of them.
+int64_t gemm_max_m(int type) { return type == QK_TYPE_Q8_0 ? 65535LL * 32 : 65535LL * 64; }
 
 int matmul(int type, const void *w, int64_t n, int64_t k, const void *xq, int64_t m, float *y, void *s) {
     int rc = require_init();
     if (rc) return rc;
     if ((rc = check_mat(type, w, n, k, xq, y))) return rc;
-    if (m < 1 || m > GEMM_MAX_M) return fail(QK_ERR_ARG, "m=%lld tokens (1..%lld)", (long long)m, GEMM_MAX_M);
+    if (m < 1 || m > gemm_max_m(type))
+        return fail(QK_ERR_ARG, "m=%lld tokens (1..%lld)", (long long)m, (long long)gemm_max_m(type));
     HIP_OK(qk::launch_gemm(type, static_cast<const uint8_t *>(w), n, k, static_cast<const uint8_t *>(xq), m, y,
                            fused_of(st().tier.load()), stream_of(s)),
            "gemm launch");
@@ -824,8 +826,8 @@ int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f, int64_t k, c
     if (rc) return rc;
     if (!x || !out || n_tok < 1) return fail(QK_ERR_ARG, "bad activation arguments");
     if ((rc = check_weight_args(host_w, type, k, out_f))) return rc;
-    if (n_tok > GEMM_MAX_M)
-        return fail(QK_ERR_ARG, "n_tok=%lld tokens (1..%lld)", (long long)n_tok, GEMM_MAX_M);
+    if (n_tok > gemm_max_m(type))
+        return fail(QK_ERR_ARG, "n_tok=%lld tokens (1..%lld)", (long long)n_tok, (long long)gemm_max_m(type));
     Lane *l = nullptr;
     if ((rc = my_lane(&l))) return rc;
     std::shared_lock<std::shared_mutex> rl;

@@ -761,7 +761,11 @@ __global__ __launch_bounds__(512) void k_gemm_q80(const uint8_t *__restrict__ w,
         if (b0 + G8_KB < nb) load_step(b0 + G8_KB);      // next step in flight during compute
         lds_barrier();
         const int kn = (nb - b0 < G8_KB) ? nb - b0 : G8_KB;
-        for (int kb = 0; kb < kn; kb++) {
+        // unrolled with a uniform guard: every LDS address is an immediate
+        // offset from one base
+#pragma unroll
+        for (int kb = 0; kb < G8_KB; kb++) {
+            if (kb >= kn) break;
 #pragma unroll
             for (int i = 0; i < TPW; i++) {
                 const int q = TPW * wave + i, rg = q % NRG, th = q / NRG;

@@ -431,6 +431,8 @@ def test_rejects_bad_shapes(lib):
     assert L.hip_matvec_q8_0(wp, 1, 65536 + 32, xp, yp, None) == 1
     assert L.hip_matmul_q8_0(wp, 1, 65536 + 32, xp, 2, yp, None) == 1
     assert L.hip_matmul_q8_0(wp, 4, 64, xp, 0, yp, None) == 1         # m = 0
+    assert L.hip_matmul_q8_0(wp, 4, 64, xp, 65535 * 32 + 1, yp, None) == 1   # above 65535 token tiles of 32
+    assert "m=" in lib.last_error()
     assert L.hip_matvec_q4k(wp, 0, 256, xp, yp, None) == 1           # empty
     assert L.hip_matvec_q4k(None, 1, 256, xp, yp, None) == 1         # null
     am = torch.zeros(1, dtype=torch.int32, device="cuda")
@@ -447,6 +449,8 @@ def test_rejects_bad_shapes(lib):
     hp = lambda a: a.ctypes.data_as(C.c_void_p)
     assert L.hip_qk_matmul_host(hp(hw), 12, 4, 1000, hp(hx), 1, hp(ho)) == 1
     assert L.hip_qk_matmul_host(hp(hw), 12, 4, 256, hp(hx), 65535 * 64 + 1, hp(ho)) == 1
+    assert "n_tok" in lib.last_error()
+    assert L.hip_qk_matmul_host(hp(hw), 8, 4, 64, hp(hx), 65535 * 32 + 1, hp(ho)) == 1
     assert "n_tok" in lib.last_error()
     assert L.hip_qk_matmul_host(hp(hw), 7, 4, 256, hp(hx), 1, hp(ho)) == 6
     assert L.hip_qk_init(1) != 0                                       # another device while initialized
