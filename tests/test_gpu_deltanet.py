@@ -99,6 +99,19 @@ def test_deltanet_other_head_dims(lib, orc):
     assert_bits_equal(host(dst), want_s, "state")
 
 
+def test_deltanet_ragged_head_dims(lib, orc):
+    # v_hd not a multiple of the 8 state columns a workgroup carries, k_hd
+    # not a multiple of 4, and a partial last chunk (130 = 2 x 64 + 2)
+    step("deltanet kd=40 vd=52 heads=5 n_tok=130")
+    q, k, v, g, b = ssm_inputs(130, H=5, kd=40, vd=52, seed=6)
+    st = state0(5, 40, 52, 6)
+    want_o, want_s = orc.deltanet_chunked(q, k, v, g, b, st)
+    dst = dev(st)
+    out = lib.deltanet_chunked(dev(q), dev(k), dev(v), dev(g), dev(b), dst)
+    assert_bits_equal(host(out), want_o, "out")
+    assert_bits_equal(host(dst), want_s, "state")
+
+
 def test_deltanet_host_seam(lib, orc):
     """The body the seam gives chunked_ssm_step_f32: host buffers, one head."""
     step("deltanet host seam")
