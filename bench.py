@@ -1,10 +1,11 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized decode GEMV path on one MI355X.
 
-Workload: the decode-step GEMV set of one
+Workload (configuration 1 of the headline metric): the decode-step GEMV set of one
 Qwen3.5-0.8B-shaped layer at batch 1 -- Q4_K gate and up (3584x1024),
 Q6_K down (1024x3584), Q5_K 2048x1024, 512x1024 and 1024x2048, Q8_0
-1024x1024 -- random blocks per the BASELINE recipe, activations already
+1024x1024 -- random blocks as configuration 0 draws them (fp16 d, dmin,
+uniform scales and quants), activations already
 quantized (Q8_K / Q8_0) and resident in HBM. One launch is one fused
 dispatch (hip_matvec_group) over the seven matrices.
 

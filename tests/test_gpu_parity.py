@@ -2,8 +2,9 @@
 inputs. Bar: bit-exact for quantizers, dequant and every row dot (both
 float-epilogue families), identical argmax token; top-k as a set.
 
-Sizes: the BASELINE configurations at full size where the oracle is fast
-(config 0-2), plus ragged and edge shapes."""
+Sizes: the benchmark configurations 0-3 at full size (the decode GEMV,
+the decode set, the LM head, the prefill GEMM), plus ragged and edge
+shapes."""
 import numpy as np
 import pytest
 
