@@ -130,12 +130,13 @@ const char *hip_qk_tier_label(int tier);
 /* ---- device layer: activation quantizers --------------------------- */
 
 /* m rows of k floats -> m * k/256 Q8_K blocks (row t at xq + t*k/256).
- * Bit-exact quantize_row_q8_K (slm/tensor.c:683-720). k % 256 == 0. */
+ * Bit-exact quantize_row_q8_K (slm/tensor.c:683-720). k % 256 == 0;
+ * m * k/256 at most 2^26 blocks. */
 int hip_quantize_q8k(const float *x, int64_t m, int64_t k, void *xq,
                      void *stream);
 /* m rows of k floats -> m * k/32 Q8_0 blocks. Bit-exact
  * tensor_quantize_row_q8_0 (slm/tensor.c:930-950; roundf, half away
- * from zero). k % 32 == 0. */
+ * from zero). k % 32 == 0; m * k/32 at most 2^27 blocks. */
 int hip_quantize_q8_0(const float *x, int64_t m, int64_t k, void *xq,
                       void *stream);
 
@@ -214,7 +215,7 @@ int hip_matmul_q8_0(const void *w, int64_t n, int64_t k, const void *xq,
 /* ---- device layer: dequantization ----------------------------------- */
 
 /* nblocks blocks -> nblocks*256 floats. Bit-exact q{4,5,6}k_dequant_block
- * (slm/tensor.c:800-820, 867-896, 988-1010). */
+ * (slm/tensor.c:800-820, 867-896, 988-1010). nblocks at most 2^26. */
 int hip_dequant_q4k(const void *w, int64_t nblocks, float *y, void *stream);
 int hip_dequant_q5k(const void *w, int64_t nblocks, float *y, void *stream);
 int hip_dequant_q6k(const void *w, int64_t nblocks, float *y, void *stream);
@@ -232,7 +233,7 @@ int hip_dequant_q6k(const void *w, int64_t nblocks, float *y, void *stream);
  * h_out (may be NULL, may equal h) receives r, x_out (may be NULL) x,
  * xq (may be NULL, needs k % 256 == 0) the Q8_K row for the next GEMV;
  * one of x_out / xq is required. w holds k floats shared by every row.
- * k is a multiple of 4, at most QK_NORM_MAX_K; m at most 2^24. Bit-exact. Device
+ * k is a multiple of 4, at most QK_NORM_MAX_K; m below 2^24. Bit-exact. Device
  * pointers; float rows 16-byte aligned. The decode chain between two
  * matmuls: slm/qwen.c:936-948 (h = h + mix; ffn_norm) and the norm that
  * opens each layer's mixer (slm/qwen.c:332-334). */

@@ -366,7 +366,10 @@ int hip_quantize_q8k(const float *x, int64_t m, int64_t k, void *xq, void *strea
     int rc = require_init();
     if (rc) return rc;
     if (!x || !xq) return fail(QK_ERR_ARG, "null pointer");
-    if (m < 1 || k < 1 || k % QK_K) return fail(QK_ERR_ARG, "bad shape m=%lld k=%lld", (long long)m, (long long)k);
+    // a dispatch counts its work-items in 32 bits: 64 per block
+    if (m < 1 || k < 1 || k % QK_K || m > ((int64_t)1 << 26) / (k / QK_K))
+        return fail(QK_ERR_ARG, "bad shape m=%lld k=%lld (k a multiple of 256, m*k/256 at most 2^26)", (long long)m,
+                    (long long)k);
     if (!aligned(x, 16) || !aligned(xq, 4)) return fail(QK_ERR_ARG, "x must be 16-byte and xq 4-byte aligned");
     HIP_OK(qk::launch_quantize_q8k(x, m * (k / QK_K), static_cast<uint8_t *>(xq), stream_of(stream)),
            "quantize_q8k launch");
@@ -377,7 +380,10 @@ int hip_quantize_q8_0(const float *x, int64_t m, int64_t k, void *xq, void *stre
     int rc = require_init();
     if (rc) return rc;
     if (!x || !xq) return fail(QK_ERR_ARG, "null pointer");
-    if (m < 1 || k < 1 || k % QK8_0) return fail(QK_ERR_ARG, "bad shape m=%lld k=%lld", (long long)m, (long long)k);
+    // a dispatch counts its work-items in 32 bits: 32 per block
+    if (m < 1 || k < 1 || k % QK8_0 || m > ((int64_t)1 << 27) / (k / QK8_0))
+        return fail(QK_ERR_ARG, "bad shape m=%lld k=%lld (k a multiple of 32, m*k/32 at most 2^27)", (long long)m,
+                    (long long)k);
     if (!aligned(x, 4) || !aligned(xq, 2)) return fail(QK_ERR_ARG, "misaligned x/xq");
     HIP_OK(qk::launch_quantize_q8_0(x, m * (k / QK8_0), static_cast<uint8_t *>(xq), stream_of(stream)),
            "quantize_q8_0 launch");
@@ -465,7 +471,8 @@ int hip_matmul_q8_0(const void *w, int64_t n, int64_t k, const void *xq, int64_t
 static int dequant(int type, const void *w, int64_t nblocks, float *y, void *s) {
     int rc = require_init();
     if (rc) return rc;
-    if (!w || !y || nblocks < 1) return fail(QK_ERR_ARG, "bad dequant arguments");
+    if (!w || !y || nblocks < 1 || nblocks > ((int64_t)1 << 26))   // 64 work-items per block, 32-bit count
+        return fail(QK_ERR_ARG, "bad dequant arguments (nblocks 1..2^26)");
     if (!aligned(y, 16)) return fail(QK_ERR_ARG, "y must be 16-byte aligned");
     if (!aligned(w, 2)) return fail(QK_ERR_ARG, "w must be 2-byte aligned");
     HIP_OK(qk::launch_dequant(type, static_cast<const uint8_t *>(w), nblocks, y, stream_of(s)), "dequant launch");
@@ -481,8 +488,9 @@ int hip_add_rmsnorm_q8k(const float *h, const float *delta, const float *w, floa
     if (rc) return rc;
     if (!h || !w) return fail(QK_ERR_ARG, "null pointer");
     if (!x_out && !xq) return fail(QK_ERR_ARG, "x_out and xq are both NULL");
-    if (m < 1 || m > ((int64_t)1 << 24) || k < 4 || k % 4 || k > QK_NORM_MAX_K)   // one workgroup per row
-        return fail(QK_ERR_ARG, "bad shape m=%lld k=%lld (m at most 2^24, k a multiple of 4, at most %d)",
+    // one 256-thread workgroup per row; a dispatch counts work-items in 32 bits
+    if (m < 1 || m >= ((int64_t)1 << 24) || k < 4 || k % 4 || k > QK_NORM_MAX_K)
+        return fail(QK_ERR_ARG, "bad shape m=%lld k=%lld (m below 2^24, k a multiple of 4, at most %d)",
                     (long long)m, (long long)k, QK_NORM_MAX_K);
     if (xq && k % QK_K) return fail(QK_ERR_ARG, "k=%lld: a Q8_K row needs a multiple of 256", (long long)k);
     if (!aligned(h, 16) || !aligned(delta, 16) || !aligned(w, 16) || !aligned(h_out, 16) || !aligned(x_out, 16) ||
@@ -742,7 +750,8 @@ int register_locked(const void *host_w, int type, int64_t k, int64_t n) {
 int check_weight_args(const void *host_w, int type, int64_t k, int64_t n) {
     if (!host_w) return fail(QK_ERR_ARG, "null weight");
     if (block_bytes(type) == 0) return fail(QK_ERR_UNSUPPORTED, "unsupported tensor type %d", type);
-    if (k < 1 || n < 1 || k % block_elems(type)) return fail(QK_ERR_ARG, "bad weight shape");
+    if (k < 1 || n < 1 || k % block_elems(type) || k > QK_MAX_K || n > 0x7fffffffLL)
+        return fail(QK_ERR_ARG, "bad weight shape n=%lld k=%lld", (long long)n, (long long)k);
     return QK_OK;
 }
 

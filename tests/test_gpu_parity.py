@@ -432,6 +432,12 @@ def test_rejects_bad_shapes(lib):
     assert L.hip_matvec_q8_0(wp, 1, 65536 + 32, xp, yp, None) == 1
     assert L.hip_matmul_q8_0(wp, 1, 65536 + 32, xp, 2, yp, None) == 1
     assert L.hip_matmul_q8_0(wp, 4, 64, xp, 0, yp, None) == 1         # m = 0
+    # grids whose 32-bit work-item count would wrap
+    fp = C.c_void_p(y.data_ptr())
+    assert L.hip_quantize_q8k(fp, (1 << 26) + 1, 256, xp, None) == 1
+    assert L.hip_quantize_q8_0(fp, (1 << 27) + 1, 32, xp, None) == 1
+    assert L.hip_dequant_q4k(wp, (1 << 26) + 1, yp, None) == 1
+    assert L.hip_add_rmsnorm_q8k(fp, None, fp, C.c_float(1e-6), 1 << 24, 256, fp, None, xp, None) == 1
     assert L.hip_matmul_q8_0(wp, 4, 64, xp, 65535 * 32 + 1, yp, None) == 1   # above 65535 token tiles of 32
     assert "m=" in lib.last_error()
     assert L.hip_matvec_q4k(wp, 0, 256, xp, yp, None) == 1           # empty
