@@ -288,7 +288,17 @@ __global__ __launch_bounds__(256) void k_smp_events(const float *logits, int64_t
     __shared__ uint32_t tk_sh;
     const int64_t base = (int64_t)b * sb;
     const int32_t n4 = (nlist + 3) >> 2;
-    for (int32_t j = threadIdx.x; j < n4 * 4; j += 256) keys[j] = j < nlist ? fkey(tops[j]) : 0u;   // 0: below all
+    for (int32_t j0 = threadIdx.x; j0 < n4 * 4; j0 += 256 * 8) {   // eight loads in flight per round
+        uint32_t kv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int32_t j = j0 + 256 * u;
+            kv[u] = j < nlist ? fkey(tops[j]) : 0u;                // 0: below all
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (j0 + 256 * u < n4 * 4) keys[j0 + 256 * u] = kv[u];
+    }
     if (threadIdx.x == 0) nr_sh = 0;
     __syncthreads();
     uint32_t tkey = 0;
@@ -451,16 +461,36 @@ __global__ __launch_bounds__(1024) void k_smp_slots(const float *logits, int64_t
     __shared__ int32_t skip;
     int32_t *byr = reinterpret_cast<int32_t *>(buf);
     const int tid = threadIdx.x;
-    if (tid == 0) {
-        int32_t acc = 0, nf = 0;
-        for (int32_t b = 0; b < nblk; b++) {
-            off[b] = acc;
-            acc += ev_n[b];
-            nf |= nan_flag[b];
+    if (tid < 64) {
+        // event offsets: wave-parallel exclusive scan, lane l owning blocks
+        // 4l .. 4l+3 (every load in flight at once); NaN in the fill
+        const int lane = tid;
+        int32_t nf = 0, c4[4], own = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int32_t b = 4 * lane + q;
+            nf |= b < nblk ? nan_flag[b] : 0;
+            c4[q] = b < nblk ? ev_n[b] : 0;
+            own += c4[q];
         }
-        off[nblk] = acc;
-        skip = nf != 0 || n <= k || acc == 0 || k + acc > SMP_NMAX;
-        if (skip) *ok = 0;
+        const bool nan_fill = __ballot(nf != 0) != 0;
+        int32_t incl = own;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int32_t y = __shfl_up(incl, o);
+            if (lane >= o) incl += y;
+        }
+        int32_t acc = incl - own;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            if (4 * lane + q <= nblk) off[4 * lane + q] = acc;
+            acc += c4[q];
+        }
+        const int32_t total = __builtin_amdgcn_readlane(incl, 63);
+        if (lane == 0) {
+            off[nblk] = total;
+            skip = nan_fill || n <= k || total == 0 || k + total > SMP_NMAX;
+            if (skip) *ok = 0;
+        }
     }
     __syncthreads();
     if (skip) return;                                  // uniform
