@@ -118,18 +118,44 @@ __global__ __launch_bounds__(256) void k_dn_prep(DnArgs a, DnScratch s) {
         dm[i * DN_C + j] = i > j ? qk_expf(__fsub_rn(gcs[i], gcs[j])) : 0.0f;
     }
     const int64_t ho = (int64_t)ck.slot * DN_C;
-    for (int p = first; p < n * kd; p += stride) {
-        const int t = p / kd, d = p % kd;
-        const float b = a.beta[(ck.c0 + t) * a.H + h];
-        const float kbv = __fmul_rn(row_of(a.k, a, ck.c0, t, h, kd)[d], b);
-        const float ge = gex[t];
-        s.kb[(ho + t) * kd + d] = kbv;
-        s.kbg[(ho + t) * kd + d] = __fmul_rn(kbv, ge);
-        s.qg[(ho + t) * kd + d] = __fmul_rn(ge, row_of(a.q, a, ck.c0, t, h, kd)[d]);
+    // the rows in rounds of four elements per thread, every load of a
+    // round in flight before its products (64 x 128 elements: one round)
+    for (int p0 = first; p0 < n * kd; p0 += 4 * stride) {
+        float kv[4], qv[4], bv[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int p = p0 + u * stride, t = p / kd, d = p % kd;
+            const bool in = p < n * kd;
+            kv[u] = in ? row_of(a.k, a, ck.c0, t, h, kd)[d] : 0.0f;
+            qv[u] = in ? row_of(a.q, a, ck.c0, t, h, kd)[d] : 0.0f;
+            bv[u] = in ? a.beta[(ck.c0 + t) * a.H + h] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int p = p0 + u * stride, t = p / kd, d = p % kd;
+            if (p < n * kd) {
+                const float kbv = __fmul_rn(kv[u], bv[u]);
+                const float ge = gex[t];
+                s.kb[(ho + t) * kd + d] = kbv;
+                s.kbg[(ho + t) * kd + d] = __fmul_rn(kbv, ge);
+                s.qg[(ho + t) * kd + d] = __fmul_rn(ge, qv[u]);
+            }
+        }
     }
-    for (int p = first; p < n * vd; p += stride) {
-        const int t = p / vd, e = p % vd;
-        s.vb[(ho + t) * vd + e] = __fmul_rn(row_of(a.v, a, ck.c0, t, h, vd)[e], a.beta[(ck.c0 + t) * a.H + h]);
+    for (int p0 = first; p0 < n * vd; p0 += 4 * stride) {
+        float vv[4], bv[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int p = p0 + u * stride, t = p / vd, e = p % vd;
+            const bool in = p < n * vd;
+            vv[u] = in ? row_of(a.v, a, ck.c0, t, h, vd)[e] : 0.0f;
+            bv[u] = in ? a.beta[(ck.c0 + t) * a.H + h] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int p = p0 + u * stride, t = p / vd, e = p % vd;
+            if (p < n * vd) s.vb[(ho + t) * vd + e] = __fmul_rn(vv[u], bv[u]);
+        }
     }
 }
 
