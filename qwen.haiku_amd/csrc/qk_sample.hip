@@ -390,14 +390,16 @@ __global__ __launch_bounds__(256) void k_smp_events(const float *logits, int64_t
                 key8[m] = lane + 64 * m < nr2 ? rk[lane + 64 * m] : 0u;
                 key8[4 + m] = lane + 64 * m < nc ? fkey(cv[c0 + lane + 64 * m]) : 0u;
             }
+            // bisection; each step's count is eight ballots' popcounts, so
+            // the step is a short scalar chain (0 keys are padding:
+            // cand >= 1)
             uint32_t t = 0;
             for (int bit = 31; bit >= 0; bit--) {
                 const uint32_t cand = t | (1u << bit);
-                int32_t cnt = 0;
+                int32_t cnt = tk >= cand ? k - nr2 : 0;
 #pragma unroll
-                for (int m = 0; m < 8; m++) cnt += key8[m] >= cand;   // 0 keys are padding: cand >= 1
-                if (lane == 0 && tk >= cand) cnt += k - nr2;
-                if (wave_sum_i(cnt) >= k) t = cand;
+                for (int m = 0; m < 8; m++) cnt += __builtin_popcountll(__ballot(key8[m] >= cand));
+                if (cnt >= k) t = cand;
             }
             int32_t nn = 0;                            // R'' = the keys above t, compacted by the wave
 #pragma unroll
