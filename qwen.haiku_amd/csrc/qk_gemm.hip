@@ -1,6 +1,7 @@
 // qk_gemm.hip -- chunked-prefill GEMM over native GGUF K-quant and Q8_0
-// blocks (gfx950, int8 MFMA). The K-quant kernel is described here; the
-// Q8_0 kernel (k_gemm_q80) has its own description further down.
+// blocks (gfx950, int8 MFMA). The K-quant kernel is described here; its
+// 128-token-tile form for long prompts (k_gemm_w) and the Q8_0 kernel
+// (k_gemm_q80) have their own descriptions further down.
 //
 // y[t*n + j] = row_dot(W row j, xq row t): the token loop of
 // tensor_matmul_q{4k,5k,6k}_f32 (slm/tensor.c:838-851, 908-918,
@@ -634,6 +635,149 @@ void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb, const uint8_t *__r
     }
 }
 
+// ---- wide token tiles (Q4_K / Q5_K) ---------------------------------------------
+// For prompts long enough to give many token tiles: a 512-thread workgroup
+// owns 128 tokens x 64 weight rows, and wave w computes the 32x32 sub-tile
+// at tokens 32*(w/2), rows 32*(w%2) over the whole super-block, so no int32
+// parts are exchanged and each weight tile is unpacked once per 128 tokens.
+// Every thread stages a quarter of one activation row and an eighth of one
+// weight row: one 16-byte run of nibbles with both of its sub-blocks' scale
+// digits, and one of the row's eight mins. The arithmetic per output is the
+// 64-token kernel's.
+#define GW_BM 128                     // tokens per wide tile
+
+template <int NP>
+struct __attribute__((aligned(16))) GemmWLds {
+    int8_t a[GW_BM][GM_LD];           // activation quants of the super-block
+    int8_t b[NP][64][GM_LD];          // dequantised int8 weight planes
+    int8_t am[GW_BM][16];             // bsum pairs as two int8 digits
+    float yd[GW_BM];                  // Q8_K d per token
+    uint8_t mn[64][8];                // 6-bit mins
+    float wd[64];                     // fp16 d, widened
+    float wdm[64];                    // fp16 dmin, widened
+};
+
+// Eighth e of a Q4_K / Q5_K weight row: qs run q = e%4 of half e/4 (chunk
+// c = 2*(e/4) + q/2, positions 16*(q&1)..+16), the header, and for Q5_K the
+// qh bytes of those positions. Rows past n (row == nullptr) stage zeros.
+struct WRawE { uint4 hdr, p, qh; };
+
+template <int TYPE>
+__device__ __forceinline__ void load_we(WRawE &a, const uint8_t *row, int e, int i) {
+    a.hdr = a.p = a.qh = make_uint4(0, 0, 0, 0);
+    if (!row) return;
+    const int q = e & 3, half = e >> 2;
+    if constexpr (TYPE == 12) {
+        const uint8_t *p = row + (int64_t)i * Q4K_BYTES;
+        a.hdr = ld16(p);
+        a.p = ld16(p + 16 + 64 * half + 16 * q);
+    } else {
+        const uint8_t *p = row + (int64_t)i * Q5K_BYTES;
+        a.hdr = ld16(p);
+        a.qh = ld16(p + 16 + 16 * (q & 1));
+        a.p = ld16(p + 48 + 64 * half + 16 * q);
+    }
+}
+
+template <int TYPE, typename GL>
+__device__ __forceinline__ void store_we(GL &s, const WRawE &a, int r, int e) {
+    const int q = e & 3, c = 2 * (e >> 2) + (q >> 1), l0 = 16 * (q & 1);
+    if constexpr (TYPE == 12) store_piece4(s, r, c, l0, a.p, a.hdr);
+    else store_piece5(s, r, c, l0, a.p, a.qh, a.hdr);
+    int32_t sc, mm;
+    scale_min(a.hdr.y, a.hdr.z, a.hdr.w, e, sc, mm);
+    s.mn[r][e] = (uint8_t)mm;
+    if (e == 0) s.wd[r] = h2f(a.hdr.x & 0xffffu);
+    if (e == 1) s.wdm[r] = h2f(a.hdr.x >> 16);
+}
+
+template <int TYPE, bool FUSED>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(TYPE == 12 ? 4 : 2)))
+void k_gemm_w(const uint8_t *__restrict__ w, int64_t n, int nb, const uint8_t *__restrict__ xq, int64_t m,
+              float *__restrict__ y) {
+    constexpr int NP = Planes<TYPE>::n;
+    constexpr int BB = TYPE == 12 ? Q4K_BYTES : Q5K_BYTES;
+    __shared__ GemmWLds<NP> s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, h = lane >> 5;
+    const int tm = 32 * (wave >> 1), tn = 32 * (wave & 1);
+    const int64_t r0 = (int64_t)blockIdx.x * 64, t0 = (int64_t)blockIdx.y * GW_BM;
+    const int at = tid >> 2, aq = tid & 3;                   // activation row, quarter
+    const int wt = tid >> 3, we = tid & 7;                   // weight row, eighth
+    // activation rows of this token tile: one buffer of at most 128 x 256 x
+    // 292 bytes, so every offset is 32-bit; rows past m read zeros
+    const int mrows = (m - t0 < GW_BM) ? (int)(m - t0) : GW_BM;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(xq + t0 * nb * Q8K_BYTES), 0, mrows * nb * Q8K_BYTES, 0x00020000);
+    const int xoff = at * nb * Q8K_BYTES;
+    const uint8_t *wrow = r0 + wt < n ? w + (r0 + wt) * nb * BB : nullptr;
+
+    ActRaw ar;
+    WRawE wr;
+    load_act(ar, xr, xoff, aq, 0);
+    load_we<TYPE>(wr, wrow, we, 0);
+    const int8_t *arow = &s.a[tm + col][0];
+    const v16i zero = {0};
+    float sum[16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) sum[v] = 0.0f;
+    for (int i = 0; i < nb; i++) {
+        lds_barrier();                                       // previous super-block's reads done
+        store_act(s, ar, at, aq);
+        store_we<TYPE>(s, wr, wt, we);
+        if (i + 1 < nb) {                                    // next super-block in flight during compute
+            load_act(ar, xr, xoff, aq, i + 1);
+            load_we<TYPE>(wr, wrow, we, i + 1);
+        }
+        lds_barrier();
+        // one accumulation chain per digit plane over the super-block
+        v16i acc[NP];
+#pragma unroll
+        for (int pl = 0; pl < NP; pl++) acc[pl] = zero;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const v4i av = *(const QK_LDS v4i *)(arow + 32 * c + 16 * h);
+#pragma unroll
+            for (int pl = 0; pl < NP; pl++) {
+                const v4i bv = *(const QK_LDS v4i *)(&s.b[pl][tn + col][32 * c + 16 * h]);
+                acc[pl] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, acc[pl], 0, 0, 0);
+            }
+        }
+        int32_t is[16];
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            is[v] = acc[0][v] + 8 * acc[1][v];
+            if constexpr (NP == 3) is[v] += 16 * acc[2][v];
+        }
+        // isum_mins as two small MFMAs (bsum pair digits lo | hi against the
+        // mins: mins = lo_product + 128 * hi_product exactly)
+        const long amv = *(const QK_LDS long *)&s.am[tm + col][8 * h];
+        const long mnv = *(const QK_LDS long *)&s.mn[tn + col][0];
+        const v16i dl = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 0 ? mnv : 0L, zero, 0, 0, 0);
+        const v16i dh = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 1 ? mnv : 0L, zero, 0, 0, 0);
+        const float wd = s.wd[tn + col], wdm = s.wdm[tn + col];
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int32_t mins = dl[v] + dh[v] * 128;
+            const float yd = s.yd[tm + tok_of(v, h)];
+            const float d = __fmul_rn(yd, wd);
+            const float dmin = __fmul_rn(yd, wdm);
+            const float pm = __fmul_rn(dmin, (float)mins);
+            const float term =
+                FUSED ? __builtin_fmaf(d, (float)is[v], -pm) : __fsub_rn(__fmul_rn(d, (float)is[v]), pm);
+            sum[v] = __fadd_rn(sum[v], term);
+        }
+    }
+    const int64_t row = r0 + tn + col;
+    if (row < n) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int64_t t = t0 + tm + tok_of(v, h);
+            if (t < m) __builtin_nontemporal_store(FUSED ? bcast8(sum[v]) : sum[v], &y[t * n + row]);
+        }
+    }
+}
+
 // ---- Q8_0 x Q8_0 --------------------------------------------------------------
 // The token loop of tensor_matmul_q8_0_f32 (slm/tensor.c:952-981) over
 // q8_0_dot_q8_0 (simd/avx.c:65-158, simd/quants.h:244-256). Per 32-element
@@ -839,6 +983,23 @@ hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, const u
         return hipGetLastError();
     }
     const int nb = (int)(k / QK_K);
+    if (type == 12 || type == 13) {
+        // 128-token tiles once they give at least three quarters of the CUs
+        // a workgroup (at N = 3584, K = 1024: faster from 224 tiles on,
+        // slower at 112)
+        const unsigned mtw = (unsigned)((m + GW_BM - 1) / GW_BM);
+        if ((uint64_t)((n + 63) / 64) * mtw >= 192) {
+            const dim3 grid((unsigned)((n + 63) / 64), mtw);
+            if (type == 12) {
+                if (fused) hipLaunchKernelGGL((k_gemm_w<12, true>), grid, dim3(512), 0, s, w, n, nb, xq, m, y);
+                else hipLaunchKernelGGL((k_gemm_w<12, false>), grid, dim3(512), 0, s, w, n, nb, xq, m, y);
+            } else {
+                if (fused) hipLaunchKernelGGL((k_gemm_w<13, true>), grid, dim3(512), 0, s, w, n, nb, xq, m, y);
+                else hipLaunchKernelGGL((k_gemm_w<13, false>), grid, dim3(512), 0, s, w, n, nb, xq, m, y);
+            }
+            return hipGetLastError();
+        }
+    }
     const unsigned mt = (unsigned)((m + GM_BM - 1) / GM_BM);
     // 64-row tiles when they alone give every CU a workgroup, else 32-row
     // tiles (twice the workgroups, k split four ways)

@@ -184,6 +184,9 @@ GEMM_SHAPES = [
     # 32-row tiles with a four-way k split
     (13, 4096, 1024, 512), (14, 4096, 1024, 300), (12, 4160, 512, 260),
     (12, 40, 65536, 9), (14, 33, 25600, 3),                                  # k up to the limit
+    # 128-token tiles (at least 192 of them) with partial row and token
+    # tiles, and a single super-block
+    (12, 4100, 512, 300), (13, 3000, 256, 520),
     # Q8_0: config 1's matrix and the model's ssm_alpha / ssm_beta at a
     # 512-token prompt; a step of one block (65 = 8 * 8 + 1); partial row
     # and token tiles; one block; k at the limit
