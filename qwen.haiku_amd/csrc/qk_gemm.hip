@@ -985,10 +985,13 @@ hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, const u
     const int nb = (int)(k / QK_K);
     if (type == 12 || type == 13) {
         // 128-token tiles once they give at least three quarters of the CUs
-        // a workgroup (at N = 3584, K = 1024: faster from 224 tiles on,
-        // slower at 112)
+        // a workgroup. Q4_K (two workgroups per CU) at N = 3584, K = 1024:
+        // faster at 224 to 896 tiles, slower at 112. Q5_K's three planes
+        // leave room for one workgroup per CU, so its tiles must fit one
+        // round: faster at 224 (14.2 -> 12.7 us), slower at 336 and 896.
         const unsigned mtw = (unsigned)((m + GW_BM - 1) / GW_BM);
-        if ((uint64_t)((n + 63) / 64) * mtw >= 192) {
+        const uint64_t tiles = (uint64_t)((n + 63) / 64) * mtw;
+        if (tiles >= 192 && (type == 12 || tiles <= 256)) {
             const dim3 grid((unsigned)((n + 63) / 64), mtw);
             if (type == 12) {
                 if (fused) hipLaunchKernelGGL((k_gemm_w<12, true>), grid, dim3(512), 0, s, w, n, nb, xq, m, y);

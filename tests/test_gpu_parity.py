@@ -180,9 +180,12 @@ GEMM_SHAPES = [
     (13, 2048, 1024, 96), (13, 1024, 2048, 33),
     (12, 100, 768, 37), (13, 65, 256, 1), (14, 63, 512, 65), (14, 129, 1280, 7),
     (12, 64, 256, 64), (12, 1, 512, 3),
-    # 64-row tiles (at least 256 of them) for every type; the others run
-    # 32-row tiles with a four-way k split
+    # 64-row tiles for every type: 64-token tiles (at least 256 of them,
+    # fewer than 192 128-token tiles, or more than 256 for Q5_K), else
+    # 128-token tiles (Q4_K / Q5_K); the others run 32-row tiles with a
+    # four-way k split
     (13, 4096, 1024, 512), (14, 4096, 1024, 300), (12, 4160, 512, 260),
+    (12, 8256, 256, 128), (13, 2112, 256, 1100),
     (12, 40, 65536, 9), (14, 33, 25600, 3),                                  # k up to the limit
     # 128-token tiles (at least 192 of them) with partial row and token
     # tiles, and a single super-block
