@@ -35,6 +35,10 @@
 extern "C" {
 #endif
 
+/* libqk is built with hidden visibility; the entry points declared here
+ * are the only names it exports into the host process. */
+#pragma GCC visibility push(default)
+
 /* Super-block / block sizes, simd/quants.h:30-31. */
 #define QK_K  256
 #define QK8_0 32
@@ -89,7 +93,8 @@ enum {
     QK_ERR_NOT_INIT     = 3,   /* hip_qk_init not called / failed      */
     QK_ERR_UNREGISTERED = 4,   /* host weight pointer not registered   */
     QK_ERR_NOMEM        = 5,
-    QK_ERR_UNSUPPORTED  = 6    /* tensor type not on this path         */
+    QK_ERR_UNSUPPORTED  = 6    /* tensor type not on this path, or the */
+                               /* host libm expf is not the FMA build  */
 };
 
 /* CPU dispatch tiers whose float epilogue the kernels reproduce
@@ -292,8 +297,11 @@ int hip_lmhead_q6k_argmax_topk(const void *w, int64_t n, int64_t k,
  * process ends. With logits == NULL, n is at most QK_NOALLOC_MAX_N.
  * Every call on one GPU shares that array, whichever stream it uses:
  * calls that overlap in time on one GPU race, so keep them on one stream
- * or order them. Same arguments and results as
- * hip_lmhead_q6k_argmax_topk. */
+ * or order them. An eager call from another stream while the previous
+ * eager call is still in flight fails with QK_ERR_ARG and enqueues
+ * nothing; calls captured into graphs are not tracked, so graphs that
+ * hold this call must be replayed in order. Same arguments and results
+ * as hip_lmhead_q6k_argmax_topk. */
 #define QK_NOALLOC_MAX_N 262144
 int hip_lmhead_q6k_argmax_topk_noalloc(const void *w, int64_t n, int64_t k,
                                        const void *xq, int topk,
@@ -409,6 +417,8 @@ int hip_qk_lmhead_host(const void *host_w, int64_t n, int64_t k,
                        const float *x, int topk, float *logits,
                        int32_t *argmax, int32_t *topk_idx,
                        float *topk_val);
+
+#pragma GCC visibility pop
 
 #ifdef __cplusplus
 }

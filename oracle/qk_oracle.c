@@ -583,18 +583,14 @@ void qko_rng_seed(uint64_t seed, uint64_t *st) {
     if (st[0] == 0 && st[1] == 0) st[0] = 1;
 }
 
-/* One sampling step of slm_generate_raw (slm/slm.c:309-322): the ids in
- * mask (eos / eot while fewer than min_new tokens exist) set to -inf,
- * then sample_with (slm/sampler.c:134-181): repetition penalty in place
+/* sample_with (slm/sampler.c:134-181): repetition penalty in place
  * (:49-63), greedy argmax when temperature <= 0, else topk_collect
  * (:70-93), topk_softmax (:97-111), topk_sort_desc (:116-129), top-p,
  * min-p and the roulette pick with one uniform draw. logits are modified
  * in place; st (2 words) advances on the sampling path only. */
-int32_t qko_sample(float *logits, int64_t n, float temperature, int32_t top_k, float top_p, float min_p,
-                   float penalty, int32_t window, uint64_t *st, const int32_t *history, int32_t hist_n,
-                   const int32_t *mask, int32_t n_mask) {
-    for (int32_t i = 0; i < n_mask; i++)
-        if (mask[i] >= 0 && mask[i] < n) logits[mask[i]] = -INFINITY;
+static int32_t sample_with_core(float *logits, int64_t n, float temperature, int32_t top_k, float top_p,
+                                float min_p, float penalty, int32_t window, uint64_t *st, const int32_t *history,
+                                int32_t hist_n) {
     if (penalty != 1.0f && hist_n != 0) {
         int32_t start = (window > 0 && window < hist_n) ? hist_n - window : 0;
         for (int32_t i = start; i < hist_n; i++) {
@@ -659,6 +655,27 @@ int32_t qko_sample(float *logits, int64_t n, float temperature, int32_t top_k, f
         if (u <= c) { picked = j; break; }
     }
     return idx[picked];
+}
+
+/* One sampling step of slm_generate_raw (slm/slm.c:309-333): each id in
+ * mask (eos / eot while fewer than min_new tokens exist) has its value
+ * saved and is set to -inf, in mask order; then sample_with; then the
+ * saved values go back in mask order, so an id masked twice ends at the
+ * second save, -inf. */
+int32_t qko_sample(float *logits, int64_t n, float temperature, int32_t top_k, float top_p, float min_p,
+                   float penalty, int32_t window, uint64_t *st, const int32_t *history, int32_t hist_n,
+                   const int32_t *mask, int32_t n_mask) {
+    float saved[n_mask > 0 ? n_mask : 1];
+    for (int32_t i = 0; i < n_mask; i++)
+        if (mask[i] >= 0 && mask[i] < n) {
+            saved[i] = logits[mask[i]];
+            logits[mask[i]] = -INFINITY;
+        }
+    const int32_t tok = sample_with_core(logits, n, temperature, top_k, top_p, min_p, penalty, window, st, history,
+                                         hist_n);
+    for (int32_t i = 0; i < n_mask; i++)
+        if (mask[i] >= 0 && mask[i] < n) logits[mask[i]] = saved[i];
+    return tok;
 }
 
 /* ---- chunked Gated DeltaNet ------------------------------------------- */

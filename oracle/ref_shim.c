@@ -346,9 +346,10 @@ int ref_swiglu(int64_t n, const float *gate, const float *up, float *act) {
 }
 
 /* sample_with (slm/sampler.c:134) on a 1-D view of logits (modified in
- * place, as the reference does), after the min_new masking of
- * slm_generate_raw (slm/slm.c:309-322); st holds struct rng's two words
- * and is advanced. rng_seed (slm/model.c:431) for the tests' seeds. */
+ * place, as the reference does), between the min_new masking of
+ * slm_generate_raw and its restore of the masked values
+ * (slm/slm.c:309-333); st holds struct rng's two words and is advanced.
+ * rng_seed (slm/model.c:431) for the tests' seeds. */
 int32_t ref_sample(float *logits, int64_t n, float temperature, int32_t top_k, float top_p, float min_p,
                    float penalty, int32_t window, uint64_t *st, const int32_t *history, int32_t hist_n,
                    const int32_t *mask, int32_t n_mask) {
@@ -360,14 +361,20 @@ int32_t ref_sample(float *logits, int64_t n, float temperature, int32_t top_k, f
     sp.min_p = min_p;
     sp.repetition_penalty = penalty;
     sp.repetition_window = window;
+    float saved[n_mask > 0 ? n_mask : 1];
     for (int32_t i = 0; i < n_mask; i++)
-        if (mask[i] >= 0 && mask[i] < n) logits[mask[i]] = -INFINITY;
+        if (mask[i] >= 0 && mask[i] < n) {
+            saved[i] = logits[mask[i]];
+            logits[mask[i]] = -INFINITY;
+        }
     struct rng r;
     r.s0 = st[0];
     r.s1 = st[1];
     int32_t tok = sample_with(&t, &sp, &r, history, hist_n);
     st[0] = r.s0;
     st[1] = r.s1;
+    for (int32_t i = 0; i < n_mask; i++)
+        if (mask[i] >= 0 && mask[i] < n) logits[mask[i]] = saved[i];
     return tok;
 }
 

@@ -23,6 +23,10 @@
 #include "../../include/qk.h"
 #include "qk_kernels.h"
 
+#include <cmath>
+#define QK_EXPF_HOST 1                         // qk_expf on the host, for host_expf_ok
+#include "qk_expf.h"
+
 namespace {
 
 thread_local std::string g_err;
@@ -107,6 +111,13 @@ constexpr size_t NOALLOC_SCRATCH_BYTES = NOALLOC_SEL_BYTES + (size_t)QK_NOALLOC_
 static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
 constexpr int MAX_DEVICES = 64;
 void *g_noalloc[MAX_DEVICES];             // each device's `scratch`, set by hip_qk_init
+// The last eager call of each device: its stream and an event recorded
+// after it (created by hip_qk_init), so a call from another stream while
+// that one is still in flight fails instead of racing on `scratch`.
+std::mutex g_noalloc_mu;
+hipEvent_t g_noalloc_ev[MAX_DEVICES];
+hipStream_t g_noalloc_last[MAX_DEVICES];
+bool g_noalloc_pending[MAX_DEVICES];
 
 // detect_cpu + simd_init tier selection, simd/simd.c:142-170,208-229.
 int detect_tier() {
@@ -128,6 +139,41 @@ int detect_tier() {
 }
 
 int fused_of(int tier) { return (tier == QK_TIER_AVX2 || tier == QK_TIER_AVXVNNI) ? 1 : 0; }
+
+// The SiLU, softmax and DeltaNet gates of the reference call the host
+// libm expf, and glibc picks one of two builds of it per CPU (fused
+// multiply-adds on hosts with FMA and AVX2). The device implements the
+// fused build (qk_expf.h). The builds differ on exactly two float inputs;
+// this compares the host's expf with the restatement there, so it sees
+// whichever build the process's libm dispatched to (tunables included).
+bool host_expf_ok() {
+    static const bool ok = [] {
+        static const uint32_t probe[2] = {0x4202422fu, 0xc27c65d9u};
+        for (uint32_t b : probe) {
+            volatile uint32_t vb = b;                  // keep the compiler from folding expf
+            float x;
+            const uint32_t bb = vb;
+            std::memcpy(&x, &bb, 4);
+            const float h = std::exp(x), d = qk_expf(x);
+            uint32_t hb, db;
+            std::memcpy(&hb, &h, 4);
+            std::memcpy(&db, &d, 4);
+            if (hb != db) return false;
+        }
+        return true;
+    }();
+    return ok;
+}
+
+// Entry points whose kernels call expf: refused (before anything else,
+// so the refusal shows on any host) when the host libm is the other build.
+int require_host_expf(const char *what) {
+    if (host_expf_ok()) return QK_OK;
+    return fail(QK_ERR_UNSUPPORTED,
+                "%s needs expf, and this host's libm expf is not the fused (FMA) build that the device "
+                "reproduces: results would differ from the reference on this host",
+                what);
+}
 
 hipStream_t stream_of(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
@@ -309,12 +355,15 @@ int hip_qk_init(int device) {
     if (device < MAX_DEVICES && !g_noalloc[device]) {
         void *p = nullptr;
         HIP_OK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        HIP_OK(hipEventCreateWithFlags(&g_noalloc_ev[device], hipEventDisableTiming), "hipEventCreate(noalloc)");
         g_noalloc[device] = p;
     }
     s.device = device;
     s.cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     s.tier.store(detect_tier());
-    s.label = std::string(prop.gcnArchName) + " " + prop.name + " / tier " + hip_qk_tier_label(s.tier.load());
+    char label[512];
+    snprintf(label, sizeof label, "%s %s / tier %s", prop.gcnArchName, prop.name, hip_qk_tier_label(s.tier.load()));
+    s.label = label;
     s.gen.fetch_add(1);
     t_dev_gen = s.gen.load();
     s.init = true;
@@ -504,7 +553,9 @@ int hip_add_rmsnorm_q8k(const float *h, const float *delta, const float *w, floa
 }
 
 int hip_silu_f32(const float *x, int64_t n, float *y, void *stream) {
-    int rc = require_init();
+    int rc = require_host_expf("hip_silu_f32");
+    if (rc) return rc;
+    rc = require_init();
     if (rc) return rc;
     if (!x || !y || n < 1) return fail(QK_ERR_ARG, "bad silu arguments");
     if (!aligned(x, 4) || !aligned(y, 4)) return fail(QK_ERR_ARG, "x/y misaligned");
@@ -513,7 +564,9 @@ int hip_silu_f32(const float *x, int64_t n, float *y, void *stream) {
 }
 
 int hip_swiglu_q8k(const float *gate, const float *up, int64_t m, int64_t k, float *act, void *xq, void *stream) {
-    int rc = require_init();
+    int rc = require_host_expf("hip_swiglu_q8k");
+    if (rc) return rc;
+    rc = require_init();
     if (rc) return rc;
     if (!gate || !up) return fail(QK_ERR_ARG, "null pointer");
     if (!act && !xq) return fail(QK_ERR_ARG, "act and xq are both NULL");
@@ -649,15 +702,18 @@ int hip_lmhead_q6k_argmax_topk(const void *w, int64_t n, int64_t k, const void *
 
 int hip_sample(float *logits, int64_t n, const qk_sampler *sp, uint64_t *rng, const int32_t *history,
                int32_t hist_n, const int32_t *mask, int32_t n_mask, int32_t *token, void *stream) {
-    int rc = require_init();
-    if (rc) return rc;
+    int rc;
+    // the softmax of every non-greedy pick (a NaN temperature is not
+    // greedy, slm/sampler.c:140) exponentiates
+    if (sp && !(sp->temperature <= 0.0f) && (rc = require_host_expf("hip_sample"))) return rc;
+    if ((rc = require_init())) return rc;
     if (!logits || !sp || !token) return fail(QK_ERR_ARG, "null pointer");
     if (n < 1 || n > QK_SAMPLE_MAX_N) return fail(QK_ERR_ARG, "n=%lld logits (1..%d)", (long long)n, QK_SAMPLE_MAX_N);
     if (hist_n < 0 || (hist_n > 0 && !history)) return fail(QK_ERR_ARG, "history of %d tokens", hist_n);
     if (n_mask < 0 || n_mask > QK_SAMPLE_MAX_MASK || (n_mask > 0 && !mask))
         return fail(QK_ERR_ARG, "n_mask=%d (0..%d)", n_mask, QK_SAMPLE_MAX_MASK);
-    if (sp->temperature > 0.0f && (!rng || !aligned(rng, 8)))
-        return fail(QK_ERR_ARG, "sampling needs the 8-byte aligned rng state");
+    if (!(sp->temperature <= 0.0f) && (!rng || !aligned(rng, 8)))
+        return fail(QK_ERR_ARG, "sampling (temperature > 0 or NaN) needs the 8-byte aligned rng state");
     if (!aligned(logits, 4) || !aligned(token, 4) || !aligned(history, 4))
         return fail(QK_ERR_ARG, "misaligned logits/token/history");
     int32_t k = sp->top_k > 0 ? sp->top_k : QK_TOPK_MAX;    // slm/sampler.c:143-144
@@ -673,7 +729,9 @@ int hip_sample(float *logits, int64_t n, const qk_sampler *sp, uint64_t *rng, co
 
 int hip_deltanet_chunked(const float *q, const float *k, const float *v, const float *g_log, const float *beta,
                          int64_t n_tok, int n_heads, int k_hd, int v_hd, float *state, float *out, void *stream) {
-    int rc = require_init();
+    int rc = require_host_expf("hip_deltanet_chunked");
+    if (rc) return rc;
+    rc = require_init();
     if (rc) return rc;
     if (!q || !k || !v || !g_log || !beta || !state || !out) return fail(QK_ERR_ARG, "null pointer");
     if (n_tok < 1 || n_tok > 0x7fffffffLL || n_heads < 1 || n_heads > 1024 || k_hd < 1 || v_hd < 1 ||
@@ -683,16 +741,21 @@ int hip_deltanet_chunked(const float *q, const float *k, const float *v, const f
     if (!aligned(q, 4) || !aligned(k, 4) || !aligned(v, 4) || !aligned(g_log, 4) || !aligned(beta, 4) ||
         !aligned(state, 4) || !aligned(out, 4))
         return fail(QK_ERR_ARG, "misaligned float arrays");
-    {   // out is written while later phases still read the inputs and the state
+    {   // out and the state are written while later phases and other
+        // workgroups still read the inputs (and out, the state)
         const size_t nq = (size_t)n_tok * n_heads * k_hd * 4, nv = (size_t)n_tok * n_heads * v_hd * 4;
         const size_t ng = (size_t)n_tok * n_heads * 4, ns = (size_t)n_heads * k_hd * v_hd * 4;
-        auto overlap = [&](const void *a, size_t na) {
-            const uintptr_t x = reinterpret_cast<uintptr_t>(out), y = reinterpret_cast<uintptr_t>(a);
-            return x < y + na && y < x + nv;
+        auto overlap = [](const void *o, size_t no, const void *a, size_t na) {
+            const uintptr_t x = reinterpret_cast<uintptr_t>(o), y = reinterpret_cast<uintptr_t>(a);
+            return x < y + na && y < x + no;
         };
-        if (overlap(q, nq) || overlap(k, nq) || overlap(v, nv) || overlap(g_log, ng) || overlap(beta, ng) ||
-            overlap(state, ns))
+        auto hits_input = [&](const void *o, size_t no) {
+            return overlap(o, no, q, nq) || overlap(o, no, k, nq) || overlap(o, no, v, nv) ||
+                   overlap(o, no, g_log, ng) || overlap(o, no, beta, ng);
+        };
+        if (hits_input(out, nv) || overlap(out, nv, state, ns))
             return fail(QK_ERR_ARG, "out overlaps an input or the state");
+        if (hits_input(state, ns)) return fail(QK_ERR_ARG, "state overlaps an input");
     }
     void *scratch = nullptr;
     if ((rc = stream_scratch(stream_of(stream), qk::deltanet_scratch_bytes(n_heads, k_hd, v_hd, n_tok), &scratch)))
@@ -719,12 +782,35 @@ int hip_lmhead_q6k_argmax_topk_noalloc(const void *w, int64_t n, int64_t k, cons
     if (lmhead_scratch_bytes(n, topk, logits == nullptr) > NOALLOC_SCRATCH_BYTES ||
         qk::lmhead_cand_bytes(n, topk) > NOALLOC_SEL_BYTES)
         return fail(QK_ERR_ARG, "static scratch too small for n=%lld", (long long)n);
+    // Every call on this GPU shares `scratch`. An eager call from another
+    // stream than the last one, while the last one is still in flight,
+    // would race on it: refused. (Calls captured into a graph are not
+    // tracked; their replays must be ordered by the caller.)
+    const hipStream_t sm = stream_of(stream);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(sm, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (!capturing && g_noalloc_pending[dev] && g_noalloc_last[dev] != sm &&
+        hipEventQuery(g_noalloc_ev[dev]) == hipErrorNotReady)
+        return fail(QK_ERR_ARG,
+                    "the previous allocation-free LM head call on this GPU, on another stream, is still in flight: "
+                    "both share one static scratch array; order the calls or keep them on one stream");
     // the kernels clear their own counter; nothing else must start at zero
-    return lmhead_launch(w, n, k, xq, topk, logits, argmax, topk_idx, topk_val, p, stream_of(stream));
+    if ((rc = lmhead_launch(w, n, k, xq, topk, logits, argmax, topk_idx, topk_val, p, sm))) return rc;
+    if (!capturing) {
+        HIP_OK(hipEventRecord(g_noalloc_ev[dev], sm), "hipEventRecord(noalloc)");
+        g_noalloc_last[dev] = sm;
+        g_noalloc_pending[dev] = true;
+    }
+    return QK_OK;
 }
+
+}  // extern "C"
 
 // ---- host seam ---------------------------------------------------------------
 
+// Helpers of the seam entry points: C++ linkage and internal to this
+// file, so libqk exports none of their names into the host process.
 namespace {
 // Caller holds s.wmu exclusively.
 int register_locked(const void *host_w, int type, int64_t k, int64_t n) {
@@ -779,6 +865,8 @@ int acquire_weight(const void *host_w, int type, int64_t k, int64_t n, std::shar
     return fail(QK_ERR_UNREGISTERED, "weight %p was unregistered during the call", host_w);
 }
 }  // namespace
+
+extern "C" {
 
 int hip_qk_register_weight(const void *host_w, int type, int64_t k, int64_t n) {
     int rc = require_init();
@@ -943,7 +1031,9 @@ int hip_qk_lmhead_host(const void *host_w, int64_t n, int64_t k, const float *x,
 
 int hip_qk_deltanet_host(int n, int k_hd, int v_hd, const float *q, const float *k, const float *v,
                          const float *g_log, const float *beta, float *state, float *out) {
-    int rc = require_init();
+    int rc = require_host_expf("hip_qk_deltanet_host");
+    if (rc) return rc;
+    rc = require_init();
     if (rc) return rc;
     if (!q || !k || !v || !g_log || !beta || !state || !out) return fail(QK_ERR_ARG, "null pointer");
     if (n < 1 || n > 64 || k_hd < 1 || v_hd < 1 || k_hd > QK_DELTANET_MAX_HD || v_hd > QK_DELTANET_MAX_HD)
@@ -954,7 +1044,9 @@ int hip_qk_deltanet_host(int n, int k_hd, int v_hd, const float *q, const float 
 
 int hip_qk_deltanet_layer_host(int64_t n_tok, int n_heads, int k_hd, int v_hd, const float *q, const float *k,
                                const float *v, const float *g_log, const float *beta, float *state, float *out) {
-    int rc = require_init();
+    int rc = require_host_expf("hip_qk_deltanet_layer_host");
+    if (rc) return rc;
+    rc = require_init();
     if (rc) return rc;
     if (!q || !k || !v || !g_log || !beta || !state || !out) return fail(QK_ERR_ARG, "null pointer");
     if (n_tok < 1 || n_tok > 0x7fffffffLL || n_heads < 1 || n_heads > 1024 || k_hd < 1 || v_hd < 1 ||

@@ -14,12 +14,16 @@
  * final rounding to float. glibc ships two builds of that code and x86
  * hosts with FMA (every AVX2 / AVX-VNNI machine) dispatch to the one whose
  * multiply-adds are fused; this header is that form. Checked against the
- * host expf over all 2^32 inputs (tests/test_oracle.py builds it on the
- * CPU); the table entries are pinned there to the correctly rounded
- * 2^(i/32).
+ * host expf over all 2^32 inputs (tests/test_chain_oracle.py builds it on
+ * the CPU); the table entries are pinned there to the correctly rounded
+ * 2^(i/32). The two glibc builds differ on exactly two float inputs,
+ * 0x4202422f and 0xc27c65d9 (scanned over all 2^32 with the unfused form
+ * of this code); libqk's host side evaluates the host expf there and
+ * refuses the entry points that need expf when it is not the fused build.
  *
- * Compiled as device code inside the HIP sources and as plain C by the
- * CPU check.
+ * Compiled as device code inside the HIP sources, as host code when
+ * QK_EXPF_HOST is defined (the check above), and as plain C by the CPU
+ * check.
  */
 #ifndef QK_EXPF_H
 #define QK_EXPF_H
@@ -27,7 +31,7 @@
 #include <stdint.h>
 #include <string.h>
 
-#if defined(__HIP__)
+#if defined(__HIP__) && !defined(QK_EXPF_HOST)
 #define QK_EXPF_FN __device__ static inline
 #define QK_EXPF_DATA __device__ static const
 #else

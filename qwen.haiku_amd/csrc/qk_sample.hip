@@ -96,12 +96,20 @@ __device__ __forceinline__ void penalty_entry(float *logits, int64_t n, const in
 // staged in LDS) the penalty.
 __global__ __launch_bounds__(256) void k_smp_penalty(float *logits, int64_t n, const int32_t *history,
                                                      int32_t start, int32_t hist_n, float penalty, int32_t m0,
-                                                     int32_t m1, int32_t n_mask) {
+                                                     int32_t m1, int32_t n_mask, float *saved) {
     __shared__ int32_t hw[SMP_HIST_LDS];
-    if ((int)threadIdx.x < n_mask) {
-        const int32_t t = threadIdx.x ? m1 : m0;
-        if (t >= 0 && t < n) logits[t] = -__builtin_inff();
+    // the min_new masks in the reference's order, each value saved first
+    // (a repeated id saves the -inf the first mask left)
+    if (threadIdx.x == 0) {
+        for (int32_t i = 0; i < n_mask; i++) {
+            const int32_t t = i ? m1 : m0;
+            if (t >= 0 && t < n) {
+                saved[i] = logits[t];
+                logits[t] = -__builtin_inff();
+            }
+        }
     }
+    __syncthreads();
     const int32_t w = hist_n - start;
     if (w > SMP_HIST_LDS) return;                      // k_smp_penalty_wide takes it
     for (int32_t i = threadIdx.x; i < w; i += 256) hw[i] = history[start + i];
@@ -162,8 +170,22 @@ __global__ __launch_bounds__(256) void k_smp_argmax_part(const float *logits, in
     if (threadIdx.x == 0) part[blockIdx.x] = ArgPart{bv, bi};
 }
 
-__global__ __launch_bounds__(256) void k_smp_argmax_final(const float *logits, const ArgPart *part, int32_t nblk,
-                                                          int32_t *token) {
+// After the pick, the masked ids get their saved values back in mask
+// order, as slm_generate_raw restores eos / eot after sample_with
+// (slm/slm.c:324-333); an id masked twice ends at the second save, -inf.
+struct SmpMask {
+    int32_t m0, m1, n;
+};
+
+__device__ __forceinline__ void restore_masks(float *logits, int64_t n, SmpMask mk, const float *saved) {
+    for (int32_t i = 0; i < mk.n; i++) {
+        const int32_t t = i ? mk.m1 : mk.m0;
+        if (t >= 0 && t < n) logits[t] = saved[i];
+    }
+}
+
+__global__ __launch_bounds__(256) void k_smp_argmax_final(float *logits, int64_t n, const ArgPart *part, int32_t nblk,
+                                                          int32_t *token, SmpMask mk, const float *saved) {
     __shared__ ArgPart sh[4];
     float bv = 0.0f;
     int32_t bi = -1;
@@ -172,6 +194,7 @@ __global__ __launch_bounds__(256) void k_smp_argmax_final(const float *logits, c
     if (threadIdx.x == 0) {
         const float v0 = logits[0];
         *token = (v0 != v0 || bi < 0) ? 0 : bi;
+        restore_masks(logits, n, mk, saved);
     }
 }
 
@@ -701,10 +724,10 @@ __device__ void chain_literal(float *val, int32_t *idx, int32_t filled, const Sm
     *token = idx[picked];
 }
 
-__global__ __launch_bounds__(64) void k_smp_finish(const float *logits, int64_t n, SmpArgs a, const int32_t *ev_idx,
-                                                   const float *ev_val, const int32_t *ev_n, const int32_t *nan_flag,
-                                                   const float *res_val, const int32_t *res_idx,
-                                                   const int32_t *res_ok, uint64_t *rng, int32_t *token) {
+__device__ __forceinline__ void smp_finish(const float *logits, int64_t n, SmpArgs a, const int32_t *ev_idx,
+                                           const float *ev_val, const int32_t *ev_n, const int32_t *nan_flag,
+                                           const float *res_val, const int32_t *res_idx, const int32_t *res_ok,
+                                           uint64_t *rng, int32_t *token) {
     __shared__ float val[SMP_KMAX];
     __shared__ int32_t idx[SMP_KMAX];
     __shared__ int32_t off[SMP_KMAX + 1];              // event offsets per block (nblk <= 256)
@@ -905,6 +928,17 @@ __global__ __launch_bounds__(64) void k_smp_finish(const float *logits, int64_t 
     }
 }
 
+// The pick, then lane 0 (which wrote the token on every path) puts the
+// masked ids back.
+__global__ __launch_bounds__(64) void k_smp_finish(float *logits, int64_t n, SmpArgs a, const int32_t *ev_idx,
+                                                   const float *ev_val, const int32_t *ev_n, const int32_t *nan_flag,
+                                                   const float *res_val, const int32_t *res_idx,
+                                                   const int32_t *res_ok, uint64_t *rng, int32_t *token, SmpMask mk,
+                                                   const float *saved) {
+    smp_finish(logits, n, a, ev_idx, ev_val, ev_n, nan_flag, res_val, res_idx, res_ok, rng, token);
+    if (threadIdx.x == 0) restore_masks(logits, n, mk, saved);
+}
+
 // ---- launcher -------------------------------------------------------------------
 // Block size: the smallest power of two >= 1024 with nblk * k within the
 // LDS list budget (n <= QK_SAMPLE_MAX_N keeps it <= 4096 and nblk <= 256).
@@ -921,22 +955,17 @@ size_t sample_scratch_bytes(int64_t n, int32_t k) {
            + (size_t)nblk * (size_t)k * 4              // per-block top-k lists
            + (size_t)nblk * 4 * 2                      // event counts, NaN flags
            + (size_t)((n + SMP_BLOCK - 1) / SMP_BLOCK) * sizeof(ArgPart) + 256    // greedy partials
-           + (size_t)SMP_KMAX * 8 + 16;                // resolved slots and their flag
+           + (size_t)SMP_KMAX * 8 + 16;                // resolved slots, their flag, the masked values
 }
 
 hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k, float top_p, float min_p,
                          float penalty, int32_t window, uint64_t *rng, const int32_t *history, int32_t hist_n,
                          const int32_t *mask, int32_t n_mask, int32_t *token, void *scratch, hipStream_t s) {
-    const int32_t start = (window > 0 && window < hist_n) ? hist_n - window : 0;
-    hipLaunchKernelGGL(k_smp_penalty, dim3(1), dim3(256), 0, s, logits, n, history, start, hist_n, penalty,
-                       n_mask > 0 ? mask[0] : -1, n_mask > 1 ? mask[1] : -1, n_mask);
-    const int32_t w = hist_n - start;
-    if (w > SMP_HIST_LDS && penalty != 1.0f)
-        hipLaunchKernelGGL(k_smp_penalty_wide, dim3((unsigned)((w + 255) / 256)), dim3(256), 0, s, logits, n,
-                           history + start, w, penalty);
     const int32_t sb = sample_block(n, k);
     const int32_t nblk = (int32_t)((n + sb - 1) / sb);
-    if (nblk > SMP_KMAX || sb > 4096) return hipErrorInvalidValue;   // the caller's n limit keeps both
+    // checked before the first launch, so a refused call leaves the logits
+    // untouched (the caller's n limit keeps both)
+    if (nblk > SMP_KMAX || sb > 4096 || n_mask < 0 || n_mask > 2) return hipErrorInvalidValue;
     uint8_t *p = static_cast<uint8_t *>(scratch);
     int32_t *ev_idx = reinterpret_cast<int32_t *>(p);
     p += (size_t)nblk * sb * 4;
@@ -953,10 +982,20 @@ hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k,
     float *res_val = reinterpret_cast<float *>(pr);
     int32_t *res_idx = reinterpret_cast<int32_t *>(pr + (size_t)SMP_KMAX * 4);
     int32_t *res_ok = reinterpret_cast<int32_t *>(pr + (size_t)SMP_KMAX * 8);
+    float *saved = reinterpret_cast<float *>(pr + (size_t)SMP_KMAX * 8 + 8);
+    const SmpMask mk{n_mask > 0 ? mask[0] : -1, n_mask > 1 ? mask[1] : -1, n_mask};
+
+    const int32_t start = (window > 0 && window < hist_n) ? hist_n - window : 0;
+    hipLaunchKernelGGL(k_smp_penalty, dim3(1), dim3(256), 0, s, logits, n, history, start, hist_n, penalty, mk.m0,
+                       mk.m1, n_mask, saved);
+    const int32_t w = hist_n - start;
+    if (w > SMP_HIST_LDS && penalty != 1.0f)
+        hipLaunchKernelGGL(k_smp_penalty_wide, dim3((unsigned)((w + 255) / 256)), dim3(256), 0, s, logits, n,
+                           history + start, w, penalty);
     if (temperature <= 0.0f) {
         const int32_t ablk = (int32_t)((n + SMP_BLOCK - 1) / SMP_BLOCK);
         hipLaunchKernelGGL(k_smp_argmax_part, dim3(ablk), dim3(256), 0, s, logits, n, part);
-        hipLaunchKernelGGL(k_smp_argmax_final, dim3(1), dim3(256), 0, s, logits, part, ablk, token);
+        hipLaunchKernelGGL(k_smp_argmax_final, dim3(1), dim3(256), 0, s, logits, n, part, ablk, token, mk, saved);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(k_smp_blocks, dim3(nblk), dim3(256), (size_t)sb * 4, s, logits, n, k, sb, tops, nan_flag);
@@ -968,7 +1007,7 @@ hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k,
                        nan_flag, res_val, res_idx, res_ok);
     SmpArgs a{temperature, top_p, min_p, k, sb, nblk};
     hipLaunchKernelGGL(k_smp_finish, dim3(1), dim3(64), 0, s, logits, n, a, ev_idx, ev_val, ev_n, nan_flag, res_val,
-                       res_idx, res_ok, rng, token);
+                       res_idx, res_ok, rng, token, mk, saved);
     return hipGetLastError();
 }
 

@@ -40,3 +40,73 @@ def test_header_block_sizes():
     for name, size in (("qk_q8k_block", 292), ("qk_q4k_block", 144), ("qk_q5k_block", 176),
                        ("qk_q6k_block", 210), ("qk_q8_0_block", 34)):
         assert re.search(rf"}} {name};\s+/\* {size} B", text), name
+
+
+def test_exports_only_the_api():
+    """libqk drops into a host process: the only plain (C) names it exports
+    are the entry points of include/qk.h and the compilation-unit ids the
+    HIP toolchain emits (__hip_cuid_*); everything else it exports is a
+    HIP kernel handle, a C++ name in namespace qk (built with hidden
+    visibility, so no internal helper leaks into the host's namespace)."""
+    import shutil
+    import subprocess
+    import pytest
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", "--defined-only", qk.LIB], capture_output=True, text=True, check=True).stdout
+    names = [ln.split()[-1] for ln in out.splitlines() if ln.strip()]
+    api = set(qk.header_functions())
+    plain = [n for n in names if not n.startswith("_Z") and not n.startswith("__hip_cuid_")]
+    assert sorted(plain) == sorted(api), sorted(set(plain) ^ api)
+    assert all(n.startswith("_ZN2qk") for n in names if n.startswith("_Z")), \
+        [n for n in names if n.startswith("_Z") and not n.startswith("_ZN2qk")]
+
+
+_EXPF_PROBE = r"""
+import ctypes as C, sys
+L = C.CDLL(sys.argv[1])
+L.hip_qk_last_error.restype = C.c_char_p
+class S(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float), ("min_p", C.c_float),
+                ("repetition_penalty", C.c_float), ("repetition_window", C.c_int32)]
+out = []
+out.append(L.hip_silu_f32(None, C.c_int64(1), None, None))
+out.append(L.hip_swiglu_q8k(None, None, C.c_int64(1), C.c_int64(256), None, None, None))
+out.append(L.hip_deltanet_chunked(None, None, None, None, None, C.c_int64(1), 1, 1, 1, None, None, None))
+out.append(L.hip_qk_deltanet_host(1, 1, 1, None, None, None, None, None, None, None))
+out.append(L.hip_sample(None, C.c_int64(1), C.byref(S(0.7, 40, 0.9, 0.05, 1.0, 0)), None, None, 0, None, 0, None, None))
+out.append(L.hip_sample(None, C.c_int64(1), C.byref(S(float("nan"), 40, 0.9, 0.05, 1.0, 0)), None, None, 0, None, 0, None, None))
+out.append(L.hip_sample(None, C.c_int64(1), C.byref(S(0.0, 40, 0.9, 0.05, 1.0, 0)), None, None, 0, None, 0, None, None))
+out.append(L.hip_add_rmsnorm_q8k(None, None, None, C.c_float(1e-6), C.c_int64(1), C.c_int64(256), None, None, None, None))
+print(" ".join(map(str, out)))
+print(L.hip_qk_last_error().decode())
+"""
+
+
+def test_expf_entry_points_need_the_fused_libm_build():
+    """The device restates glibc's fused (FMA) expf. glibc picks its expf
+    build per CPU; with the FMA build switched off through its tunables
+    the entry points whose kernels exponentiate (SiLU, SwiGLU, the chunked
+    DeltaNet, non-greedy sampling) refuse with QK_ERR_UNSUPPORTED, before
+    anything else, while the greedy sampler and the norm (no expf) only
+    report the missing hip_qk_init. On this host's default build every
+    entry point reaches the init check."""
+    import os
+    import subprocess
+    import sys
+    import pytest
+    def probe(env):
+        r = subprocess.run([sys.executable, "-c", _EXPF_PROBE, qk.LIB], capture_output=True, text=True, env=env,
+                           check=True)
+        codes, msg = r.stdout.splitlines()[0], r.stdout.splitlines()[1]
+        return [int(c) for c in codes.split()], msg
+    env = dict(os.environ)
+    env.pop("GLIBC_TUNABLES", None)
+    codes, _ = probe(env)
+    if codes[0] == 6:
+        pytest.skip("this host's libm expf is the unfused build")
+    assert codes == [3] * 8, codes
+    env["GLIBC_TUNABLES"] = "glibc.cpu.hwcaps=-FMA"
+    codes, msg = probe(env)
+    assert codes == [6, 6, 6, 6, 6, 6, 3, 3], codes

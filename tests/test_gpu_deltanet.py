@@ -141,6 +141,9 @@ def test_deltanet_rejects_bad_shapes(lib):
     g2 = torch.zeros((4, 2), device="cuda")
     with pytest.raises(qk.QKError):                    # out written over v, which later phases still read
         lib.deltanet_chunked(q2, q2, q2, g2, g2, torch.zeros((2, 128, 128), device="cuda"), out=q2)
+    buf = torch.zeros(2 * 128 * 128 + 1024, device="cuda")
+    with pytest.raises(qk.QKError, match="state overlaps an input"):   # the state is written while k is read
+        lib.deltanet_chunked(q2, buf[:1024].view(4, 2, 128), q2, g2, g2, buf[512:512 + 2 * 128 * 128].view(2, 128, 128))
     with pytest.raises(qk.QKError):                    # head dim past QK_DELTANET_MAX_HD, host layer
         lib.deltanet_layer_host(np.zeros((4, 2, 129)), np.zeros((4, 2, 129)), np.zeros((4, 2, 128)),
                                 np.zeros((4, 2)), np.zeros((4, 2)), np.zeros((2, 129, 128)))

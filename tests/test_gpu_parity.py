@@ -86,6 +86,9 @@ def test_matvec(tier, orc, wtype, n, k, epi, t):
     step(f"matvec type={wtype} n={n} k={k} tier={t}")
     lib.set_tier(t)
     w = synth.blocks(wtype, n, k, seed=n, tag=wtype)
+    if wtype == 8:                                     # quants of -128 (a valid GGUF byte): the first block
+        w[0, 2:34] = 0x80                              # of row 0 and the last block of the last row
+        w[-1, -32:] = 0x80
     x = np.concatenate([synth.activations(2, k, seed=k), edge_rows(k)[[0, 6, 7]]])
     xq = orc.quantize_for(wtype, x)
     wd = dev(w)

@@ -123,4 +123,6 @@ def test_sample_rejects_bad_arguments(lib):
         lib.sample(lg, sp, rng, mask=[1, 2, 3])           # at most two masked ids
     with pytest.raises(qk.QKError):
         lib.sample(lg, sp, None)                          # sampling needs the rng
+    with pytest.raises(qk.QKError):                       # a NaN temperature samples too (slm/sampler.c:140)
+        lib.sample(lg, dict(sp, temperature=float("nan")), None)
     lib.sample(lg, dict(sp, temperature=0.0), None)       # greedy does not

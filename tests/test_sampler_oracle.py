@@ -75,3 +75,29 @@ def test_sample_oracle_vocab_sequence(orc, ref):
 def test_rng_seed_matches_reference(orc, ref):
     for seed in (0, 1, 42, 2 ** 63, 2 ** 64 - 1):
         assert np.array_equal(orc.rng_seed(seed), ref.rng_seed(seed))
+
+
+@pytest.mark.parametrize("temperature", [0.0, 0.7])
+def test_sample_mask_restore_closed_form(orc, ref, temperature):
+    """slm_generate_raw saves the eos / eot logits before masking them and
+    puts the saved values back after sample_with (slm/slm.c:309-333): a
+    masked id ends at its value from before the mask (the repetition
+    penalty never reaches it), an id masked twice ends at -inf (its
+    second save), an id out of range is left alone; the other logits are
+    penalized as usual."""
+    n = 500
+    rng = np.random.default_rng(3)
+    logits = (rng.standard_normal(n) * 3).astype(np.float32)
+    e1, e2 = 17, 311
+    hist = np.array([e1, e2, 5, 5, 9], np.int32)
+    sp = dict(temperature=temperature, top_k=40, top_p=0.9, min_p=0.05, repetition_penalty=1.25,
+              repetition_window=0)
+    for impl in (orc, ref):
+        _, out, _ = impl.sample(logits, sp, orc.rng_seed(7), hist, np.array([e1, e2], np.int32))
+        assert out[e1] == logits[e1] and out[e2] == logits[e2]
+        pen = lambda v: v / np.float32(1.25) if v > 0 else v * np.float32(1.25)
+        assert out[9] == np.float32(pen(logits[9]))
+        _, out, _ = impl.sample(logits, sp, orc.rng_seed(7), hist, np.array([e1, e1], np.int32))
+        assert out[e1] == -np.inf
+        _, out, _ = impl.sample(logits, sp, orc.rng_seed(7), hist, np.array([-1, n + 5], np.int32))
+        assert out[e1] == np.float32(pen(logits[e1]))

@@ -68,3 +68,35 @@ def test_noalloc_lmhead_limits(lib):
     assert f(p(w), 262145, 1024, p(xq), 0, None, p(am), None, None, None) == 1
     assert "static scratch" in lib.last_error()
     assert f(p(w), 4, 1024, p(xq), 300, None, p(am), None, None, None) == 1      # topk above the maximum
+
+
+def test_noalloc_lmhead_refuses_overlap_from_another_stream(lib, orc):
+    """Two streams calling at once would share the static scratch: a call
+    from another stream while the previous call is still queued fails with
+    QK_ERR_ARG; once it has finished, or on the same stream, calls go
+    through. (Stream a is held busy by a large fp32 matmul first, so the
+    first call is certainly still queued when the second arrives.)"""
+    import torch
+    f = _bind(lib)
+    n, k, topk = 31040, 1024, 8
+    w = torch.from_numpy(synth.blocks(14, n, k, seed=60)).cuda()
+    xq = torch.from_numpy(orc.quantize_q8k(synth.activations(1, k, seed=60))[0]).cuda()
+    big = torch.randn(4096, 4096, device="cuda")
+    a, b = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    print("[gpu] noalloc overlap: busy stream a, then a call on a and one on b", flush=True)
+    with torch.cuda.stream(a):
+        for _ in range(4):
+            big = big @ big * 1e-3
+        am_a, _, _ = _call(lib, f, w, n, k, xq, topk, None)
+    with torch.cuda.stream(b):
+        with pytest.raises(qk.QKError) as e:
+            _call(lib, f, w, n, k, xq, topk, None)
+    assert e.value.rc == 1 and "in flight" in str(e.value)
+    with torch.cuda.stream(a):
+        am_a2, _, _ = _call(lib, f, w, n, k, xq, topk, None)        # same stream: ordered, allowed
+    a.synchronize()
+    with torch.cuda.stream(b):
+        am_b, _, _ = _call(lib, f, w, n, k, xq, topk, None)         # the other one finished: allowed
+    b.synchronize()
+    assert int(am_a.cpu()[0]) == int(am_a2.cpu()[0]) == int(am_b.cpu()[0])
