@@ -47,6 +47,12 @@
  * reference's slm_forward_step unchanged, every matmul a round trip
  * through the seam. Both report their host synchronisations per token.
  *
+ * Prefill path of the GPU build (--prefill): "layer" (default) runs
+ * qk_prefill.c, the reference's batched pass with each DeltaNet layer's
+ * chunk loop as one GPU call; "seam" runs the reference's
+ * slm_forward_batch unchanged, one GPU call per head and chunk. The JSON
+ * line reports the prefill seconds spent inside GPU calls.
+ *
  * --sample SEED (non-zero) replaces the greedy pick with the reference's
  * default sampler chain (slm_sampler_defaults, slm/sampler.c:22-31):
  * rng_seed(SEED) and a history holding the prompt, as slm_generate_raw
@@ -56,7 +62,7 @@
  *
  * Usage: qwen_e2e [--prompt P] [--gen G] [--seed S] [--layers L]
  *                 [--write-gguf PATH | --gguf PATH] [--decode chain|seam]
- *                 [--sample SEED]
+ *                 [--prefill layer|seam] [--sample SEED]
  */
 #if defined(QK_E2E_GPU)
 #include "qk_seam.c"
@@ -66,6 +72,7 @@
 #include "gguf_write.c"
 #if defined(QK_E2E_GPU)
 #include "qk_decode.c"
+#include "qk_prefill.c"
 #endif
 
 #include <time.h>
@@ -267,7 +274,7 @@ static double e2e_now(void) {
 int main(int argc, char **argv) {
     int32_t n_prompt = 512, n_gen = 256, n_layers = 24;
     uint64_t seed = 0, sample_seed = 0;
-    const char *write_path = NULL, *load_path = NULL, *decode_mode = "chain";
+    const char *write_path = NULL, *load_path = NULL, *decode_mode = "chain", *prefill_mode = "layer";
     for (int i = 1; i + 1 < argc; i += 2) {
         if (strcmp(argv[i], "--prompt") == 0) n_prompt = atoi(argv[i + 1]);
         else if (strcmp(argv[i], "--gen") == 0) n_gen = atoi(argv[i + 1]);
@@ -276,13 +283,15 @@ int main(int argc, char **argv) {
         else if (strcmp(argv[i], "--write-gguf") == 0) write_path = argv[i + 1];
         else if (strcmp(argv[i], "--gguf") == 0) load_path = argv[i + 1];
         else if (strcmp(argv[i], "--decode") == 0) decode_mode = argv[i + 1];
+        else if (strcmp(argv[i], "--prefill") == 0) prefill_mode = argv[i + 1];
         else if (strcmp(argv[i], "--sample") == 0) sample_seed = (uint64_t)strtoull(argv[i + 1], NULL, 10);
     }
-    const int chain = strcmp(decode_mode, "chain") == 0;
+    const int chain = strcmp(decode_mode, "chain") == 0, layer_prefill = strcmp(prefill_mode, "layer") == 0;
     if (n_prompt < 2 || n_gen < 1 || n_layers < 1 || (write_path && load_path) ||
-        (!chain && strcmp(decode_mode, "seam") != 0)) {
+        (!chain && strcmp(decode_mode, "seam") != 0) || (!layer_prefill && strcmp(prefill_mode, "seam") != 0)) {
         fprintf(stderr, "usage: %s [--prompt P>=2] [--gen G>=1] [--seed S] [--layers L>=1] "
-                        "[--write-gguf PATH | --gguf PATH] [--decode chain|seam] [--sample SEED]\n", argv[0]);
+                        "[--write-gguf PATH | --gguf PATH] [--decode chain|seam] [--prefill layer|seam] "
+                        "[--sample SEED]\n", argv[0]);
         return 2;
     }
     simd_init();
@@ -409,14 +418,27 @@ int main(int argc, char **argv) {
 
     /* prefill (slm/slm.c:278-283) */
     double t0 = e2e_now();
+#if defined(QK_E2E_GPU)
+    struct tensor *logits = layer_prefill ? qk_forward_batch(c, prompt, n_prompt, 0)
+                                          : slm_forward_batch(c, prompt, n_prompt, 0);
+#else
+    (void)layer_prefill;
     struct tensor *logits = slm_forward_batch(c, prompt, n_prompt, 0);
-    (void)logits;
+#endif
+    /* the prefill's last-token logits, for the stream comparison */
+    double pl_min = logits->data[0], pl_max = logits->data[0], pl_sum = 0;
+    for (int64_t i = 0; i < (int64_t)cfg.vocab_size; i++) {
+        const double v = logits->data[i];
+        pl_min = v < pl_min ? v : pl_min;
+        pl_max = v > pl_max ? v : pl_max;
+        pl_sum += v;
+    }
     int32_t pos = n_prompt;
     double t1 = e2e_now();
     double pf_mm = 0.0, pf_dn = 0.0;   /* prefill seconds inside the GPU matmul / DeltaNet calls */
 #if defined(QK_E2E_GPU)
     pf_mm = qk_seam_matmul_s;
-    pf_dn = qk_seam_deltanet_s;
+    pf_dn = qk_seam_deltanet_s + qk_prefill_layer_calls;
 #endif
     fprintf(stderr, "[e2e] prefill %.3f s\n", t1 - t0);
 
@@ -505,6 +527,7 @@ int main(int argc, char **argv) {
     const double nv = (double)cfg.vocab_size;
     printf("{\"mode\": \"%s\", \"source\": \"%s\", \"tier\": \"%s\", \"layers\": %d, \"prompt\": %d, \"gen\": %d, \"seed\": %llu, "
            "\"prefill_s\": %.6f, \"prefill_gpu_matmul_s\": %.6f, \"prefill_gpu_deltanet_s\": %.6f, "
+           "\"prefill_path\": \"%s\", \"prefill_logits\": {\"min\": %.9g, \"max\": %.9g, \"sum\": %.17g}, "
            "\"decode_s\": %.6f, \"prefill_tok_s\": %.3f, \"decode_tok_s\": %.3f, "
            "\"decode_path\": \"%s\", \"sampler\": \"%s\", \"host_syncs_per_token\": %.2f, \"prefetch_hits\": %.0f, \"prefetch_misses\": %.0f, "
            "\"distinct_tokens\": %d, \"nonfinite_logits\": %lld, \"last_logits\": {\"min\": %.6g, \"max\": %.6g, "
@@ -514,7 +537,13 @@ int main(int argc, char **argv) {
 #else
            "cpu",
 #endif
-           load_path ? "gguf" : "built", simd_dispatch_label(), n_layers, n_prompt, n_gen, (unsigned long long)seed, t1 - t0, pf_mm, pf_dn, t2 - td,
+           load_path ? "gguf" : "built", simd_dispatch_label(), n_layers, n_prompt, n_gen, (unsigned long long)seed, t1 - t0, pf_mm, pf_dn,
+#if defined(QK_E2E_GPU)
+           layer_prefill ? "gpu-layer" : "gpu-seam",
+#else
+           "cpu",
+#endif
+           pl_min, pl_max, pl_sum, t2 - td,
            n_prompt / (t1 - t0), n_gen / (t2 - td),
 #if defined(QK_E2E_GPU)
            chain ? "gpu-chain" : "gpu-seam",

@@ -55,12 +55,20 @@ def test_e2e_greedy_tokens_identical(prompt, gen):
     assert cpu["nonfinite_logits"] == 0
     assert cpu["distinct_tokens"] >= gen // 4
     for mode in ("seam", "chain"):
-        gpu = run(E2E_GPU, 240, prompt=prompt, gen=gen, seed=0, decode=mode)
-        print(f"[e2e] gpu-{mode} prefill {gpu['prefill_tok_s']:.1f} tok/s decode {gpu['decode_tok_s']:.1f} tok/s "
+        # the pure drop-in (the reference's slm_forward_batch, one GPU call
+        # per DeltaNet head and chunk) with the seam decode; qk_prefill.c's
+        # one call per DeltaNet layer with the device decode step
+        prefill = "seam" if mode == "seam" else "layer"
+        gpu = run(E2E_GPU, 240, prompt=prompt, gen=gen, seed=0, decode=mode, prefill=prefill)
+        print(f"[e2e] gpu-{mode} prefill ({prefill}) {gpu['prefill_tok_s']:.1f} tok/s, "
+              f"{gpu['prefill_gpu_matmul_s']:.3f} s in matmul calls, {gpu['prefill_gpu_deltanet_s']:.3f} s in "
+              f"DeltaNet calls; decode {gpu['decode_tok_s']:.1f} tok/s "
               f"({gpu['host_syncs_per_token']:.1f} host syncs/token); cpu prefill {cpu['prefill_tok_s']:.1f} "
               f"decode {cpu['decode_tok_s']:.1f}", flush=True)
         assert gpu["tier"] == cpu["tier"]
         assert gpu["nonfinite_logits"] == 0
+        assert gpu["prefill_path"] == f"gpu-{prefill}"
+        assert gpu["prefill_logits"] == cpu["prefill_logits"], mode
         assert gpu["tokens"] == cpu["tokens"], mode
         assert gpu["last_logits"] == cpu["last_logits"], mode
         if mode == "chain":
@@ -185,3 +193,56 @@ def test_gguf_gpu_tokens_identical(tmp_path):
     assert gpu["source"] == "gguf"
     assert gpu["tokens"] == cpu["tokens"]
     assert gpu["last_logits"] == cpu["last_logits"]
+
+
+# ---- the reference's own generation loop through the one-line binding -----------
+# slm_drive.c includes the reference's TU root slm/slm.c (with qk_seam.c in
+# front for the GPU build, host/_build/slm_drive_gpu; unchanged for the CPU
+# twin, oracle/_ref/slm_drive_cpu) and calls slm_generate_raw
+# (slm/slm.c:237-358) on token ids over a GGUF file written by qwen_e2e.
+# The generated ids come from the reference's own token trace.
+DRIVE_CPU = os.path.join(ROOT, "oracle", "_ref", "slm_drive_cpu")
+DRIVE_GPU = os.path.join(ROOT, "qwen.haiku_amd", "host", "_build", "slm_drive_gpu")
+
+
+def drive(path, gguf, timeout=300, flags=(), **kw):
+    if not os.path.exists(path):
+        pytest.fail(f"{path} is not built (make -C oracle; make -C qwen.haiku_amd/host)")
+    args = [path, "--gguf", gguf] + list(flags)
+    for k, v in kw.items():
+        args += [f"--{k.replace('_', '-')}", str(v)]
+    print(f"[e2e] {' '.join(os.path.relpath(a, ROOT) if a == path else a for a in args)}", flush=True)
+    r = subprocess.run(args, capture_output=True, text=True, timeout=timeout)
+    assert r.returncode == 0, f"{path} failed ({r.returncode}):\n{r.stderr[-2000:]}"
+    toks = [int(ln.split()[1]) for ln in r.stderr.splitlines() if ln.startswith("[tok] ")]
+    return json.loads(r.stdout.strip().splitlines()[-1]), toks
+
+
+@pytest.fixture(scope="module")
+def drive_gguf(tmp_path_factory):
+    path = str(tmp_path_factory.mktemp("drive") / "m4.gguf")
+    run(E2E_CPU, 120, prompt=48, gen=48, layers=4, seed=8, **{"write-gguf": path})   # max_position 97
+    return path
+
+
+def test_slm_drive_cpu_deterministic(drive_gguf):
+    a, ta = drive(DRIVE_CPU, drive_gguf, prompt=24, gen=12, seed=2)
+    b, tb = drive(DRIVE_CPU, drive_gguf, prompt=24, gen=12, seed=2)
+    assert ta == tb and a["generated"] == len(ta) == 12
+    assert len(set(ta)) > 1
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["greedy", "batch", "sampled"])
+def test_slm_generate_raw_through_seam(drive_gguf, mode):
+    """The reference's slm_generate_raw, prefill (per token, or
+    slm_forward_batch) and decode loop unchanged, with the seam in front:
+    the token stream must equal the unchanged reference's."""
+    flags = ("--batch",) if mode != "greedy" else ()
+    kw = dict(prompt=32, gen=40, seed=5)
+    if mode == "sampled":
+        kw.update(sample=11, min_new=6)
+    cpu, tc = drive(DRIVE_CPU, drive_gguf, flags=flags, **kw)
+    gpu, tg = drive(DRIVE_GPU, drive_gguf, flags=flags, **kw)
+    assert tc and tg == tc
+    assert gpu["generated"] == cpu["generated"] == len(tc)
