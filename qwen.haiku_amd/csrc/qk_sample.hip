@@ -13,16 +13,17 @@
 //  * after any prefix the slots hold the k largest values of the prefix
 //    (ties kept by the earlier element), so logit i (i >= k) enters iff
 //    fewer than k earlier logits are >= it;
-//  * per block of logits: the block's k largest values, sorted
-//    (k_smp_blocks); the k-th largest value T_b of everything before the
-//    block, by bisection over the union of those lists (held in LDS);
-//    then, for the block's logits above T_b, the exact count of earlier
-//    logits >= them (the earlier logits above T_b, fewer than k, plus the
-//    block's own earlier candidates). Those with a count below k are the
-//    entering events, listed in index order with their values
-//    (k_smp_events);
-//  * one wave gathers the events into LDS, replays them in order on the k
-//    slots, then runs the rest of the chain on the k survivors as the
+//  * per block of logits: the block's k largest values (k_smp_blocks);
+//    the k-th largest value T_b of everything before the block, by
+//    bisection over the union of those lists (held in registers, counted
+//    by ballots); then, for the block's logits above T_b, the exact count
+//    of earlier logits >= them (the earlier logits above T_b, fewer than
+//    k, plus the block's own earlier candidates). Those with a count
+//    below k are the entering events, listed in index order with their
+//    values (k_smp_events);
+//  * the final slots: in closed form when the values are distinct
+//    (k_smp_slots), else one wave replays the events in order on the k
+//    slots; then the rest of the chain on the k survivors as the
 //    reference writes it (k_smp_finish).
 // A NaN logit after the first k never enters and never compares >=, so it
 // counts as -inf; a NaN among the first k breaks the prefix argument
@@ -46,6 +47,15 @@ __device__ __forceinline__ uint32_t fkey(float f) {
 }
 __device__ __forceinline__ float fkey_inv(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// LDS ordering between the lanes of one wave, for code that not every
+// wave runs (a workgroup barrier there would pair with the other waves'
+// barrier somewhere else).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
 // Wave-wide reductions through DPP within each 16-lane row, then the four
@@ -204,7 +214,9 @@ __global__ __launch_bounds__(256) void k_smp_argmax_final(float *logits, int64_t
 // enters the slots and never compares >= anything, so it is read as -inf
 // here; a NaN among the first k (the initial fill) is flagged instead and
 // k_smp_finish then runs topk_collect literally.
-constexpr int SMP_LIST_MAX = 16384;                    // floats of top-k lists (64 KB of LDS)
+constexpr int SMP_LIST_MAX = 16384;                    // keys of the prefix lists a block holds
+constexpr int SMP_WG = 1024;                           // threads of the selection kernels (16 waves)
+constexpr int SMP_SBMAX = 4096;                        // largest block
 
 __device__ __forceinline__ float smp_load(const float *logits, int64_t n, int64_t i, int32_t k, int32_t &nan_fill) {
     if (i >= n) return -__builtin_inff();
@@ -216,245 +228,282 @@ __device__ __forceinline__ float smp_load(const float *logits, int64_t n, int64_
     return x;
 }
 
-// Per block: its k largest values (a multiset, in no particular order)
-// and whether the initial fill holds a NaN. The k-th largest key T is
-// found by bisection over the block's keys (held in registers); the list
-// is every value above T plus copies of T up to k.
-constexpr int SMP_PER_MAX = 16;                        // logits per thread (sb <= 4096)
-
-__global__ __launch_bounds__(256) void k_smp_blocks(const float *logits, int64_t n, int32_t k, int32_t sb,
-                                                    float *tops, int32_t *nan_flag) {
-    __shared__ int32_t wsum[4];
-    __shared__ int32_t cnt_sh;
-    const int64_t base = (int64_t)blockIdx.x * sb;
-    const int per = sb / 256;
-    int32_t nan_fill = 0;
-    uint32_t key[SMP_PER_MAX];
-#pragma unroll
-    for (int j = 0; j < SMP_PER_MAX; j++)
-        key[j] = j < per ? fkey(smp_load(logits, n, base + threadIdx.x * per + j, k, nan_fill)) : 0u;
-    if (threadIdx.x == 0) cnt_sh = 0;
-    uint32_t t = 0;                                    // largest key with count(>= key) >= k
-    for (int bit = 31; bit >= 0; bit--) {
-        const uint32_t cand = t | (1u << bit);
-        int32_t c = 0;
-#pragma unroll
-        for (int j = 0; j < SMP_PER_MAX; j++) c += (j < per) & (key[j] >= cand);
-        c = wave_sum_i(c);
-        if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = c;
-        __syncthreads();
-        const int32_t total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
-        __syncthreads();
-        if (total >= k) t = cand;
+// ---- wave-held sorted key lists ------------------------------------------------
+// A wave holds 64R keys, element e = 64r + lane in register r; the sorts
+// and merges below order them descending (key 0 is padding, below every
+// real key). Cross-lane exchanges go through DPP (lane ^ 1, 2, 8),
+// ds_swizzle (^ 4, 16) or ds_bpermute (^ 32, and the reversal).
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v, int s) {
+    switch (s) {
+        case 1: return (uint32_t)dpp_xor1((int32_t)v);
+        case 2: return (uint32_t)dpp_xor2((int32_t)v);
+        case 8: return (uint32_t)__builtin_amdgcn_mov_dpp((int32_t)v, 0x128, 0xF, 0xF, true);   // row_ror:8
+        case 4: return (uint32_t)__builtin_amdgcn_ds_swizzle((int32_t)v, 0x101F);
+        case 16: return (uint32_t)__builtin_amdgcn_ds_swizzle((int32_t)v, 0x401F);
+        default: return (uint32_t)__shfl_xor((int32_t)v, 32);
     }
-    float *out = tops + (int64_t)blockIdx.x * k;
+}
+
+// One compare-exchange stage of a bitonic network over the wave's list:
+// elements e and e ^ stride, the larger first where e & size is 0 (size
+// above 64R: everywhere).
+template <int R>
+__device__ __forceinline__ void bitonic_stage(uint32_t (&v)[R], int size, int stride) {
+    const int lane = threadIdx.x & 63;
+    if (stride >= 64) {
+        const int d = stride / 64;
 #pragma unroll
-    for (int j = 0; j < SMP_PER_MAX; j++)
-        if (j < per && key[j] > t) out[atomicAdd(&cnt_sh, 1)] = fkey_inv(key[j]);   // LDS counter
-    __syncthreads();
-    for (int32_t j = cnt_sh + threadIdx.x; j < k; j += 256) out[j] = fkey_inv(t);
-    const int32_t nf = wave_sum_i(nan_fill);
-    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = nf;
-    __syncthreads();
-    if (threadIdx.x == 0) nan_flag[blockIdx.x] = (wsum[0] | wsum[1] | wsum[2] | wsum[3]) != 0;
+        for (int r = 0; r < R; r++)
+            if (!(r & d)) {
+                const int r2 = r | d;
+                const bool desc = ((64 * r) & size) == 0;
+                const uint32_t hi = max(v[r], v[r2]), lo = min(v[r], v[r2]);
+                v[r] = desc ? hi : lo;
+                v[r2] = desc ? lo : hi;
+            }
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t p = lane_xor(v[r], stride);
+            const bool lower = (lane & stride) == 0;
+            const bool desc = ((64 * r + lane) & size) == 0;
+            v[r] = lower == desc ? max(v[r], p) : min(v[r], p);
+        }
+    }
+}
+
+template <int R>
+__device__ __forceinline__ void wave_sort_desc(uint32_t (&v)[R]) {
+#pragma unroll
+    for (int size = 2; size <= 64 * R; size <<= 1)
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) bitonic_stage(v, size, stride);
+}
+
+// a := the top 64R of a and b (both sorted), sorted: max(a[e], b[64R-1-e])
+// is that top as a bitonic sequence, then one bitonic merge.
+template <int R>
+__device__ __forceinline__ void wave_merge_top(uint32_t (&a)[R], const uint32_t (&b)[R]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int r = 0; r < R; r++) a[r] = max(a[r], (uint32_t)__shfl((int32_t)b[R - 1 - r], 63 - lane));
+#pragma unroll
+    for (int stride = 32 * R; stride > 0; stride >>= 1) bitonic_stage(a, 128 * R, stride);
+}
+
+// Every wave holds a sorted list; afterwards wave 0 holds the top 64R of
+// their union, sorted (a tree of merges, four barriers). lds: 16 * 64R keys.
+template <int R>
+__device__ __forceinline__ void wg_merge_top(uint32_t (&v)[R], uint32_t *lds) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int l = 1; l < 16; l <<= 1) {
+        if ((wave & (2 * l - 1)) == l)
+#pragma unroll
+            for (int r = 0; r < R; r++) lds[wave * 64 * R + 64 * r + lane] = v[r];
+        __syncthreads();
+        if ((wave & (2 * l - 1)) == 0) {
+            uint32_t o[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) o[r] = lds[(wave + l) * 64 * R + 64 * r + lane];
+            wave_merge_top(v, o);
+        }
+    }
+}
+
+// List registers for k: 64R >= k.
+__host__ __device__ constexpr int smp_regs(int32_t k) { return k <= 64 ? 1 : (k <= 128 ? 2 : 4); }
+
+// Per block: its k largest values, sorted descending, and whether the
+// initial fill holds a NaN. Each wave sorts its 64 * PER keys in
+// registers, then a tree of merges leaves the block's top 64R in wave 0.
+template <int PER, int R>
+__global__ __launch_bounds__(SMP_WG) void k_smp_blocks(const float *logits, int64_t n, int32_t k, float *tops,
+                                                       int32_t *nan_flag) {
+    __shared__ uint32_t lds[16 * 64 * R];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t base = (int64_t)blockIdx.x * (PER * SMP_WG) + wave * 64 * PER;
+    int32_t nan_fill = 0;
+    uint32_t v[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) v[r] = r < PER ? fkey(smp_load(logits, n, base + 64 * r + lane, k, nan_fill)) : 0u;
+    wave_sort_desc(v);
+    const int nf = __syncthreads_or(nan_fill);
+    wg_merge_top(v, lds);
+    if (wave == 0) {
+        float *out = tops + (int64_t)blockIdx.x * k;
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            if (64 * r + lane < k) out[64 * r + lane] = fkey_inv(v[r]);
+        if (lane == 0) nan_flag[blockIdx.x] = nf;
+    }
 }
 
 // Block b's entering events. With P = the logits before the block and
-// T = the k-th largest of P (bisection over the keys of the earlier
-// blocks' top-k lists, which hold every element of P that can matter),
-// a logit of the block can enter only if it exceeds T; for such a logit v
-// the count of earlier logits >= v is the count in R = {x in P : x > T}
-// (fewer than k elements, all inside those lists) plus the count among
-// the block's earlier candidates, which go in chunks of 256 with T and R
-// carried forward over each chunk (so no candidate scans more than R and
-// its own chunk). Events are candidates at index >= k whose count is below
-// k, written in index order with their values.
-__device__ __forceinline__ int32_t wg_sum(int32_t c, int32_t *wsum) {
-    c = wave_sum_i(c);
-    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = c;
-    __syncthreads();
-    const int32_t total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
-    __syncthreads();
-    return total;
+// T = the k-th largest of P, a logit of the block can enter only if it
+// exceeds T (in block 0, anything above -inf); such a logit v enters iff
+// fewer than k earlier logits are >= v. Earlier logits of the block that
+// are at or below T can never be >= v, so only the top k of P and the
+// block's own candidates count. Events (index >= k) are written in index
+// order with their values.
+//
+// The top k of P is the top of the earlier blocks' sorted lists: wave w
+// merges lists w, w + 16, ... (batches as trees), then a tree of merges
+// across the waves. Inside the block, sub-chunk c (64 consecutive logits,
+// register j of wave w for c = PER w + j) is sorted in registers; the top
+// 64R of P and of the sub-chunks before c comes from a prefix scan of the
+// waves' tops (Hillis-Steele over 16 waves) and the wave's own earlier
+// sub-chunks. A candidate's count is then a binary search in that sorted
+// top plus the earlier lanes of its sub-chunk, read lane by lane.
+template <int R>
+__device__ __forceinline__ void wave_put(uint32_t *dst, const uint32_t (&v)[R]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int r = 0; r < R; r++) dst[64 * r + lane] = v[r];
+}
+template <int R>
+__device__ __forceinline__ void wave_get(uint32_t (&v)[R], const uint32_t *src) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int r = 0; r < R; r++) v[r] = src[64 * r + lane];
 }
 
-// count of keys >= x among keys[0, n4 * 4), n4 uint4 groups split over
-// the workgroup; four independent LDS reads in flight per step
-__device__ __forceinline__ int32_t count_keys_ge(const uint4 *keys4, int32_t n4, uint32_t x) {
-    int32_t c = 0;
-    int32_t j = threadIdx.x;
-    for (; j + 768 < n4; j += 1024) {
-        const uint4 a = keys4[j], b = keys4[j + 256], d = keys4[j + 512], e = keys4[j + 768];
-        c += (a.x >= x) + (a.y >= x) + (a.z >= x) + (a.w >= x) + (b.x >= x) + (b.y >= x) + (b.z >= x) +
-             (b.w >= x) + (d.x >= x) + (d.y >= x) + (d.z >= x) + (d.w >= x) + (e.x >= x) + (e.y >= x) +
-             (e.z >= x) + (e.w >= x);
-    }
-    for (; j < n4; j += 256) {
-        const uint4 a = keys4[j];
-        c += (a.x >= x) + (a.y >= x) + (a.z >= x) + (a.w >= x);
-    }
-    return c;
-}
-
-__global__ __launch_bounds__(256) void k_smp_events(const float *logits, int64_t n, int32_t k, int32_t sb,
-                                                    int32_t lcap, const float *tops, int32_t *ev_idx, float *ev_val,
-                                                    int32_t *ev_n) {
-    extern __shared__ uint4 lds4[];
+template <int PER, int R>
+__global__ __launch_bounds__(SMP_WG) void k_smp_events(const float *logits, int64_t n, int32_t k,
+                                                       const float *tops, int32_t *ev_idx, float *ev_val,
+                                                       int32_t *ev_n) {
+    constexpr int SB = PER * SMP_WG;
+    constexpr int LB = 16 / R;                         // lists loaded per batch (a power of two)
+    __shared__ uint32_t lds[16 * 64 * R];              // merge exchanges, then each wave's running top
+    __shared__ uint32_t pb[64 * R];                    // the top of P, sorted
+    __shared__ int32_t ecnt[16 * PER];                 // events per sub-chunk, then their offsets
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int32_t b = blockIdx.x;
-    const int32_t nlist = b * k;                       // prefix list elements (<= lcap, lcap % 4 == 0)
-    uint32_t *keys = reinterpret_cast<uint32_t *>(lds4);
-    float *cv = reinterpret_cast<float *>(keys + lcap);   // sb candidate values
-    int32_t *ci = reinterpret_cast<int32_t *>(cv + sb);   // sb candidate indices
-    float *rp = reinterpret_cast<float *>(ci + sb);    // R: the prefix values above T (< k), then R' twice
-    __shared__ int32_t wsum[4];
-    __shared__ int32_t nr_sh, ncand_sh, nr2_sh;
-    __shared__ uint32_t tk_sh;
-    const int64_t base = (int64_t)b * sb;
-    const int32_t n4 = (nlist + 3) >> 2;
-    for (int32_t j0 = threadIdx.x; j0 < n4 * 4; j0 += 256 * 8) {   // eight loads in flight per round
-        uint32_t kv[8];
+    const int64_t base = (int64_t)b * SB;
+    // the block's logits first, so their loads overlap the merges
+    int32_t nan_fill = 0;
+    float x[PER];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int32_t j = j0 + 256 * u;
-            kv[u] = j < nlist ? fkey(tops[j]) : 0u;                // 0: below all
+    for (int j = 0; j < PER; j++) x[j] = smp_load(logits, n, base + 64 * (wave * PER + j) + lane, k, nan_fill);
+    uint32_t tkey = 0;                                 // block 0: no prefix
+    if (b > 0) {                                       // earlier blocks are full: SB >= k
+        uint32_t acc[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = 0u;
+        for (int32_t s0 = wave; s0 < b; s0 += 16 * LB) {
+            uint32_t l[LB][R];
+#pragma unroll
+            for (int q = 0; q < LB; q++)
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const int32_t sl = s0 + 16 * q, e = 64 * r + lane;
+                    l[q][r] = sl < b && e < k ? fkey(tops[(int64_t)sl * k + e]) : 0u;
+                }
+#pragma unroll
+            for (int h = 1; h < LB; h <<= 1)           // independent merges at each level
+#pragma unroll
+                for (int q = 0; q + h < LB; q += 2 * h)
+                    if (s0 + 16 * (q + h) < b) wave_merge_top(l[q], l[q + h]);
+            wave_merge_top(acc, l[0]);
         }
-#pragma unroll
-        for (int u = 0; u < 8; u++)
-            if (j0 + 256 * u < n4 * 4) keys[j0 + 256 * u] = kv[u];
+        wg_merge_top(acc, lds);
+        if (wave == 0) wave_put(pb, acc);
+        __syncthreads();
+        tkey = pb[k - 1];
     }
-    if (threadIdx.x == 0) nr_sh = 0;
-    __syncthreads();
-    uint32_t tkey = 0;
-    if (b > 0) {                                       // earlier blocks are full: sb >= k
-        for (int bit = 31; bit >= 0; bit--) {
-            const uint32_t cand = tkey | (1u << bit);
-            if (wg_sum(count_keys_ge(lds4, n4, cand), wsum) >= k) tkey = cand;
-        }
-        for (int32_t j = threadIdx.x; j < nlist; j += 256)
-            if (keys[j] > tkey) rp[atomicAdd(&nr_sh, 1)] = fkey_inv(keys[j]);   // LDS counter; order irrelevant
+    // keys of the candidates; 0 (counts for nothing) elsewhere
+    uint32_t key[PER], cl[PER][R];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const uint32_t kx = fkey(x[j]);
+        key[j] = (b > 0 ? kx > tkey : x[j] > -__builtin_inff()) ? kx : 0u;
+        uint32_t one[1] = {key[j]};
+        wave_sort_desc(one);
+        cl[j][0] = one[0];
+#pragma unroll
+        for (int r = 1; r < R; r++) cl[j][r] = 0u;
     }
-    // candidates in index order: thread t owns elements [t*per, t*per + per)
-    const int per = sb / 256;                          // 4 .. 16
-    int32_t flag = 0, nan_fill = 0;
-    float x[SMP_PER_MAX];
+    uint32_t top[R];                                   // the wave's sub-chunks, then the prefix before them
 #pragma unroll
-    for (int j = 0; j < SMP_PER_MAX; j++) {
-        x[j] = j < per ? smp_load(logits, n, base + threadIdx.x * per + j, k, nan_fill) : -__builtin_inff();
-        const bool c = j < per && (b > 0 ? fkey(x[j]) > tkey : x[j] > -__builtin_inff());
-        flag |= (int32_t)c << j;
-    }
-    const int32_t mycount = __builtin_popcount(flag);
-    int32_t incl = mycount;                            // inclusive scan within the wave
-    for (int o = 1; o < 64; o <<= 1) {
-        const int32_t y = __shfl_up(incl, o);
-        if ((threadIdx.x & 63) >= o) incl += y;
-    }
-    if ((threadIdx.x & 63) == 63) wsum[threadIdx.x >> 6] = incl;
-    __syncthreads();
-    int32_t off = incl - mycount;
-    for (int w = 0; w < (int)(threadIdx.x >> 6); w++) off += wsum[w];
-    if (threadIdx.x == 255) ncand_sh = off + mycount;
+    for (int r = 0; r < R; r++) top[r] = cl[0][r];
 #pragma unroll
-    for (int j = 0; j < SMP_PER_MAX; j++)
-        if (flag >> j & 1) {
-            cv[off] = x[j];                            // a candidate is never NaN
-            ci[off] = (int32_t)(base + threadIdx.x * per + j);
-            off++;
-        }
-    __syncthreads();
-    const int32_t ncand = ncand_sh, nr = nr_sh;
-    // The candidates in chunks of 256, in index order, with a running
-    // threshold: the top k of everything before a chunk is the multiset
-    // R' (the values above T', fewer than k, as keys in rk) plus k - |R'|
-    // copies of T' (key 0 while fewer than k values came before). A
-    // candidate at or below T' has k earlier values >= it; one above it
-    // counts those in R' and its own chunk's earlier candidates. After a
-    // chunk, T' becomes the k-th largest of R', the copies and the chunk
-    // (a bisection), and R' the values above it.
-    uint32_t *rk = reinterpret_cast<uint32_t *>(rp);  // R' (rp's values, as keys)
-    uint32_t *rk2 = rk + k;                           // the next R'
-    for (int32_t r = threadIdx.x; r < nr; r += 256) rk[r] = fkey(rp[r]);
-    if (threadIdx.x == 0) {
-        tk_sh = tkey;
-        nr2_sh = nr;
-    }
-    __syncthreads();
-    for (int32_t c0 = 0; c0 < ncand; c0 += 256) {
-        const uint32_t tk = tk_sh;
-        const int32_t nr2 = nr2_sh;                    // < k <= 256
-        const int32_t c = c0 + threadIdx.x;
-        const bool act = c < ncand;
-        const uint32_t kv = act ? fkey(cv[c]) : 0u;
-        if (act && ci[c] >= k && kv > tk) {            // the initial fill never enters
-            int32_t cnt = 0, r = 0;
-            for (; r + 8 <= nr2; r += 8) {             // eight independent reads per step
-                const uint4 a = *reinterpret_cast<const uint4 *>(&rk[r]);
-                const uint4 b2 = *reinterpret_cast<const uint4 *>(&rk[r + 4]);
-                cnt += (a.x >= kv) + (a.y >= kv) + (a.z >= kv) + (a.w >= kv) + (b2.x >= kv) + (b2.y >= kv) +
-                       (b2.z >= kv) + (b2.w >= kv);
-            }
-            for (; r < nr2; r++) cnt += rk[r] >= kv;
-            const float v = cv[c];
-            int32_t e = c0;
-            for (; e + 8 <= c && cnt < k; e += 8)
-                cnt += (cv[e] >= v) + (cv[e + 1] >= v) + (cv[e + 2] >= v) + (cv[e + 3] >= v) + (cv[e + 4] >= v) +
-                       (cv[e + 5] >= v) + (cv[e + 6] >= v) + (cv[e + 7] >= v);
-            for (; e < c && cnt < k; e++) cnt += cv[e] >= v;
-            if (cnt < k) ci[c] |= (int32_t)0x80000000;   // indices are < 2^31
-        }
-        if (c0 + 256 >= ncand) break;                  // uniform: the last chunk
-        __syncthreads();                               // every count has read rk
-        if (threadIdx.x < 64) {                        // one wave: the next T' and R'
-            const int lane = threadIdx.x;
-            const int32_t nc = ncand - c0 < 256 ? ncand - c0 : 256;
-            uint32_t key8[8];                          // R' entries l + 64m, chunk entries l + 64m
+    for (int j = 1; j < PER; j++) wave_merge_top(top, cl[j]);
+    // inclusive scan of the waves' tops (Hillis-Steele), then shift by one
+    uint32_t *my = lds + wave * 64 * R;
 #pragma unroll
-            for (int m = 0; m < 4; m++) {
-                key8[m] = lane + 64 * m < nr2 ? rk[lane + 64 * m] : 0u;
-                key8[4 + m] = lane + 64 * m < nc ? fkey(cv[c0 + lane + 64 * m]) : 0u;
-            }
-            // bisection; each step's count is eight ballots' popcounts, so
-            // the step is a short scalar chain (0 keys are padding:
-            // cand >= 1)
-            uint32_t t = 0;
-            for (int bit = 31; bit >= 0; bit--) {
-                const uint32_t cand = t | (1u << bit);
-                int32_t cnt = tk >= cand ? k - nr2 : 0;
-#pragma unroll
-                for (int m = 0; m < 8; m++) cnt += __builtin_popcountll(__ballot(key8[m] >= cand));
-                if (cnt >= k) t = cand;
-            }
-            int32_t nn = 0;                            // R'' = the keys above t, compacted by the wave
-#pragma unroll
-            for (int m = 0; m < 8; m++) {
-                const bool keep = key8[m] > t;
-                const uint64_t bal = __ballot(keep);
-                if (keep) rk2[nn + __builtin_popcountll(bal & ((1ull << lane) - 1))] = key8[m];
-                nn += __builtin_popcountll(bal);
-            }
-            for (int32_t r = lane; r < nn; r += 64) rk[r] = rk2[r];   // nn < k; the wave wrote rk2 itself
-            if (lane == 0) {
-                tk_sh = t;
-                nr2_sh = nn;
-            }
+    for (int l = 1; l < 16; l <<= 1) {
+        wave_put(my, top);
+        __syncthreads();
+        if (wave >= l) {
+            uint32_t o[R];
+            wave_get(o, lds + (wave - l) * 64 * R);
+            wave_merge_top(top, o);
         }
         __syncthreads();
     }
+    wave_put(my, top);
     __syncthreads();
-    if (threadIdx.x < 64) {                            // compact the events in order
-        int32_t written = 0;
-        for (int32_t c0 = 0; c0 < ncand; c0 += 64) {
-            const int32_t c = c0 + threadIdx.x;
-            const bool is_ev = c < ncand && ci[c] < 0;
-            const uint64_t m = __ballot(is_ev);
-            if (is_ev) {
-                const int32_t pos = written + __builtin_popcountll(m & ((1ull << threadIdx.x) - 1));
-                ev_idx[base + pos] = ci[c] & 0x7fffffff;
-                ev_val[base + pos] = cv[c];
-            }
-            written += __builtin_popcountll(m);
+    if (wave > 0) wave_get(top, lds + (wave - 1) * 64 * R);
+    else
+#pragma unroll
+        for (int r = 0; r < R; r++) top[r] = 0u;
+    if (b > 0) {
+        uint32_t p[R];
+        wave_get(p, pb);
+        wave_merge_top(top, p);
+    }
+    __syncthreads();                                   // every wave has read the scan's slots
+    // counts, sub-chunk by sub-chunk; `top` is the sorted top of everything
+    // before the sub-chunk
+    int32_t evf = 0;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        if (j > 0) wave_merge_top(top, cl[j - 1]);
+        wave_put(my, top);
+        wave_lds_sync();
+        const uint32_t kv = key[j];
+        const int64_t idx = base + 64 * (wave * PER + j) + lane;
+        bool ev = false;
+        int32_t cnt = 0;                               // leading entries of the top >= v
+        if (kv != 0u && idx >= k) {                    // the initial fill never enters
+#pragma unroll
+            for (int step = 64 * R; step > 0; step >>= 1)
+                if (cnt + step <= k && my[cnt + step - 1] >= kv) cnt += step;
+            ev = cnt < k;
         }
-        if (threadIdx.x == 0) ev_n[b] = written;
+        if (__ballot(ev)) {                            // plus the earlier lanes of the sub-chunk
+            for (int l2 = 0; l2 < 63; l2++) {
+                const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int32_t)kv, l2);
+                cnt += (l2 < lane) & (o >= kv);
+            }
+            ev = ev && cnt < k;
+        }
+        wave_lds_sync();                               // the slot is rewritten for the next sub-chunk
+        const uint64_t m = __ballot(ev);
+        evf |= (int32_t)ev << j;
+        if (lane == 0) ecnt[wave * PER + j] = __builtin_popcountll(m);
+    }
+    __syncthreads();
+    if (wave == 0) {                                   // exclusive scan of the counts, in index order
+        const int32_t c = lane < 16 * PER ? ecnt[lane] : 0;
+        int32_t inc = c;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int32_t y = __shfl_up(inc, o);
+            if (lane >= o) inc += y;
+        }
+        if (lane < 16 * PER) ecnt[lane] = inc - c;
+        if (lane == 63) ev_n[b] = inc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const bool ev = evf >> j & 1;
+        const uint64_t m = __ballot(ev);
+        if (ev) {
+            const int32_t pos = ecnt[wave * PER + j] + __builtin_popcountll(m & ((1ull << lane) - 1));
+            ev_idx[base + pos] = (int32_t)(base + 64 * (wave * PER + j) + lane);
+            ev_val[base + pos] = x[j];
+        }
     }
 }
 
@@ -724,219 +773,238 @@ __device__ void chain_literal(float *val, int32_t *idx, int32_t filled, const Sm
     *token = idx[picked];
 }
 
-__device__ __forceinline__ void smp_finish(const float *logits, int64_t n, SmpArgs a, const int32_t *ev_idx,
-                                           const float *ev_val, const int32_t *ev_n, const int32_t *nan_flag,
-                                           const float *res_val, const int32_t *res_idx, const int32_t *res_ok,
-                                           uint64_t *rng, int32_t *token) {
-    __shared__ float val[SMP_KMAX];
+constexpr int SMP_FIN = 256;                           // threads of k_smp_finish
+
+// Wave 0 places the k slots (from k_smp_slots, or by replaying the
+// events), forms the softmax numerators, their sum in slot order and the
+// quotients; the four waves rank the probabilities (topk_sort_desc's
+// order); wave 0 then cuts and picks. The masked ids get their saved
+// values back last, on every path.
+__global__ __launch_bounds__(SMP_FIN) void k_smp_finish(float *logits, int64_t n, SmpArgs a, const int32_t *ev_idx,
+                                                        const float *ev_val, const int32_t *ev_n,
+                                                        const int32_t *nan_flag, const float *res_val,
+                                                        const int32_t *res_idx, const int32_t *res_ok, uint64_t *rng,
+                                                        int32_t *token, SmpMask mk, const float *saved) {
+    __shared__ __align__(16) float val[SMP_KMAX];
     __shared__ int32_t idx[SMP_KMAX];
     __shared__ int32_t off[SMP_KMAX + 1];              // event offsets per block (nblk <= 256)
     __shared__ float sp[SMP_KMAX];                     // probabilities in sorted order
     __shared__ int32_t si[SMP_KMAX];
-    const int lane = threadIdx.x;
+    __shared__ int32_t done_sh;
+    const int tid = threadIdx.x, lane = tid & 63;
     const int32_t k = a.k, nblk = a.nblk;
     const int32_t filled = (int32_t)(n < k ? n : k);
-    // NaN in the fill; event offsets (wave-parallel exclusive scan, lane l
-    // owning blocks 4l .. 4l+3)
-    int32_t nf = 0, c4[4], own = 0;
+    // Wave 0: returns true when it ran the chain to the end literally (a
+    // NaN in the fill, or a NaN probability).
+    auto slots_softmax = [&]() -> bool {
+        // NaN in the fill; event offsets (wave-parallel exclusive scan,
+        // lane l owning blocks 4l .. 4l+3)
+        int32_t nf = 0, c4[4], own = 0;
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const int32_t b = 4 * lane + q;
-        nf |= b < nblk ? nan_flag[b] : 0;
-        c4[q] = b < nblk ? ev_n[b] : 0;
-        own += c4[q];
-    }
-    const bool nan_in_fill = __ballot(nf != 0) != 0;
-    int32_t incl = own;
-    for (int o = 1; o < 64; o <<= 1) {
-        const int32_t y = __shfl_up(incl, o);
-        if (lane >= o) incl += y;
-    }
-    int32_t acc = incl - own;
+        for (int q = 0; q < 4; q++) {
+            const int32_t b = 4 * lane + q;
+            nf |= b < nblk ? nan_flag[b] : 0;
+            c4[q] = b < nblk ? ev_n[b] : 0;
+            own += c4[q];
+        }
+        const bool nan_in_fill = __ballot(nf != 0) != 0;
+        int32_t incl = own;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int32_t y = __shfl_up(incl, o);
+            if (lane >= o) incl += y;
+        }
+        int32_t acc = incl - own;
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        if (4 * lane + q <= nblk) off[4 * lane + q] = acc;
-        acc += c4[q];
-    }
-    const int32_t total = __builtin_amdgcn_readlane(incl, 63);
-    if (lane == 0) off[nblk] = total;
-    float sv[SMP_Q];
-    int32_t sx[SMP_Q];
-    const bool resolved = *res_ok != 0;                // k_smp_slots placed the survivors
+        for (int q = 0; q < 4; q++) {
+            if (4 * lane + q <= nblk) off[4 * lane + q] = acc;
+            acc += c4[q];
+        }
+        const int32_t total = __builtin_amdgcn_readlane(incl, 63);
+        if (lane == 0) off[nblk] = total;
+        float sv[SMP_Q];
+        int32_t sx[SMP_Q];
+        const bool resolved = *res_ok != 0;            // k_smp_slots placed the survivors
 #pragma unroll
-    for (int q = 0; q < SMP_Q; q++) {
-        const int32_t s_ = q * 64 + lane;
-        sv[q] = s_ < filled ? (resolved ? res_val[s_] : logits[s_]) : 0.0f;
-        sx[q] = resolved && s_ < filled ? res_idx[s_] : s_;
-    }
-    __syncthreads();
-    if (!resolved && !nan_in_fill && n > k && total > 0) {
-        float mv;
-        int32_t ms;
-        slot_min(sv, k, mv, ms);
-        int32_t gi, ni;
-        float gv, nv;
-        gather_events(off, nblk, a.sb, 0, total, ev_idx, ev_val, gi, gv);
-        for (int32_t e0 = 0; e0 < total; e0 += 64) {
-            gather_events(off, nblk, a.sb, e0 + 64, total, ev_idx, ev_val, ni, nv);   // next batch in flight
-            const int32_t cnt = total - e0 < 64 ? total - e0 : 64;
-            for (int32_t j = 0; j < cnt; j++) {
-                const float v = readlane_f(gv, j);
-                if (!(v > mv)) continue;               // not reached when the events are exact
-                const int32_t i = __builtin_amdgcn_readlane(gi, j);
-                const int32_t q = ms >> 6;
-                if (lane == (ms & 63)) {
+        for (int q = 0; q < SMP_Q; q++) {
+            const int32_t s_ = q * 64 + lane;
+            sv[q] = s_ < filled ? (resolved ? res_val[s_] : logits[s_]) : 0.0f;
+            sx[q] = resolved && s_ < filled ? res_idx[s_] : s_;
+        }
+        wave_lds_sync();
+        if (!resolved && !nan_in_fill && n > k && total > 0) {
+            float mv;
+            int32_t ms;
+            slot_min(sv, k, mv, ms);
+            int32_t gi, ni;
+            float gv, nv;
+            gather_events(off, nblk, a.sb, 0, total, ev_idx, ev_val, gi, gv);
+            for (int32_t e0 = 0; e0 < total; e0 += 64) {
+                gather_events(off, nblk, a.sb, e0 + 64, total, ev_idx, ev_val, ni, nv);   // next batch in flight
+                const int32_t cnt = total - e0 < 64 ? total - e0 : 64;
+                for (int32_t j = 0; j < cnt; j++) {
+                    const float v = readlane_f(gv, j);
+                    if (!(v > mv)) continue;           // not reached when the events are exact
+                    const int32_t i = __builtin_amdgcn_readlane(gi, j);
+                    const int32_t q = ms >> 6;
+                    if (lane == (ms & 63)) {
 #pragma unroll
-                    for (int r = 0; r < SMP_Q; r++)
-                        if (r == q) {
-                            sv[r] = v;
-                            sx[r] = i;
-                        }
+                        for (int r = 0; r < SMP_Q; r++)
+                            if (r == q) {
+                                sv[r] = v;
+                                sx[r] = i;
+                            }
+                    }
+                    slot_min(sv, k, mv, ms);
                 }
-                slot_min(sv, k, mv, ms);
+                gi = ni;
+                gv = nv;
             }
-            gi = ni;
-            gv = nv;
         }
-    }
 #pragma unroll
-    for (int q = 0; q < SMP_Q; q++) {
-        const int32_t s_ = q * 64 + lane;
-        if (s_ < filled) {
-            val[s_] = sv[q];
-            idx[s_] = sx[q];
+        for (int q = 0; q < SMP_Q; q++) {
+            const int32_t s_ = q * 64 + lane;
+            if (s_ < filled) {
+                val[s_] = sv[q];
+                idx[s_] = sx[q];
+            }
         }
+        wave_lds_sync();
+        if (nan_in_fill) {
+            if (lane == 0) {
+                if (n > k)                             // topk_collect as written (slm/sampler.c:74-92)
+                    for (int64_t i = k; i < n; i++) {
+                        const float lv = logits[i];
+                        int32_t worst = 0;
+                        for (int32_t j = 1; j < k; j++)
+                            if (val[j] < val[worst]) worst = j;
+                        if (lv > val[worst]) {
+                            idx[worst] = (int32_t)i;
+                            val[worst] = lv;
+                        }
+                    }
+                chain_literal(val, idx, filled, a, rng, token);
+            }
+            return true;
+        }
+        // topk_softmax (slm/sampler.c:97-111): the max (its value is all
+        // that matters), the exponentials, their sum in slot order, the
+        // division
+        uint32_t mkey = 0;
+#pragma unroll
+        for (int q = 0; q < SMP_Q; q++)
+            if (q * 64 + lane < filled) mkey = max(mkey, fkey(sv[q]));
+        mkey = ~wave_min_u(~mkey);
+        const float m = fkey_inv(mkey);
+        float pe[SMP_Q];
+        int32_t bad = 0;
+#pragma unroll
+        for (int q = 0; q < SMP_Q; q++) {
+            pe[q] = q * 64 + lane < filled ? qk_expf(__fdiv_rn(__fsub_rn(sv[q], m), a.temperature)) : 0.0f;
+            bad |= pe[q] != pe[q];
+        }
+        if (__ballot(bad != 0)) {                      // NaN probabilities: the literal order matters
+            if (lane == 0) chain_literal(val, idx, filled, a, rng, token);
+            return true;
+        }
+        float sum = 0.0f;
+#pragma unroll
+        for (int q = 0; q < SMP_Q; q++)
+            for (int32_t l = 0; l < 64 && q * 64 + l < filled; l++) sum = __fadd_rn(sum, readlane_f(pe[q], l));
+        if (sum > 0.0f)
+#pragma unroll
+            for (int q = 0; q < SMP_Q; q++) pe[q] = __fdiv_rn(pe[q], sum);
+        // the probabilities for the ranking; -1 pads to a multiple of four
+        // (below every probability, equal to none)
+#pragma unroll
+        for (int q = 0; q < SMP_Q; q++) {
+            const int32_t s_ = q * 64 + lane;
+            if (s_ < ((filled + 3) & ~3)) val[s_] = s_ < filled ? pe[q] : -1.0f;
+        }
+        return false;
+    };
+    if (tid < 64) {
+        const bool done = slots_softmax();
+        if (lane == 0) done_sh = done;
     }
     __syncthreads();
-    if (nan_in_fill) {
-        if (lane == 0) {
-            if (n > k)                                 // topk_collect as written (slm/sampler.c:74-92)
-                for (int64_t i = k; i < n; i++) {
-                    const float lv = logits[i];
-                    int32_t worst = 0;
-                    for (int32_t j = 1; j < k; j++)
-                        if (val[j] < val[worst]) worst = j;
-                    if (lv > val[worst]) {
-                        idx[worst] = (int32_t)i;
-                        val[worst] = lv;
+    const bool done = done_sh != 0;
+    // topk_sort_desc (slm/sampler.c:116-129) is a stable sort by
+    // descending value: rank = #greater + #equal in earlier slots; one
+    // slot per thread, the probabilities read four at a time
+    if (!done && tid < filled) {
+        const float v = val[tid];
+        int32_t r = 0;
+        const int32_t nf4 = (filled + 3) & ~3;
+#pragma unroll 4
+        for (int32_t t = 0; t < nf4; t += 4) {
+            const float4 w = *reinterpret_cast<const float4 *>(&val[t]);
+            r += (w.x > v) | ((w.x == v) & (t < tid));
+            r += (w.y > v) | ((w.y == v) & (t + 1 < tid));
+            r += (w.z > v) | ((w.z == v) & (t + 2 < tid));
+            r += (w.w > v) | ((w.w == v) & (t + 3 < tid));
+        }
+        sp[r] = v;
+        si[r] = idx[tid];
+    }
+    __syncthreads();
+    if (tid >= 64) return;
+    if (!done) {
+        float sq[SMP_Q];
+#pragma unroll
+        for (int q = 0; q < SMP_Q; q++) sq[q] = q * 64 + lane < filled ? sp[q * 64 + lane] : 0.0f;
+        // top-p, min-p, renormalized roulette pick (slm/sampler.c:150-178);
+        // the sorted probability j is register j / 64 of lane j % 64
+        int32_t cutoff = filled;
+        if (a.top_p > 0.0f && a.top_p < 1.0f) {
+            float acc = 0.0f;
+            bool fin = false;
+#pragma unroll
+            for (int q = 0; q < SMP_Q; q++)
+                for (int32_t l = 0; l < 64 && !fin && q * 64 + l < filled; l++) {
+                    acc = __fadd_rn(acc, readlane_f(sq[q], l));
+                    if (acc >= a.top_p) {
+                        cutoff = q * 64 + l + 1;
+                        fin = true;
                     }
                 }
-            chain_literal(val, idx, filled, a, rng, token);
         }
-        return;
-    }
-    // topk_softmax (slm/sampler.c:97-111): the max (its value is all that
-    // matters), the exponentials, their sum in slot order, the division
-    uint32_t mk = 0;
+        if (a.min_p > 0.0f) {
+            const float thresh = __fmul_rn(a.min_p, readlane_f(sq[0], 0));
+            int32_t j = 1;
+            bool fin = false;
 #pragma unroll
-    for (int q = 0; q < SMP_Q; q++)
-        if (q * 64 + lane < filled) mk = max(mk, fkey(sv[q]));
-    mk = ~wave_min_u(~mk);
-    const float m = fkey_inv(mk);
-    float pe[SMP_Q];
-    int32_t bad = 0;
-#pragma unroll
-    for (int q = 0; q < SMP_Q; q++) {
-        pe[q] = q * 64 + lane < filled ? qk_expf(__fdiv_rn(__fsub_rn(sv[q], m), a.temperature)) : 0.0f;
-        bad |= pe[q] != pe[q];
-    }
-    if (__ballot(bad != 0)) {                          // NaN probabilities: the literal order matters
-        if (lane == 0) chain_literal(val, idx, filled, a, rng, token);
-        return;
-    }
-    float sum = 0.0f;
-#pragma unroll
-    for (int q = 0; q < SMP_Q; q++)
-        for (int32_t l = 0; l < 64 && q * 64 + l < filled; l++) sum = __fadd_rn(sum, readlane_f(pe[q], l));
-    if (sum > 0.0f)
-#pragma unroll
-        for (int q = 0; q < SMP_Q; q++) pe[q] = __fdiv_rn(pe[q], sum);
-    // topk_sort_desc (slm/sampler.c:116-129) is a stable sort by
-    // descending value: rank = #greater + #equal in earlier slots
-#pragma unroll
-    for (int q = 0; q < SMP_Q; q++)
-        if (q * 64 + lane < filled) val[q * 64 + lane] = pe[q];
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < SMP_Q; q++) {
-        const int32_t s_ = q * 64 + lane;
-        if (s_ < filled) {
-            const float v = pe[q];
-            int32_t r = 0;
-            for (int32_t t = 0; t < filled; t++) {
-                const float w = val[t];
-                r += (w > v) | ((w == v) & (t < s_));
-            }
-            sp[r] = v;
-            si[r] = sx[q];
+            for (int q = 0; q < SMP_Q; q++)
+                for (int32_t l = q == 0 ? 1 : 0; l < 64 && !fin; l++) {
+                    if (j < cutoff && readlane_f(sq[q], l) >= thresh) j++;
+                    else fin = true;
+                }
+            cutoff = j;
         }
-    }
-    __syncthreads();
-    float sq[SMP_Q];
-#pragma unroll
-    for (int q = 0; q < SMP_Q; q++) sq[q] = q * 64 + lane < filled ? sp[q * 64 + lane] : 0.0f;
-    // top-p, min-p, renormalized roulette pick (slm/sampler.c:150-178); the
-    // sorted probability j is register j / 64 of lane j % 64
-    int32_t cutoff = filled;
-    if (a.top_p > 0.0f && a.top_p < 1.0f) {
-        float acc = 0.0f;
-        bool done = false;
+        float tot = 0.0f;
 #pragma unroll
         for (int q = 0; q < SMP_Q; q++)
-            for (int32_t l = 0; l < 64 && !done && q * 64 + l < filled; l++) {
-                acc = __fadd_rn(acc, readlane_f(sq[q], l));
-                if (acc >= a.top_p) {
-                    cutoff = q * 64 + l + 1;
-                    done = true;
+            for (int32_t l = 0; l < 64 && q * 64 + l < cutoff; l++) tot = __fadd_rn(tot, readlane_f(sq[q], l));
+        uint64_t st[2] = {rng[0], rng[1]};
+        const float u = __fmul_rn(rng_uniform_dev(st), tot);
+        float c = 0.0f;
+        int32_t picked = 0;
+        bool fin = false;
+#pragma unroll
+        for (int q = 0; q < SMP_Q; q++)
+            for (int32_t l = 0; l < 64 && !fin && q * 64 + l < cutoff; l++) {
+                c = __fadd_rn(c, readlane_f(sq[q], l));
+                if (u <= c) {
+                    picked = q * 64 + l;
+                    fin = true;
                 }
             }
-    }
-    if (a.min_p > 0.0f) {
-        const float thresh = __fmul_rn(a.min_p, readlane_f(sq[0], 0));
-        int32_t j = 1;
-        bool done = false;
-#pragma unroll
-        for (int q = 0; q < SMP_Q; q++)
-            for (int32_t l = q == 0 ? 1 : 0; l < 64 && !done; l++) {
-                if (j < cutoff && readlane_f(sq[q], l) >= thresh) j++;
-                else done = true;
-            }
-        cutoff = j;
-    }
-    float tot = 0.0f;
-#pragma unroll
-    for (int q = 0; q < SMP_Q; q++)
-        for (int32_t l = 0; l < 64 && q * 64 + l < cutoff; l++) tot = __fadd_rn(tot, readlane_f(sq[q], l));
-    uint64_t st[2] = {rng[0], rng[1]};
-    const float u = __fmul_rn(rng_uniform_dev(st), tot);
-    float c = 0.0f;
-    int32_t picked = 0;
-    bool done = false;
-#pragma unroll
-    for (int q = 0; q < SMP_Q; q++)
-        for (int32_t l = 0; l < 64 && !done && q * 64 + l < cutoff; l++) {
-            c = __fadd_rn(c, readlane_f(sq[q], l));
-            if (u <= c) {
-                picked = q * 64 + l;
-                done = true;
-            }
+        if (lane == 0) {
+            rng[0] = st[0];
+            rng[1] = st[1];
+            *token = si[picked];
         }
-    if (lane == 0) {
-        rng[0] = st[0];
-        rng[1] = st[1];
-        *token = si[picked];
     }
-}
-
-// The pick, then lane 0 (which wrote the token on every path) puts the
-// masked ids back.
-__global__ __launch_bounds__(64) void k_smp_finish(float *logits, int64_t n, SmpArgs a, const int32_t *ev_idx,
-                                                   const float *ev_val, const int32_t *ev_n, const int32_t *nan_flag,
-                                                   const float *res_val, const int32_t *res_idx,
-                                                   const int32_t *res_ok, uint64_t *rng, int32_t *token, SmpMask mk,
-                                                   const float *saved) {
-    smp_finish(logits, n, a, ev_idx, ev_val, ev_n, nan_flag, res_val, res_idx, res_ok, rng, token);
-    if (threadIdx.x == 0) restore_masks(logits, n, mk, saved);
+    if (lane == 0) restore_masks(logits, n, mk, saved);
 }
 
 // ---- launcher -------------------------------------------------------------------
@@ -965,7 +1033,7 @@ hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k,
     const int32_t nblk = (int32_t)((n + sb - 1) / sb);
     // checked before the first launch, so a refused call leaves the logits
     // untouched (the caller's n limit keeps both)
-    if (nblk > SMP_KMAX || sb > 4096 || n_mask < 0 || n_mask > 2) return hipErrorInvalidValue;
+    if (nblk > SMP_KMAX || sb > SMP_SBMAX || n_mask < 0 || n_mask > 2) return hipErrorInvalidValue;
     uint8_t *p = static_cast<uint8_t *>(scratch);
     int32_t *ev_idx = reinterpret_cast<int32_t *>(p);
     p += (size_t)nblk * sb * 4;
@@ -998,15 +1066,20 @@ hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k,
         hipLaunchKernelGGL(k_smp_argmax_final, dim3(1), dim3(256), 0, s, logits, n, part, ablk, token, mk, saved);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(k_smp_blocks, dim3(nblk), dim3(256), (size_t)sb * 4, s, logits, n, k, sb, tops, nan_flag);
-    const int32_t lcap = ((nblk - 1) * k + 3) & ~3;   // the last block's prefix lists
-    const size_t ev_lds = (size_t)lcap * 4 + (size_t)sb * 8 + (size_t)k * 8;
-    hipLaunchKernelGGL(k_smp_events, dim3(nblk), dim3(256), ev_lds, s, logits, n, k, sb, lcap, tops, ev_idx,
-                       ev_val, ev_n);
+    // (sb, list registers): sb <= 1024 * R, since nblk * k <= SMP_LIST_MAX
+    const int R = smp_regs(k);
+    auto blocks = R == 1 ? k_smp_blocks<1, 1>
+                : R == 2 ? (sb == 1024 ? k_smp_blocks<1, 2> : k_smp_blocks<2, 2>)
+                         : (sb == 1024 ? k_smp_blocks<1, 4> : sb == 2048 ? k_smp_blocks<2, 4> : k_smp_blocks<4, 4>);
+    auto events = R == 1 ? k_smp_events<1, 1>
+                : R == 2 ? (sb == 1024 ? k_smp_events<1, 2> : k_smp_events<2, 2>)
+                         : (sb == 1024 ? k_smp_events<1, 4> : sb == 2048 ? k_smp_events<2, 4> : k_smp_events<4, 4>);
+    hipLaunchKernelGGL(blocks, dim3(nblk), dim3(SMP_WG), 0, s, logits, n, k, tops, nan_flag);
+    hipLaunchKernelGGL(events, dim3(nblk), dim3(SMP_WG), 0, s, logits, n, k, tops, ev_idx, ev_val, ev_n);
     hipLaunchKernelGGL(k_smp_slots, dim3(1), dim3(1024), 0, s, logits, n, k, sb, nblk, ev_idx, ev_val, ev_n,
                        nan_flag, res_val, res_idx, res_ok);
     SmpArgs a{temperature, top_p, min_p, k, sb, nblk};
-    hipLaunchKernelGGL(k_smp_finish, dim3(1), dim3(64), 0, s, logits, n, a, ev_idx, ev_val, ev_n, nan_flag, res_val,
+    hipLaunchKernelGGL(k_smp_finish, dim3(1), dim3(SMP_FIN), 0, s, logits, n, a, ev_idx, ev_val, ev_n, nan_flag, res_val,
                        res_idx, res_ok, rng, token, mk, saved);
     return hipGetLastError();
 }
