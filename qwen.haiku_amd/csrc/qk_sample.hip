@@ -136,6 +136,52 @@ __global__ __launch_bounds__(256) void k_smp_penalty_wide(float *logits, int64_t
     if (i < w) penalty_entry(logits, n, history, w, i, penalty);
 }
 
+// Windows of at most 64 ids skip k_smp_penalty: the first kernel of the
+// chain applies the masks and the penalty, each block to the ids in its
+// own range, on its staged logits, and writes the results back.
+struct SmpPen {
+    const int32_t *hist;                               // the window's ids
+    float *saved;                                      // the masked ids' values
+    int32_t w, m0, m1, n_mask;
+    float penalty;
+    int32_t on;                                        // 0: k_smp_penalty ran instead
+};
+
+// Wave 0 of a block whose logits [b0, b0 + len) are staged in xs: the
+// masks in order, each value saved first, then the penalty with repeats
+// compounding (the first occurrence of an id applies its count).
+__device__ void pen_block(float *xs, float *logits, int64_t n, int64_t b0, int32_t len, const SmpPen &pp) {
+    const int lane = threadIdx.x & 63;
+    if (lane == 0)
+        for (int32_t i = 0; i < pp.n_mask; i++) {
+            const int32_t t = i ? pp.m1 : pp.m0;
+            if (t >= b0 && t < b0 + len && t < n) {
+                pp.saved[i] = xs[t - b0];
+                xs[t - b0] = -__builtin_inff();
+                logits[t] = -__builtin_inff();
+            }
+        }
+    wave_lds_sync();
+    if (pp.penalty == 1.0f || pp.w == 0) return;
+    const int32_t t = lane < pp.w ? pp.hist[lane] : -1;
+    uint64_t m = __ballot(t >= b0 && t < b0 + len && t < n);
+    while (m) {
+        const int l = __builtin_ctzll(m);
+        m &= m - 1;
+        const int32_t tt = __builtin_amdgcn_readlane(t, l);
+        const uint64_t same = __ballot(t == tt);
+        if (__builtin_ctzll(same) != l) continue;      // not the id's first occurrence
+        if (lane == 0) {
+            float v = xs[tt - b0];
+            for (int r = __builtin_popcountll(same); r > 0; r--)
+                v = v > 0.0f ? __fdiv_rn(v, pp.penalty) : __fmul_rn(v, pp.penalty);
+            xs[tt - b0] = v;
+            logits[tt] = v;
+        }
+    }
+    wave_lds_sync();
+}
+
 // ---- greedy: sample_argmax (slm/model.c:401-412) ---------------------------
 // First index of the largest non-NaN logit; index 0 when logits[0] is NaN
 // (no later comparison can succeed then). Per block, then over blocks.
@@ -164,17 +210,31 @@ __device__ __forceinline__ void arg_reduce_wg(float &bv, int32_t &bi, ArgPart *s
         for (int w = 1; w < 4; w++) arg_better(bv, bi, sh[w].v, sh[w].i);
 }
 
-__global__ __launch_bounds__(256) void k_smp_argmax_part(const float *logits, int64_t n, ArgPart *part) {
+__global__ __launch_bounds__(256) void k_smp_argmax_part(float *logits, int64_t n, ArgPart *part, SmpPen pp) {
     __shared__ ArgPart sh[4];
+    __shared__ float xs[SMP_BLOCK];
     float bv = 0.0f;
     int32_t bi = -1;
     const int64_t base = (int64_t)blockIdx.x * SMP_BLOCK;
+    float xv[SMP_BLOCK / 256];
+#pragma unroll
     for (int j = 0; j < SMP_BLOCK / 256; j++) {
         const int64_t i = base + j * 256 + threadIdx.x;
-        if (i < n) {
-            const float v = logits[i];
-            if (v == v) arg_better(bv, bi, v, (int32_t)i);
-        }
+        xv[j] = i < n ? logits[i] : 0.0f;
+    }
+    if (pp.on) {                                       // uniform
+#pragma unroll
+        for (int j = 0; j < SMP_BLOCK / 256; j++) xs[j * 256 + threadIdx.x] = xv[j];
+        __syncthreads();
+        if (threadIdx.x < 64) pen_block(xs, logits, n, base, SMP_BLOCK, pp);
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < SMP_BLOCK / 256; j++) xv[j] = xs[j * 256 + threadIdx.x];
+    }
+#pragma unroll
+    for (int j = 0; j < SMP_BLOCK / 256; j++) {
+        const int64_t i = base + j * 256 + threadIdx.x;
+        if (i < n && xv[j] == xv[j]) arg_better(bv, bi, xv[j], (int32_t)i);
     }
     arg_reduce_wg(bv, bi, sh);
     if (threadIdx.x == 0) part[blockIdx.x] = ArgPart{bv, bi};
@@ -318,15 +378,43 @@ __host__ __device__ constexpr int smp_regs(int32_t k) { return k <= 64 ? 1 : (k 
 // initial fill holds a NaN. Each wave sorts its 64 * PER keys in
 // registers, then a tree of merges leaves the block's top 64R in wave 0.
 template <int PER, int R>
-__global__ __launch_bounds__(SMP_WG) void k_smp_blocks(const float *logits, int64_t n, int32_t k, float *tops,
-                                                       int32_t *nan_flag) {
+__global__ __launch_bounds__(SMP_WG) void k_smp_blocks(float *logits, int64_t n, int32_t k, float *tops,
+                                                       int32_t *nan_flag, SmpPen pp) {
     __shared__ uint32_t lds[16 * 64 * R];
+    __shared__ float xs[PER * SMP_WG];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t base = (int64_t)blockIdx.x * (PER * SMP_WG) + wave * 64 * PER;
+    const int64_t b0 = (int64_t)blockIdx.x * (PER * SMP_WG);
+    const int64_t base = b0 + wave * 64 * PER;
+    float xv[PER];
+#pragma unroll
+    for (int r = 0; r < PER; r++) {
+        const int64_t i = base + 64 * r + lane;
+        xv[r] = i < n ? logits[i] : 0.0f;
+    }
+    if (pp.on) {                                       // uniform
+#pragma unroll
+        for (int r = 0; r < PER; r++) xs[wave * 64 * PER + 64 * r + lane] = xv[r];
+        __syncthreads();
+        if (wave == 0) pen_block(xs, logits, n, b0, PER * SMP_WG, pp);
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < PER; r++) xv[r] = xs[wave * 64 * PER + 64 * r + lane];
+    }
     int32_t nan_fill = 0;
     uint32_t v[R];
 #pragma unroll
-    for (int r = 0; r < R; r++) v[r] = r < PER ? fkey(smp_load(logits, n, base + 64 * r + lane, k, nan_fill)) : 0u;
+    for (int r = 0; r < R; r++) {
+        v[r] = 0u;
+        if (r < PER) {
+            const int64_t i = base + 64 * r + lane;
+            float x = i < n ? xv[r] : -__builtin_inff();
+            if (x != x) {                              // as smp_load
+                if (i < k) nan_fill = 1;
+                x = -__builtin_inff();
+            }
+            v[r] = fkey(x);
+        }
+    }
     wave_sort_desc(v);
     const int nf = __syncthreads_or(nan_fill);
     wg_merge_top(v, lds);
@@ -1054,15 +1142,18 @@ hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k,
     const SmpMask mk{n_mask > 0 ? mask[0] : -1, n_mask > 1 ? mask[1] : -1, n_mask};
 
     const int32_t start = (window > 0 && window < hist_n) ? hist_n - window : 0;
-    hipLaunchKernelGGL(k_smp_penalty, dim3(1), dim3(256), 0, s, logits, n, history, start, hist_n, penalty, mk.m0,
-                       mk.m1, n_mask, saved);
     const int32_t w = hist_n - start;
-    if (w > SMP_HIST_LDS && penalty != 1.0f)
-        hipLaunchKernelGGL(k_smp_penalty_wide, dim3((unsigned)((w + 255) / 256)), dim3(256), 0, s, logits, n,
-                           history + start, w, penalty);
+    const SmpPen pp{w > 0 ? history + start : nullptr, saved, w, mk.m0, mk.m1, n_mask, penalty, w <= 64};
+    if (!pp.on) {
+        hipLaunchKernelGGL(k_smp_penalty, dim3(1), dim3(256), 0, s, logits, n, history, start, hist_n, penalty,
+                           mk.m0, mk.m1, n_mask, saved);
+        if (w > SMP_HIST_LDS && penalty != 1.0f)
+            hipLaunchKernelGGL(k_smp_penalty_wide, dim3((unsigned)((w + 255) / 256)), dim3(256), 0, s, logits, n,
+                               history + start, w, penalty);
+    }
     if (temperature <= 0.0f) {
         const int32_t ablk = (int32_t)((n + SMP_BLOCK - 1) / SMP_BLOCK);
-        hipLaunchKernelGGL(k_smp_argmax_part, dim3(ablk), dim3(256), 0, s, logits, n, part);
+        hipLaunchKernelGGL(k_smp_argmax_part, dim3(ablk), dim3(256), 0, s, logits, n, part, pp);
         hipLaunchKernelGGL(k_smp_argmax_final, dim3(1), dim3(256), 0, s, logits, n, part, ablk, token, mk, saved);
         return hipGetLastError();
     }
@@ -1074,7 +1165,7 @@ hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k,
     auto events = R == 1 ? k_smp_events<1, 1>
                 : R == 2 ? (sb == 1024 ? k_smp_events<1, 2> : k_smp_events<2, 2>)
                          : (sb == 1024 ? k_smp_events<1, 4> : sb == 2048 ? k_smp_events<2, 4> : k_smp_events<4, 4>);
-    hipLaunchKernelGGL(blocks, dim3(nblk), dim3(SMP_WG), 0, s, logits, n, k, tops, nan_flag);
+    hipLaunchKernelGGL(blocks, dim3(nblk), dim3(SMP_WG), 0, s, logits, n, k, tops, nan_flag, pp);
     hipLaunchKernelGGL(events, dim3(nblk), dim3(SMP_WG), 0, s, logits, n, k, tops, ev_idx, ev_val, ev_n);
     hipLaunchKernelGGL(k_smp_slots, dim3(1), dim3(1024), 0, s, logits, n, k, sb, nblk, ev_idx, ev_val, ev_n,
                        nan_flag, res_val, res_idx, res_ok);
