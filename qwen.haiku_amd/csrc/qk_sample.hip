@@ -442,7 +442,8 @@ __global__ __launch_bounds__(SMP_WG) void k_smp_blocks(float *logits, int64_t n,
 // 64R of P and of the sub-chunks before c comes from a prefix scan of the
 // waves' tops (Hillis-Steele over 16 waves) and the wave's own earlier
 // sub-chunks. A candidate's count is then a binary search in that sorted
-// top plus the earlier lanes of its sub-chunk, read lane by lane.
+// top plus the earlier lanes of its sub-chunk, read lane by lane. A block
+// with at most 64 candidates skips the scan: one wave holds them all.
 template <int R>
 __device__ __forceinline__ void wave_put(uint32_t *dst, const uint32_t (&v)[R]) {
     const int lane = threadIdx.x & 63;
@@ -464,7 +465,11 @@ __global__ __launch_bounds__(SMP_WG) void k_smp_events(const float *logits, int6
     constexpr int LB = 16 / R;                         // lists loaded per batch (a power of two)
     __shared__ uint32_t lds[16 * 64 * R];              // merge exchanges, then each wave's running top
     __shared__ uint32_t pb[64 * R];                    // the top of P, sorted
-    __shared__ int32_t ecnt[16 * PER];                 // events per sub-chunk, then their offsets
+    __shared__ int32_t ecnt[16 * PER];                 // candidates, then events per sub-chunk; offsets
+    __shared__ uint32_t c1k[64];                       // at most 64 candidates: keys, indices, values
+    __shared__ int32_t c1i[64];
+    __shared__ float c1v[64];
+    __shared__ int32_t ncand_sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int32_t b = blockIdx.x;
     const int64_t base = (int64_t)b * SB;
@@ -500,11 +505,76 @@ __global__ __launch_bounds__(SMP_WG) void k_smp_events(const float *logits, int6
         tkey = pb[k - 1];
     }
     // keys of the candidates; 0 (counts for nothing) elsewhere
-    uint32_t key[PER], cl[PER][R];
+    uint32_t key[PER];
 #pragma unroll
     for (int j = 0; j < PER; j++) {
         const uint32_t kx = fkey(x[j]);
         key[j] = (b > 0 ? kx > tkey : x[j] > -__builtin_inff()) ? kx : 0u;
+    }
+    // at most 64 candidates (every block but the first, for typical
+    // logits): one wave takes them in index order, one per lane
+    int32_t *cc = ecnt;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const uint64_t m = __ballot(key[j] != 0u);
+        if (lane == 0) cc[wave * PER + j] = __builtin_popcountll(m);
+    }
+    __syncthreads();
+    if (wave == 0) {                                   // exclusive scan of the candidate counts
+        const int32_t c = lane < 16 * PER ? cc[lane] : 0;
+        int32_t inc = c;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int32_t y = __shfl_up(inc, o);
+            if (lane >= o) inc += y;
+        }
+        if (lane < 16 * PER) cc[lane] = inc - c;
+        if (lane == 63) ncand_sh = inc;
+    }
+    __syncthreads();
+    const int32_t ncand = ncand_sh;
+    if (ncand <= 64) {                                 // uniform
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const uint64_t m = __ballot(key[j] != 0u);
+            if (key[j] != 0u) {
+                const int32_t pos = cc[wave * PER + j] + __builtin_popcountll(m & ((1ull << lane) - 1));
+                c1k[pos] = key[j];
+                c1i[pos] = (int32_t)(base + 64 * (wave * PER + j) + lane);
+                c1v[pos] = x[j];
+            }
+        }
+        __syncthreads();
+        if (wave != 0) return;
+        const uint32_t kv = lane < ncand ? c1k[lane] : 0u;
+        const int32_t idx = lane < ncand ? c1i[lane] : 0;
+        bool ev = false;
+        int32_t cnt = 0;
+        if (kv != 0u && idx >= k) {                    // the initial fill never enters
+            if (b > 0)
+#pragma unroll
+                for (int step = 64 * R; step > 0; step >>= 1)
+                    if (cnt + step <= k && pb[cnt + step - 1] >= kv) cnt += step;
+            ev = cnt < k;
+        }
+        if (__ballot(ev)) {                            // plus the earlier candidates
+            for (int l2 = 0; l2 < 63; l2++) {
+                const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int32_t)kv, l2);
+                cnt += (l2 < lane) & (o >= kv);
+            }
+            ev = ev && cnt < k;
+        }
+        const uint64_t m = __ballot(ev);
+        if (ev) {
+            const int32_t pos = __builtin_popcountll(m & ((1ull << lane) - 1));
+            ev_idx[base + pos] = idx;
+            ev_val[base + pos] = c1v[lane];
+        }
+        if (lane == 0) ev_n[b] = __builtin_popcountll(m);
+        return;
+    }
+    uint32_t cl[PER][R];                               // the sub-chunks, sorted
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
         uint32_t one[1] = {key[j]};
         wave_sort_desc(one);
         cl[j][0] = one[0];
@@ -541,7 +611,8 @@ __global__ __launch_bounds__(SMP_WG) void k_smp_events(const float *logits, int6
         wave_merge_top(top, p);
     }
     __syncthreads();                                   // every wave has read the scan's slots
-    // counts, sub-chunk by sub-chunk; `top` is the sorted top of everything
+    // (ecnt is free again: every wave read its candidate offsets before the
+    // scan's barriers) counts, sub-chunk by sub-chunk; `top` is the sorted top of everything
     // before the sub-chunk
     int32_t evf = 0;
 #pragma unroll
