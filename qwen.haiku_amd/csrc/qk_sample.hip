@@ -21,13 +21,13 @@
 //    k, plus the block's own earlier candidates). Those with a count
 //    below k are the entering events, listed in index order with their
 //    values (k_smp_events);
-//  * the final slots: in closed form when the values are distinct
-//    (k_smp_slots), else one wave replays the events in order on the k
-//    slots; then the rest of the chain on the k survivors as the
-//    reference writes it (k_smp_finish).
+//  * the final slots: in closed form when the values are distinct, else
+//    one wave replays the events in order on the k slots; then the rest
+//    of the chain on the k survivors as the reference writes it
+//    (k_smp_pick).
 // A NaN logit after the first k never enters and never compares >=, so it
 // counts as -inf; a NaN among the first k breaks the prefix argument
-// (comparisons with it are false), so k_smp_finish then runs
+// (comparisons with it are false), so k_smp_pick then runs
 // topk_collect literally.
 #include "qk_dev.h"
 #include "qk_expf.h"
@@ -273,7 +273,7 @@ __global__ __launch_bounds__(256) void k_smp_argmax_final(float *logits, int64_t
 // that nblk * k <= SMP_LIST_MAX). A NaN logit at an index >= k never
 // enters the slots and never compares >= anything, so it is read as -inf
 // here; a NaN among the first k (the initial fill) is flagged instead and
-// k_smp_finish then runs topk_collect literally.
+// k_smp_pick then runs topk_collect literally.
 constexpr int SMP_LIST_MAX = 16384;                    // keys of the prefix lists a block holds
 constexpr int SMP_WG = 1024;                           // threads of the selection kernels (16 waves)
 constexpr int SMP_SBMAX = 4096;                        // largest block
@@ -292,7 +292,8 @@ __device__ __forceinline__ float smp_load(const float *logits, int64_t n, int64_
 // A wave holds 64R keys, element e = 64r + lane in register r; the sorts
 // and merges below order them descending (key 0 is padding, below every
 // real key). Cross-lane exchanges go through DPP (lane ^ 1, 2, 8),
-// ds_swizzle (^ 4, 16) or ds_bpermute (^ 32, and the reversal).
+// ds_swizzle (^ 4, 16) or ds_bpermute (^ 32, and the reversal); an
+// all-VALU set (row shifts, v_permlane16/32_swap) measured slower.
 __device__ __forceinline__ uint32_t lane_xor(uint32_t v, int s) {
     switch (s) {
         case 1: return (uint32_t)dpp_xor1((int32_t)v);
@@ -302,6 +303,11 @@ __device__ __forceinline__ uint32_t lane_xor(uint32_t v, int s) {
         case 16: return (uint32_t)__builtin_amdgcn_ds_swizzle((int32_t)v, 0x401F);
         default: return (uint32_t)__shfl_xor((int32_t)v, 32);
     }
+}
+
+// Lane l <- lane 63 - l.
+__device__ __forceinline__ uint32_t lane_rev(uint32_t v) {
+    return (uint32_t)__shfl((int32_t)v, 63 - (int)(threadIdx.x & 63));
 }
 
 // One compare-exchange stage of a bitonic network over the wave's list:
@@ -344,11 +350,23 @@ __device__ __forceinline__ void wave_sort_desc(uint32_t (&v)[R]) {
 // is that top as a bitonic sequence, then one bitonic merge.
 template <int R>
 __device__ __forceinline__ void wave_merge_top(uint32_t (&a)[R], const uint32_t (&b)[R]) {
-    const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int r = 0; r < R; r++) a[r] = max(a[r], (uint32_t)__shfl((int32_t)b[R - 1 - r], 63 - lane));
+    for (int r = 0; r < R; r++) a[r] = max(a[r], lane_rev(b[R - 1 - r]));
 #pragma unroll
     for (int stride = 32 * R; stride > 0; stride >>= 1) bitonic_stage(a, 128 * R, stride);
+}
+
+// c := a and b (both sorted, 64R keys each) merged, sorted: a followed by
+// b reversed is a bitonic sequence; one bitonic merge over 2R registers.
+template <int R>
+__device__ __forceinline__ void wave_merge_all(const uint32_t (&a)[R], const uint32_t (&b)[R], uint32_t (&c)[2 * R]) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        c[r] = a[r];
+        c[R + r] = lane_rev(b[R - 1 - r]);
+    }
+#pragma unroll
+    for (int stride = 64 * R; stride > 0; stride >>= 1) bitonic_stage(c, 256 * R, stride);
 }
 
 // Every wave holds a sorted list; afterwards wave 0 holds the top 64R of
@@ -666,149 +684,6 @@ __global__ __launch_bounds__(SMP_WG) void k_smp_events(const float *logits, int6
     }
 }
 
-// ---- the final slots without a replay -------------------------------------------
-// When the k fill values and the entering events are all distinct, the
-// replay has a closed form. Each event evicts the smallest slot value,
-// and what enters is larger than what leaves, so the evicted values come
-// out strictly increasing: the j-th event (in index order) evicts the
-// element of rank j among all N = k + events elements (the N - k
-// smallest are exactly the evicted ones, the k largest the survivors).
-// That element sits in its own fill slot, or in the slot of the earlier
-// event that brought it in, so every event's slot is found by pointer
-// jumping over "evicts the element of rank j". One workgroup sorts the
-// elements by key (a bitonic sort in LDS), resolves the chains and writes
-// each survivor into its slot; k_smp_finish then skips its replay. Ties
-// (equal keys, -0 and +0 included), a NaN in the fill or more than
-// SMP_NMAX elements leave *ok = 0 and the replay runs.
-constexpr int SMP_NMAX = 4096;
-constexpr int SMP_NSORT = 4096;                        // sort capacity: a power of two >= SMP_NMAX
-
-__global__ __launch_bounds__(1024) void k_smp_slots(const float *logits, int64_t n, int32_t k, int32_t sb,
-                                                    int32_t nblk, const int32_t *ev_idx, const float *ev_val,
-                                                    const int32_t *ev_n, const int32_t *nan_flag, float *res_val,
-                                                    int32_t *res_idx, int32_t *ok) {
-    // (key << 32 | element) pairs, sorted ascending; then, as 32-bit
-    // words, the element of each rank and the resolved slots
-    __shared__ uint64_t buf[SMP_NSORT];
-    __shared__ int32_t off[SMP_KMAX + 1];
-    __shared__ int32_t skip;
-    int32_t *byr = reinterpret_cast<int32_t *>(buf);
-    const int tid = threadIdx.x;
-    if (tid < 64) {
-        // event offsets: wave-parallel exclusive scan, lane l owning blocks
-        // 4l .. 4l+3 (every load in flight at once); NaN in the fill
-        const int lane = tid;
-        int32_t nf = 0, c4[4], own = 0;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int32_t b = 4 * lane + q;
-            nf |= b < nblk ? nan_flag[b] : 0;
-            c4[q] = b < nblk ? ev_n[b] : 0;
-            own += c4[q];
-        }
-        const bool nan_fill = __ballot(nf != 0) != 0;
-        int32_t incl = own;
-        for (int o = 1; o < 64; o <<= 1) {
-            const int32_t y = __shfl_up(incl, o);
-            if (lane >= o) incl += y;
-        }
-        int32_t acc = incl - own;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            if (4 * lane + q <= nblk) off[4 * lane + q] = acc;
-            acc += c4[q];
-        }
-        const int32_t total = __builtin_amdgcn_readlane(incl, 63);
-        if (lane == 0) {
-            off[nblk] = total;
-            skip = nan_fill || n <= k || total == 0 || k + total > SMP_NMAX;
-            if (skip) *ok = 0;
-        }
-    }
-    __syncthreads();
-    if (skip) return;                                  // uniform
-    const int32_t total = off[nblk], N = k + total;
-    // element e: the fill slot e < k, or event e - k (in index order)
-    auto locate = [&](int32_t j) -> int64_t {          // scratch position of event j
-        int32_t lo = 0, hi = nblk;                     // last block with off[block] <= j
-        while (hi - lo > 1) {
-            const int32_t mid = (lo + hi) >> 1;
-            if (off[mid] <= j) lo = mid;
-            else hi = mid;
-        }
-        return (int64_t)lo * sb + (j - off[lo]);
-    };
-    int32_t P = 2;
-    while (P < N) P <<= 1;                             // <= SMP_NSORT
-    for (int32_t e = tid; e < P; e += 1024) {
-        uint64_t v = ~0ull;                            // padding sorts last
-        if (e < N) {
-            const float x = e < k ? logits[e] : ev_val[locate(e - k)];
-            v = ((uint64_t)fkey(x) << 32) | (uint32_t)e;
-        }
-        buf[e] = v;
-    }
-    __syncthreads();
-    for (int32_t size = 2; size <= P; size <<= 1) {    // bitonic sort, ascending
-        for (int32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int32_t i = tid; i < (P >> 1); i += 1024) {
-                const int32_t lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
-                const uint64_t a = buf[lo], b = buf[hi];
-                const bool up = (lo & size) == 0;
-                if ((a > b) == up) {
-                    buf[lo] = b;
-                    buf[hi] = a;
-                }
-            }
-            __syncthreads();
-        }
-    }
-    // ties (equal keys, -0 and +0 included) leave the order to the replay
-    int tie = 0;
-    for (int32_t r = 1 + tid; r < N; r += 1024) tie |= (buf[r] >> 32) == (buf[r - 1] >> 32);
-    if (__syncthreads_or(tie)) {
-        if (tid == 0) *ok = 0;
-        return;
-    }
-    // ranks -> elements, in place: every thread reads its entries first
-    int32_t mine[SMP_NSORT / 1024];
-#pragma unroll
-    for (int q = 0; q < SMP_NSORT / 1024; q++) {
-        const int32_t r = tid + 1024 * q;
-        mine[q] = r < N ? (int32_t)(uint32_t)buf[r] : 0;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < SMP_NSORT / 1024; q++) {
-        const int32_t r = tid + 1024 * q;
-        if (r < N) byr[r] = mine[q];
-    }
-    __syncthreads();
-    // event j evicts element byr[j]: a fill slot, or event byr[j] - k's slot
-    for (int32_t len = 1; len < 2 * total; len <<= 1) {
-        for (int32_t j = tid; j < total; j += 1024) {
-            const int32_t p = byr[j];
-            if (p >= k) byr[j] = byr[p - k];
-        }
-        __syncthreads();
-    }
-    for (int32_t r = total + tid; r < N; r += 1024) {    // the survivors into their slots
-        const int32_t e = byr[r];
-        const int32_t slot = e < k ? e : byr[e - k];
-        if (e < k) {
-            res_val[slot] = logits[e];
-            res_idx[slot] = e;
-        } else {
-            const int64_t at = locate(e - k);
-            res_val[slot] = ev_val[at];
-            res_idx[slot] = ev_idx[at];
-        }
-    }
-    if (tid == 0) *ok = 1;
-}
-
-// One wave: the k slots (LDS), the replay of the events, then the rest of
-// sample_with on lane 0.
 struct SmpArgs {
     float temperature, top_p, min_p;
     int32_t k, sb, nblk;
@@ -932,30 +807,87 @@ __device__ void chain_literal(float *val, int32_t *idx, int32_t filled, const Sm
     *token = idx[picked];
 }
 
-constexpr int SMP_FIN = 256;                           // threads of k_smp_finish
+// ---- the slots and the pick ------------------------------------------------------
+// When the k fill values and the entering events are all distinct, the
+// replay has a closed form. Each event evicts the smallest slot value,
+// and what enters is larger than what leaves, so the evicted values come
+// out strictly increasing: the j-th event (in index order) evicts the
+// element of rank j among all N = k + events elements (the N - k
+// smallest are exactly the evicted ones, the k largest the survivors).
+// That element sits in its own fill slot, or in the slot of the earlier
+// event that brought it in, so every event's slot follows from the slots
+// of earlier events. One workgroup ranks the elements (by counting for
+// N <= 1024, else a bitonic sort in LDS), resolves the slots in event
+// order (one wave, 64 at a time, pointer jumping inside each group) and
+// places the survivors. Ties (equal keys, -0 and +0 included), a NaN in
+// the fill or more than SMP_NMAX elements send it to the replay instead:
+// one wave replays the events in order on the k slots. Then the rest of
+// the chain: the softmax numerators, their sum in slot order and the
+// quotients (wave 0), the ranking of the probabilities (every thread),
+// the cut and the pick (wave 0), and the masked ids get their saved values
+// back.
+constexpr int SMP_NMAX = 4096;
 
-// Wave 0 places the k slots (from k_smp_slots, or by replaying the
-// events), forms the softmax numerators, their sum in slot order and the
-// quotients; the four waves rank the probabilities (topk_sort_desc's
-// order); wave 0 then cuts and picks. The masked ids get their saved
-// values back last, on every path.
-__global__ __launch_bounds__(SMP_FIN) void k_smp_finish(float *logits, int64_t n, SmpArgs a, const int32_t *ev_idx,
-                                                        const float *ev_val, const int32_t *ev_n,
-                                                        const int32_t *nan_flag, const float *res_val,
-                                                        const int32_t *res_idx, const int32_t *res_ok, uint64_t *rng,
-                                                        int32_t *token, SmpMask mk, const float *saved) {
-    __shared__ __align__(16) float val[SMP_KMAX];
-    __shared__ int32_t idx[SMP_KMAX];
+// One level of wg_sort_keys: waves w with w % 2l == 0 merge wave w + l's
+// list into theirs (exchanged through ex).
+template <int RC>
+__device__ __forceinline__ void sort_level(const uint32_t (&cur)[RC], uint32_t (&nxt)[2 * RC], int l, uint32_t *ex) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if ((wave & (2 * l - 1)) == l)
+#pragma unroll
+        for (int r = 0; r < RC; r++) ex[(wave >> 1) * 64 * RC + 64 * r + lane] = cur[r];
+    __syncthreads();
+    if ((wave & (2 * l - 1)) == 0) {
+        uint32_t o[RC];
+#pragma unroll
+        for (int r = 0; r < RC; r++) o[r] = ex[((wave + l) >> 1) * 64 * RC + 64 * r + lane];
+        wave_merge_all(cur, o, nxt);
+    }
+    __syncthreads();
+}
+
+// The keys of elements [0, N), N <= 1024 RW, sorted descending into out
+// (key 0 pads): each wave sorts its 64 RW keys in registers, then four
+// levels of merges leave them all in wave 0. ex: 8 * 64 * 8 RW keys.
+template <int RW>
+__device__ __forceinline__ void wg_sort_keys(const uint32_t *keys, int32_t N, uint32_t *ex, uint32_t *out) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t v1[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const int32_t e = wave * 64 * RW + 64 * r + lane;
+        v1[r] = e < N ? keys[e] : 0u;
+    }
+    wave_sort_desc(v1);
+    uint32_t v2[2 * RW], v4[4 * RW], v8[8 * RW], v16[16 * RW];
+    sort_level(v1, v2, 1, ex);
+    sort_level(v2, v4, 2, ex);
+    sort_level(v4, v8, 4, ex);
+    sort_level(v8, v16, 8, ex);
+    if (wave == 0)
+#pragma unroll
+        for (int r = 0; r < 16 * RW; r++) out[64 * r + lane] = v16[r];
+}
+
+__global__ __launch_bounds__(SMP_WG) void k_smp_pick(float *logits, int64_t n, SmpArgs a, const int32_t *ev_idx,
+                                                     const float *ev_val, const int32_t *ev_n,
+                                                     const int32_t *nan_flag, uint64_t *rng, int32_t *token,
+                                                     SmpMask mk, const float *saved) {
     __shared__ int32_t off[SMP_KMAX + 1];              // event offsets per block (nblk <= 256)
+    __shared__ __align__(16) uint32_t skey[SMP_NMAX];  // element e: fill slot e < k, or event e - k
+    __shared__ float sval[SMP_NMAX];
+    __shared__ int32_t sid[SMP_NMAX];
+    __shared__ int32_t byr[SMP_NMAX];                  // element of each rank; then the events' slots
+    __shared__ uint64_t buf[SMP_NMAX];                 // (key << 32 | element), for the sort
+    __shared__ __align__(16) float val[SMP_KMAX];      // the slots: values, then probabilities
+    __shared__ int32_t idx[SMP_KMAX];
     __shared__ float sp[SMP_KMAX];                     // probabilities in sorted order
     __shared__ int32_t si[SMP_KMAX];
-    __shared__ int32_t done_sh;
+    __shared__ int32_t total_sh, nanf_sh, done_sh;
     const int tid = threadIdx.x, lane = tid & 63;
     const int32_t k = a.k, nblk = a.nblk;
     const int32_t filled = (int32_t)(n < k ? n : k);
-    // Wave 0: returns true when it ran the chain to the end literally (a
-    // NaN in the fill, or a NaN probability).
-    auto slots_softmax = [&]() -> bool {
+    if (tid < 64) {
         // NaN in the fill; event offsets (wave-parallel exclusive scan,
         // lane l owning blocks 4l .. 4l+3)
         int32_t nf = 0, c4[4], own = 0;
@@ -978,19 +910,139 @@ __global__ __launch_bounds__(SMP_FIN) void k_smp_finish(float *logits, int64_t n
             if (4 * lane + q <= nblk) off[4 * lane + q] = acc;
             acc += c4[q];
         }
-        const int32_t total = __builtin_amdgcn_readlane(incl, 63);
-        if (lane == 0) off[nblk] = total;
+        if (lane == 0) {
+            total_sh = __builtin_amdgcn_readlane(incl, 63);
+            nanf_sh = nan_in_fill;
+        }
+    }
+    __syncthreads();
+    const int32_t total = n > k ? total_sh : 0;
+    const bool nan_in_fill = nanf_sh != 0;
+    const int32_t N = k + total;
+    // scratch position of event j: the last block with off[block] <= j
+    auto locate = [&](int32_t j) -> int64_t {
+        int32_t lo = 0, hi = nblk;
+        while (hi - lo > 1) {
+            const int32_t mid = (lo + hi) >> 1;
+            if (off[mid] <= j) lo = mid;
+            else hi = mid;
+        }
+        return (int64_t)lo * a.sb + (j - off[lo]);
+    };
+    // the closed form applies: no NaN in the fill, events to place, room
+    bool closed = !nan_in_fill && total > 0 && N <= SMP_NMAX;
+    if (closed) {                                      // uniform
+        for (int32_t e = tid; e < N; e += SMP_WG) {
+            float x;
+            int32_t id;
+            if (e < k) {
+                x = logits[e];
+                id = e;
+            } else {
+                const int64_t at = locate(e - k);
+                x = ev_val[at];
+                id = ev_idx[at];
+            }
+            skey[e] = fkey(x);
+            sval[e] = x;
+            sid[e] = id;
+        }
+        __syncthreads();
+        int tie = 0;
+        if (N <= 2 * SMP_WG) {                         // sorted in registers; ranks by binary search
+            uint32_t *sorted = reinterpret_cast<uint32_t *>(buf);   // 2048 keys, then the exchange area
+            uint32_t *ex = sorted + 2 * SMP_WG;
+            if (N <= SMP_WG) wg_sort_keys<1>(skey, N, ex, sorted);
+            else wg_sort_keys<2>(skey, N, ex, sorted);
+            __syncthreads();
+            for (int32_t e = tid; e < N; e += SMP_WG) {
+                const uint32_t kv = skey[e];
+                int32_t pos = 0;                       // keys above kv
+                for (int32_t step = 2 * SMP_WG; step > 0; step >>= 1)
+                    if (pos + step <= N && sorted[pos + step - 1] > kv) pos += step;
+                tie |= pos + 1 < N && sorted[pos + 1] == kv;   // another key equal to kv
+                byr[N - 1 - pos] = e;
+            }
+        } else {                                       // bitonic sort of (key, element), ascending
+            int32_t P = 2;
+            while (P < N) P <<= 1;                     // <= SMP_NMAX
+            for (int32_t e = tid; e < P; e += SMP_WG)
+                buf[e] = e < N ? ((uint64_t)skey[e] << 32) | (uint32_t)e : ~0ull;   // padding sorts last
+            __syncthreads();
+            for (int32_t size = 2; size <= P; size <<= 1) {
+                for (int32_t stride = size >> 1; stride > 0; stride >>= 1) {
+                    for (int32_t i = tid; i < (P >> 1); i += SMP_WG) {
+                        const int32_t lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+                        const uint64_t x0 = buf[lo], x1 = buf[hi];
+                        const bool up = (lo & size) == 0;
+                        if ((x0 > x1) == up) {
+                            buf[lo] = x1;
+                            buf[hi] = x0;
+                        }
+                    }
+                    __syncthreads();
+                }
+            }
+            for (int32_t r = tid; r < N; r += SMP_WG) {
+                byr[r] = (int32_t)(uint32_t)buf[r];
+                tie |= r > 0 && (buf[r] >> 32) == (buf[r - 1] >> 32);
+            }
+        }
+        closed = !__syncthreads_or(tie);               // ties leave the order to the replay
+    }
+    if (closed) {
+        if (tid < 64) {                                // event j's slot, in event order
+            for (int32_t c0 = 0; c0 < total; c0 += 64) {
+                const int32_t j = c0 + lane;
+                int32_t p = j < total ? byr[j] : 0;    // the element event j evicts
+                int32_t slot = p, d = -1;              // resolved slot, or the in-group event it waits on
+                if (j < total && p >= k) {
+                    if (p - k < c0) slot = byr[p - k];   // an earlier group: resolved already
+                    else d = p - k - c0;               // an earlier lane of this group
+                }
+                for (int it = 0; it < 6 && __ballot(d >= 0); it++) {   // pointer jumping inside the group
+                    const int32_t ts = __shfl(slot, d < 0 ? lane : d);
+                    const int32_t td = __shfl(d, d < 0 ? lane : d);
+                    if (d >= 0) {
+                        if (td < 0) {
+                            slot = ts;
+                            d = -1;
+                        } else {
+                            d = td;
+                        }
+                    }
+                }
+                wave_lds_sync();                       // every lane has read byr for this group
+                if (j < total) byr[j] = slot;
+                wave_lds_sync();
+            }
+        }
+        __syncthreads();
+        for (int32_t r = total + tid; r < N; r += SMP_WG) {   // the survivors into their slots
+            const int32_t e = byr[r];
+            const int32_t slot = e < k ? e : byr[e - k];
+            val[slot] = sval[e];
+            idx[slot] = sid[e];
+        }
+    } else {
+        for (int32_t s_ = tid; s_ < filled; s_ += SMP_WG) {   // the fill
+            val[s_] = logits[s_];
+            idx[s_] = s_;
+        }
+    }
+    __syncthreads();
+    // Wave 0: returns true when it ran the chain to the end literally (a
+    // NaN in the fill, or a NaN probability).
+    auto slots_softmax = [&]() -> bool {
         float sv[SMP_Q];
         int32_t sx[SMP_Q];
-        const bool resolved = *res_ok != 0;            // k_smp_slots placed the survivors
 #pragma unroll
         for (int q = 0; q < SMP_Q; q++) {
             const int32_t s_ = q * 64 + lane;
-            sv[q] = s_ < filled ? (resolved ? res_val[s_] : logits[s_]) : 0.0f;
-            sx[q] = resolved && s_ < filled ? res_idx[s_] : s_;
+            sv[q] = s_ < filled ? val[s_] : 0.0f;
+            sx[q] = s_ < filled ? idx[s_] : s_;
         }
-        wave_lds_sync();
-        if (!resolved && !nan_in_fill && n > k && total > 0) {
+        if (!closed && !nan_in_fill && total > 0) {   // the replay
             float mv;
             int32_t ms;
             slot_min(sv, k, mv, ms);
@@ -1018,16 +1070,16 @@ __global__ __launch_bounds__(SMP_FIN) void k_smp_finish(float *logits, int64_t n
                 gi = ni;
                 gv = nv;
             }
-        }
 #pragma unroll
-        for (int q = 0; q < SMP_Q; q++) {
-            const int32_t s_ = q * 64 + lane;
-            if (s_ < filled) {
-                val[s_] = sv[q];
-                idx[s_] = sx[q];
+            for (int q = 0; q < SMP_Q; q++) {
+                const int32_t s_ = q * 64 + lane;
+                if (s_ < filled) {
+                    val[s_] = sv[q];
+                    idx[s_] = sx[q];
+                }
             }
+            wave_lds_sync();
         }
-        wave_lds_sync();
         if (nan_in_fill) {
             if (lane == 0) {
                 if (n > k)                             // topk_collect as written (slm/sampler.c:74-92)
@@ -1065,10 +1117,12 @@ __global__ __launch_bounds__(SMP_FIN) void k_smp_finish(float *logits, int64_t n
             if (lane == 0) chain_literal(val, idx, filled, a, rng, token);
             return true;
         }
-        float sum = 0.0f;
+        float sum = 0.0f;                              // in slot order; slots past filled add +0
 #pragma unroll
         for (int q = 0; q < SMP_Q; q++)
-            for (int32_t l = 0; l < 64 && q * 64 + l < filled; l++) sum = __fadd_rn(sum, readlane_f(pe[q], l));
+            if (q * 64 < filled)
+#pragma unroll
+                for (int l = 0; l < 64; l++) sum = __fadd_rn(sum, readlane_f(pe[q], l));
         if (sum > 0.0f)
 #pragma unroll
             for (int q = 0; q < SMP_Q; q++) pe[q] = __fdiv_rn(pe[q], sum);
@@ -1090,20 +1144,28 @@ __global__ __launch_bounds__(SMP_FIN) void k_smp_finish(float *logits, int64_t n
     // topk_sort_desc (slm/sampler.c:116-129) is a stable sort by
     // descending value: rank = #greater + #equal in earlier slots; one
     // slot per thread, the probabilities read four at a time
-    if (!done && tid < filled) {
-        const float v = val[tid];
+    if (!done) {                                       // uniform; four threads per slot
+        const int32_t sl = tid >> 2, t0 = (tid & 3) * 64;
+        const int32_t nf4 = (filled + 3) & ~3, t1 = t0 + 64 < nf4 ? t0 + 64 : nf4;
+        float v = 0.0f;
         int32_t r = 0;
-        const int32_t nf4 = (filled + 3) & ~3;
+        if (sl < filled) {
+            v = val[sl];
 #pragma unroll 4
-        for (int32_t t = 0; t < nf4; t += 4) {
-            const float4 w = *reinterpret_cast<const float4 *>(&val[t]);
-            r += (w.x > v) | ((w.x == v) & (t < tid));
-            r += (w.y > v) | ((w.y == v) & (t + 1 < tid));
-            r += (w.z > v) | ((w.z == v) & (t + 2 < tid));
-            r += (w.w > v) | ((w.w == v) & (t + 3 < tid));
+            for (int32_t t = t0; t < t1; t += 4) {
+                const float4 w = *reinterpret_cast<const float4 *>(&val[t]);
+                r += (w.x > v) | ((w.x == v) & (t < sl));
+                r += (w.y > v) | ((w.y == v) & (t + 1 < sl));
+                r += (w.z > v) | ((w.z == v) & (t + 2 < sl));
+                r += (w.w > v) | ((w.w == v) & (t + 3 < sl));
+            }
         }
-        sp[r] = v;
-        si[r] = idx[tid];
+        r += dpp_xor1(r);                              // the quad's four parts
+        r += dpp_xor2(r);
+        if (sl < filled && (tid & 3) == 0) {
+            sp[r] = v;
+            si[r] = idx[sl];
+        }
     }
     __syncthreads();
     if (tid >= 64) return;
@@ -1112,51 +1174,53 @@ __global__ __launch_bounds__(SMP_FIN) void k_smp_finish(float *logits, int64_t n
 #pragma unroll
         for (int q = 0; q < SMP_Q; q++) sq[q] = q * 64 + lane < filled ? sp[q * 64 + lane] : 0.0f;
         // top-p, min-p, renormalized roulette pick (slm/sampler.c:150-178);
-        // the sorted probability j is register j / 64 of lane j % 64
+        // the sorted probability j is register j / 64 of lane j % 64. The
+        // three running sums there (top-p's acc, the total over the cut,
+        // the pick's c) are one sequence of adds from 0 in sorted order, so
+        // one pass keeps every partial sum (lane j % 64 of pre[j / 64]);
+        // entries past filled add +0.
+        float pre[SMP_Q];
+        float acc = 0.0f;
+#pragma unroll
+        for (int q = 0; q < SMP_Q; q++) {
+            pre[q] = 0.0f;
+            if (q * 64 < filled)
+#pragma unroll
+                for (int l = 0; l < 64; l++) {
+                    acc = __fadd_rn(acc, readlane_f(sq[q], l));
+                    pre[q] = lane == l ? acc : pre[q];
+                }
+        }
+        // the first j meeting a per-lane predicate, or -1
+        auto first = [&](auto pred) -> int32_t {
+#pragma unroll
+            for (int q = 0; q < SMP_Q; q++) {
+                const uint64_t m = __ballot(q * 64 + lane < filled && pred(q));
+                if (m) return q * 64 + (int32_t)__builtin_ctzll(m);
+            }
+            return -1;
+        };
         int32_t cutoff = filled;
         if (a.top_p > 0.0f && a.top_p < 1.0f) {
-            float acc = 0.0f;
-            bool fin = false;
-#pragma unroll
-            for (int q = 0; q < SMP_Q; q++)
-                for (int32_t l = 0; l < 64 && !fin && q * 64 + l < filled; l++) {
-                    acc = __fadd_rn(acc, readlane_f(sq[q], l));
-                    if (acc >= a.top_p) {
-                        cutoff = q * 64 + l + 1;
-                        fin = true;
-                    }
-                }
+            const int32_t j = first([&](int q) { return pre[q] >= a.top_p; });
+            if (j >= 0) cutoff = j + 1;
         }
         if (a.min_p > 0.0f) {
             const float thresh = __fmul_rn(a.min_p, readlane_f(sq[0], 0));
-            int32_t j = 1;
-            bool fin = false;
-#pragma unroll
-            for (int q = 0; q < SMP_Q; q++)
-                for (int32_t l = q == 0 ? 1 : 0; l < 64 && !fin; l++) {
-                    if (j < cutoff && readlane_f(sq[q], l) >= thresh) j++;
-                    else fin = true;
-                }
-            cutoff = j;
+            const int32_t c0 = cutoff;
+            const int32_t j = first([&](int q) { return q * 64 + lane >= 1 && q * 64 + lane < c0 && !(sq[q] >= thresh); });
+            cutoff = j >= 0 ? j : (c0 > 1 ? c0 : 1);
         }
+        const int32_t lt = cutoff - 1;
         float tot = 0.0f;
 #pragma unroll
         for (int q = 0; q < SMP_Q; q++)
-            for (int32_t l = 0; l < 64 && q * 64 + l < cutoff; l++) tot = __fadd_rn(tot, readlane_f(sq[q], l));
+            if (q == lt / 64) tot = readlane_f(pre[q], lt % 64);
         uint64_t st[2] = {rng[0], rng[1]};
         const float u = __fmul_rn(rng_uniform_dev(st), tot);
-        float c = 0.0f;
-        int32_t picked = 0;
-        bool fin = false;
-#pragma unroll
-        for (int q = 0; q < SMP_Q; q++)
-            for (int32_t l = 0; l < 64 && !fin && q * 64 + l < cutoff; l++) {
-                c = __fadd_rn(c, readlane_f(sq[q], l));
-                if (u <= c) {
-                    picked = q * 64 + l;
-                    fin = true;
-                }
-            }
+        const int32_t c1 = cutoff;
+        const int32_t pj = first([&](int q) { return q * 64 + lane < c1 && u <= pre[q]; });
+        const int32_t picked = pj >= 0 ? pj : 0;
         if (lane == 0) {
             rng[0] = st[0];
             rng[1] = st[1];
@@ -1182,7 +1246,7 @@ size_t sample_scratch_bytes(int64_t n, int32_t k) {
            + (size_t)nblk * (size_t)k * 4              // per-block top-k lists
            + (size_t)nblk * 4 * 2                      // event counts, NaN flags
            + (size_t)((n + SMP_BLOCK - 1) / SMP_BLOCK) * sizeof(ArgPart) + 256    // greedy partials
-           + (size_t)SMP_KMAX * 8 + 16;                // resolved slots, their flag, the masked values
+           + 16;                                       // the masked values
 }
 
 hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k, float top_p, float min_p,
@@ -1206,10 +1270,7 @@ hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k,
     p += (size_t)nblk * 4;
     ArgPart *part = reinterpret_cast<ArgPart *>((reinterpret_cast<uintptr_t>(p) + 15) & ~(uintptr_t)15);
     uint8_t *pr = reinterpret_cast<uint8_t *>(part + (n + SMP_BLOCK - 1) / SMP_BLOCK);
-    float *res_val = reinterpret_cast<float *>(pr);
-    int32_t *res_idx = reinterpret_cast<int32_t *>(pr + (size_t)SMP_KMAX * 4);
-    int32_t *res_ok = reinterpret_cast<int32_t *>(pr + (size_t)SMP_KMAX * 8);
-    float *saved = reinterpret_cast<float *>(pr + (size_t)SMP_KMAX * 8 + 8);
+    float *saved = reinterpret_cast<float *>(pr);
     const SmpMask mk{n_mask > 0 ? mask[0] : -1, n_mask > 1 ? mask[1] : -1, n_mask};
 
     const int32_t start = (window > 0 && window < hist_n) ? hist_n - window : 0;
@@ -1238,11 +1299,9 @@ hipError_t launch_sample(float *logits, int64_t n, float temperature, int32_t k,
                          : (sb == 1024 ? k_smp_events<1, 4> : sb == 2048 ? k_smp_events<2, 4> : k_smp_events<4, 4>);
     hipLaunchKernelGGL(blocks, dim3(nblk), dim3(SMP_WG), 0, s, logits, n, k, tops, nan_flag, pp);
     hipLaunchKernelGGL(events, dim3(nblk), dim3(SMP_WG), 0, s, logits, n, k, tops, ev_idx, ev_val, ev_n);
-    hipLaunchKernelGGL(k_smp_slots, dim3(1), dim3(1024), 0, s, logits, n, k, sb, nblk, ev_idx, ev_val, ev_n,
-                       nan_flag, res_val, res_idx, res_ok);
-    SmpArgs a{temperature, top_p, min_p, k, sb, nblk};
-    hipLaunchKernelGGL(k_smp_finish, dim3(1), dim3(SMP_FIN), 0, s, logits, n, a, ev_idx, ev_val, ev_n, nan_flag, res_val,
-                       res_idx, res_ok, rng, token, mk, saved);
+    SmpArgs sa{temperature, top_p, min_p, k, sb, nblk};
+    hipLaunchKernelGGL(k_smp_pick, dim3(1), dim3(SMP_WG), 0, s, logits, n, sa, ev_idx, ev_val, ev_n, nan_flag, rng,
+                       token, mk, saved);
     return hipGetLastError();
 }
 
