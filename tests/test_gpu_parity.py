@@ -327,6 +327,15 @@ def test_lmhead_argmax_nan_rules(lib, orc, case):
         finite = np.where(np.isnan(want), -np.inf, want)
         order = np.lexsort((np.arange(n), -finite))[:topk]
         assert set(host(ti).tolist()) == set(order.tolist())
+        # topk_collect (slm/sampler.c:70-93) instead keeps a NaN of the
+        # first k rows in its fill slot (a NaN never compares as the worst
+        # slot) while the other slots end with the largest numbers: the two
+        # sets differ exactly by those NaN rows. hip_sample, which needs the
+        # slot order, follows topk_collect (tests/test_gpu_sampler.py).
+        ci, _ = orc.topk_collect(want, topk)
+        nan_fill = {r for r in range(topk) if np.isnan(want[r])}
+        assert nan_fill == {5}
+        assert set(ci.tolist()) == nan_fill | set(order[:topk - len(nan_fill)].tolist())
 
 
 def test_lmhead_two_streams_concurrently(lib, orc):
