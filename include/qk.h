@@ -331,11 +331,14 @@ typedef struct {
  * softmax over its slots, the stable descending sort, top-p, min-p and
  * the roulette pick with one draw from the reference's rng, whose two
  * words (struct rng, slm/model.c:414) live in device memory at rng and
- * advance exactly as rng_next does. *token (device) receives the id; the
- * pick, the penalized logits and the rng state are bit for bit the
- * reference's, NaN logits included. token may point into history (at
- * entry hist_n) to append the pick. Scratch is per stream, as for the LM
- * head. n is at most QK_SAMPLE_MAX_N. */
+ * advance exactly as rng_next does. *token (device) receives the id.
+ * After the pick the masked ids get back the values they had before
+ * masking, as slm_generate_raw restores eos / eot after sample_with
+ * (slm/slm.c:324-333; an id masked twice keeps the -inf the first mask
+ * left); the other logits stay penalized. The pick, the logits and the
+ * rng state are bit for bit the reference's, NaN logits included. token
+ * may point into history (at entry hist_n) to append the pick. Scratch is
+ * per stream, as for the LM head. n is at most QK_SAMPLE_MAX_N. */
 #define QK_SAMPLE_MAX_MASK 2
 #define QK_SAMPLE_MAX_N 262144
 int hip_sample(float *logits, int64_t n, const qk_sampler *sp, uint64_t *rng,
