@@ -862,10 +862,10 @@ __global__ __launch_bounds__(256) void k_gemm_r(const uint8_t *__restrict__ w, i
             load_w(i + 1);
         }
         lds_barrier();
-        v16i acc[NT][2];
-#pragma unroll
-        for (int j = 0; j < NT; j++) acc[j][0] = acc[j][1] = zero;
-        uint32_t mn[8];                                // 6-bit mins, as the mins operand
+        // this super-block's B operands: the two digit planes of every
+        // sub-block, and the mins operand
+        v4i pb[8][2];
+        uint32_t mn[8];                                // 6-bit mins
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const uint32_t M = 0x0F0F0F0Fu;
@@ -879,33 +879,38 @@ __global__ __launch_bounds__(256) void k_gemm_r(const uint8_t *__restrict__ w, i
                 scale_min(cw.hdr.y, cw.hdr.z, cw.hdr.w, sb, sc, mm);
                 mn[sb] = (uint32_t)mm;
                 const uint32_t lo = (uint32_t)sc & 7u, hi = (uint32_t)sc >> 3;
-                const v4i b0 = {(int)bmul(q[hs][0], lo), (int)bmul(q[hs][1], lo), (int)bmul(q[hs][2], lo),
+                pb[sb][0] = v4i{(int)bmul(q[hs][0], lo), (int)bmul(q[hs][1], lo), (int)bmul(q[hs][2], lo),
                                 (int)bmul(q[hs][3], lo)};
-                const v4i b1 = {(int)bmul(q[hs][0], hi), (int)bmul(q[hs][1], hi), (int)bmul(q[hs][2], hi),
+                pb[sb][1] = v4i{(int)bmul(q[hs][0], hi), (int)bmul(q[hs][1], hi), (int)bmul(q[hs][2], hi),
                                 (int)bmul(q[hs][3], hi)};
-#pragma unroll
-                for (int j = 0; j < NT; j++) {
-                    const v4i av = *(const QK_LDS v4i *)(&sa[32 * j + col][32 * sb + 16 * h]);
-                    acc[j][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b0, acc[j][0], 0, 0, 0);
-                    acc[j][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b1, acc[j][1], 0, 0, 0);
-                }
             }
         }
         const long mnv = (long)((uint64_t)mn[0] | (uint64_t)mn[1] << 8 | (uint64_t)mn[2] << 16 |
                                 (uint64_t)mn[3] << 24 | (uint64_t)mn[4] << 32 | (uint64_t)mn[5] << 40 |
                                 (uint64_t)mn[6] << 48 | (uint64_t)mn[7] << 56);
         const float wd = h2f(cw.hdr.x & 0xffffu), wdm = h2f(cw.hdr.x >> 16);
+        // token tile j's products, then its fp32 terms; the products of
+        // tile j + 1 come first in the order, beside tile j's terms
+        v16i a0[NT], a1[NT], dl[NT], dh[NT];
+        auto products = [&](int j) {
+            a0[j] = a1[j] = zero;
 #pragma unroll
-        for (int j = 0; j < NT; j++) {
-            // isum_mins as two small MFMAs (bsum pair digits lo | hi against
-            // the mins: mins = lo_product + 128 * hi_product exactly)
+            for (int sb = 0; sb < 8; sb++) {
+                const v4i av = *(const QK_LDS v4i *)(&sa[32 * j + col][32 * sb + 16 * h]);
+                a0[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, pb[sb][0], a0[j], 0, 0, 0);
+                a1[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, pb[sb][1], a1[j], 0, 0, 0);
+            }
+            // isum_mins as two small MFMAs (bsum pair digits lo | hi
+            // against the mins: mins = lo_product + 128 * hi_product)
             const long amv = *(const QK_LDS long *)&sam[32 * j + col][8 * h];
-            const v16i dl = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 0 ? mnv : 0L, zero, 0, 0, 0);
-            const v16i dh = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 1 ? mnv : 0L, zero, 0, 0, 0);
+            dl[j] = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 0 ? mnv : 0L, zero, 0, 0, 0);
+            dh[j] = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 1 ? mnv : 0L, zero, 0, 0, 0);
+        };
+        auto terms = [&](int j) {
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const int32_t is = acc[j][0][v] + 8 * acc[j][1][v];
-                const int32_t mins = dl[v] + dh[v] * 128;
+                const int32_t is = a0[j][v] + 8 * a1[j][v];
+                const int32_t mins = dl[j][v] + dh[j][v] * 128;
                 const float yd = syd[32 * j + tok_of(v, h)];
                 const float d = __fmul_rn(yd, wd);
                 const float dmin = __fmul_rn(yd, wdm);
@@ -914,7 +919,14 @@ __global__ __launch_bounds__(256) void k_gemm_r(const uint8_t *__restrict__ w, i
                     FUSED ? __builtin_fmaf(d, (float)is, -pm) : __fsub_rn(__fmul_rn(d, (float)is), pm);
                 sum[j][v] = __fadd_rn(sum[j][v], term);
             }
+        };
+        products(0);
+#pragma unroll
+        for (int j = 1; j < NT; j++) {
+            products(j);
+            terms(j - 1);
         }
+        terms(NT - 1);
     }
     if (row < n) {
 #pragma unroll
