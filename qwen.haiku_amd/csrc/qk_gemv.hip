@@ -1006,9 +1006,9 @@ __global__ __launch_bounds__(256, LM ? 4 : 5) void k_gemv(uint32_t t0, uint32_t 
             amax_partial[blockIdx.x] = m;
         }
     }
-    // Top-k candidate counter for the LM head's filter kernel, which runs
-    // after this one on the same stream.
-    if (zero_ctr && blockIdx.x == 0 && threadIdx.x == 0) *zero_ctr = 0;
+    // Top-k candidate and finished-block counters for the LM head's filter
+    // kernel, which runs after this one on the same stream.
+    if (zero_ctr && blockIdx.x == 0 && threadIdx.x < 2) zero_ctr[threadIdx.x] = 0;
 }
 
 void gemv_plan(GemvDesc &d) {
@@ -1115,10 +1115,10 @@ hipError_t launch_gemv(GemvArgs &a, int max_grid, hipStream_t s) {
 // groups of G workgroups. k_topk_filter takes as its bound T the k-th
 // largest group maximum, searched on the top 16 bits of the value key
 // (low bits zero, so T stays a lower bound), and collects every logit
-// whose value key is >= T: all of the top k are among them. k_topk_final
-// ranks the candidates. If more than TOPK_CAND logits pass (a
-// pathological flat distribution), k_topk_final falls back to k exact
-// passes over all logits.
+// whose value key is >= T: all of the top k are among them. The last
+// filter block to finish ranks the candidates (topk_rank). If more than
+// TOPK_CAND logits pass (a pathological flat distribution), it falls back
+// to k exact passes over all logits.
 #define TOPK_CAND 4096
 // Workgroups of the LM-head GEMV (grid-stride over tiles), one maximum
 // each: two per CU. Measured with argmax on 248320 x 1024: 1024 (four per
@@ -1229,6 +1229,9 @@ __device__ K block_kth_largest(const K (&key)[R], const bool (&have)[R], int k, 
     return prefix;
 }
 
+__device__ void topk_rank(const float *__restrict__ logits, int64_t n, const uint64_t *__restrict__ cand,
+                          uint32_t c, int topk, int32_t *__restrict__ topk_idx, float *__restrict__ topk_val);
+
 // Grid: ceil(n / 4096) blocks of 1024 when topk > 0, else one block.
 // Block 0 writes the argmax. With topk > 0 every block finds the same
 // bound T from the nparts (<= LMHEAD_WG) workgroup maxima, then collects
@@ -1236,7 +1239,9 @@ __device__ K block_kth_largest(const K (&key)[R], const bool (&have)[R], int k, 
 __global__ __launch_bounds__(1024) void k_topk_filter(const float *__restrict__ logits, int64_t n,
                                                       const uint64_t *__restrict__ partial, int nparts,
                                                       int topk, uint64_t *__restrict__ cand,
-                                                      uint32_t *__restrict__ ctr, int32_t *__restrict__ argmax) {
+                                                      uint32_t *__restrict__ ctr, int32_t *__restrict__ argmax,
+                                                      int32_t *__restrict__ topk_idx,
+                                                      float *__restrict__ topk_val) {
     __shared__ uint32_t gkey[1024];                    // group maxima (value keys)
     __shared__ uint64_t red[16];
     __shared__ uint32_t tsh;
@@ -1299,25 +1304,41 @@ __global__ __launch_bounds__(1024) void k_topk_filter(const float *__restrict__ 
         const int64_t i = base + t + 1024 * r;
         if (i < n && valkey(v[r]) >= T) {
             const uint32_t slot = atomicAdd(ctr, 1u);
-            if (slot < TOPK_CAND) cand[slot] = ((uint64_t)valkey(v[r]) << 32) | (0xffffffffu - (uint32_t)i);
+            if (slot < TOPK_CAND)
+                __hip_atomic_exchange(&cand[slot], ((uint64_t)valkey(v[r]) << 32) | (0xffffffffu - (uint32_t)i),
+                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+    // The last block to finish ranks the candidates: every thread's
+    // atomics have completed (waitcnt) before the block counts itself done.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t == 0) {
+        const uint32_t done = __hip_atomic_fetch_add(&ctr[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        tsh = done == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!tsh) return;                                  // uniform
+    const uint32_t c = __hip_atomic_load(&ctr[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    topk_rank(logits, n, cand, c, topk, topk_idx, topk_val);
 }
 
-// One block of 1024: the exact top-k of the filtered candidates, ranked
-// value-descending / row-ascending.
-__global__ __launch_bounds__(1024) void k_topk_final(const float *__restrict__ logits, int64_t n,
-                                                     const uint64_t *__restrict__ cand,
-                                                     const uint32_t *__restrict__ ctr, int topk,
-                                                     int32_t *__restrict__ topk_idx,
-                                                     float *__restrict__ topk_val) {
+// The exact top-k of the filtered candidates, ranked value-descending /
+// row-ascending, by the filter's last block (all 1024 threads). The
+// candidates and their count were written by atomics at agent scope, which
+// bypass the per-XCD L2, so plain agent-scope atomic loads see them.
+__device__ __forceinline__ uint64_t agent_load(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ void topk_rank(const float *__restrict__ logits, int64_t n, const uint64_t *__restrict__ cand,
+                          uint32_t c, int topk, int32_t *__restrict__ topk_idx, float *__restrict__ topk_val) {
     __shared__ uint32_t hist[258];
     __shared__ uint64_t win[1024];                     // candidates (ranking) or winners
     __shared__ uint64_t red[16];
     __shared__ uint32_t nwin;
     const int t = threadIdx.x;
-    const uint32_t c = *ctr;
-    const uint64_t mine = cand[t];                     // t < 1024 <= TOPK_CAND; used when t < c
+    const uint64_t mine = agent_load(&cand[t]);        // t < 1024 <= TOPK_CAND; used when t < c
     if (t == 0) nwin = 0;
     int nw;                                            // keys in win[] to rank
     if (c <= 1024) {
@@ -1331,7 +1352,7 @@ __global__ __launch_bounds__(1024) void k_topk_final(const float *__restrict__ l
         for (int r = 0; r < 4; r++) {
             const uint32_t i = t + 1024 * r;
             have[r] = i < c;
-            key[r] = r == 0 ? mine : have[r] ? cand[i] : 0;
+            key[r] = r == 0 ? mine : have[r] ? agent_load(&cand[i]) : 0;
         }
         const uint64_t T = block_kth_largest<4, 64, uint64_t>(key, have, topk, hist);
 #pragma unroll
@@ -1414,12 +1435,7 @@ hipError_t launch_lmhead(const uint8_t *w, int64_t n, int64_t k, const uint8_t *
     if (grid > LMHEAD_WG) return hipErrorInvalidValue;
     const unsigned fgrid = topk > 0 ? (unsigned)cdiv(n, 4096) : 1u;
     hipLaunchKernelGGL(k_topk_filter, dim3(fgrid), dim3(1024), 0, s, logits, n, partial, grid, topk, cand, ctr,
-                       argmax);
-    if (topk > 0) {
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        hipLaunchKernelGGL(k_topk_final, dim3(1), dim3(1024), 0, s, logits, n, cand, ctr, topk, topk_idx,
-                           topk_val);
-    }
+                       argmax, topk_idx, topk_val);
     return hipGetLastError();
 }
 
