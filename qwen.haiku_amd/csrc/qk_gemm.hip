@@ -939,6 +939,143 @@ __global__ __launch_bounds__(256) void k_gemm_r(const uint8_t *__restrict__ w, i
     }
 }
 
+// ---- super-blocks across waves (Q4_K, short prompts) ---------------------------
+// A 256-thread workgroup owns one 32-token x 32-row output tile; in round
+// r its wave w computes super-block 4r + w, so the waves of a workgroup run
+// the super-blocks of a tile side by side instead of one after another.
+// The super-block terms are formed exactly as in k_gemm_r (lane l: row
+// l % 32, k-half l / 32) and then summed in super-block order: every wave
+// writes its 16 terms per lane to LDS, and wave w adds, for outputs
+// 4w..4w+3 of every lane, the round's terms in order to the running sums
+// (sum starts at +0.0, so the first term enters exactly), which is the
+// reference's sequential `sum += term`.
+template <bool FUSED>
+__global__ __launch_bounds__(256) void k_gemm_ks(const uint8_t *__restrict__ w, int64_t n, int nb,
+                                                 const uint8_t *__restrict__ xq, int64_t m, float *__restrict__ y) {
+    // super-block 4r + q in sa[q]: a token's 256 quants, then in the row's
+    // last 16 bytes its bsum pairs as two int8 digits
+    __shared__ __attribute__((aligned(16))) int8_t sa[4][32][GM_LD];
+    __shared__ __attribute__((aligned(16))) float st[4][16][64];       // the waves' terms, [wave][v][lane]
+    __shared__ float syd[4][32];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, h = lane >> 5;
+    const int64_t r0 = (int64_t)blockIdx.x * 32, t0 = (int64_t)blockIdx.y * 32;
+    const int mrows = (m - t0 < 32) ? (int)(m - t0) : 32;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(xq + t0 * nb * Q8K_BYTES), 0, mrows * nb * Q8K_BYTES, 0x00020000);
+    // staging: thread t stages eighth e = t % 8 of token t / 8 for each of
+    // the round's four super-blocks (super-block 4r + q in sa[q])
+    const int at = tid >> 3, ae = tid & 7;
+    const int64_t row = r0 + col;
+    const uint8_t *wp = w + (row < n ? row : n - 1) * nb * Q4K_BYTES;
+    const v16i zero = {0};
+    float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};          // this lane's outputs v = 4 * wave + b
+    for (int r = 0; r < nb; r += 4) {
+        const int sb = r + wave;                       // this wave's super-block
+        const bool act = sb < nb;                      // wave-uniform
+        // weights of this wave's super-block, in flight during staging
+        struct W5 { uint4 hdr, p[4]; } cw;
+        {
+            const uint8_t *p = wp + (int64_t)(act ? sb : nb - 1) * Q4K_BYTES;
+            cw.hdr = ld16(p);
+#pragma unroll
+            for (int c = 0; c < 4; c++) cw.p[c] = ld16(p + 16 + 32 * c + 16 * h);
+        }
+        // the round's activations, in flight during the unpack
+        struct A8 { uint4 q0, q1; uint32_t bp, d; } ar[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int o = at * nb * Q8K_BYTES + (r + q < nb ? r + q : nb - 1) * Q8K_BYTES;
+            ar[q].q0 = bl128(xr, o + 4 + 32 * ae);
+            ar[q].q1 = bl128(xr, o + 20 + 32 * ae);
+            ar[q].bp = bl32(xr, o + 260 + 4 * ae);
+            ar[q].d = bl32(xr, o);
+        }
+        // previous round's reads done, then this round's activations
+        auto stage = [&]() {
+            if (r > 0) lds_barrier();
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                if (r + q >= nb) break;                // uniform
+                *(QK_LDS uint4 *)&sa[q][at][32 * ae] = ar[q].q0;
+                *(QK_LDS uint4 *)&sa[q][at][32 * ae + 16] = ar[q].q1;
+                const int32_t pr = (int32_t)(int16_t)(ar[q].bp & 0xffffu) + (int32_t)(int16_t)(ar[q].bp >> 16);
+                sa[q][at][256 + ae] = (int8_t)(pr & 127);
+                sa[q][at][264 + ae] = (int8_t)(pr >> 7);
+                if (ae == 0) syd[q][at] = __uint_as_float(ar[q].d);
+            }
+            lds_barrier();
+        };
+        if (!act) stage();                             // wave-uniform: the barriers match the active waves'
+        if (act) {
+            v4i pb[8][2];
+            uint32_t mn[8];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint32_t M = 0x0F0F0F0Fu;
+                const uint4 v = cw.p[c];
+                const uint32_t q[2][4] = {{v.x & M, v.y & M, v.z & M, v.w & M},
+                                          {(v.x >> 4) & M, (v.y >> 4) & M, (v.z >> 4) & M, (v.w >> 4) & M}};
+#pragma unroll
+                for (int hs = 0; hs < 2; hs++) {
+                    const int s2 = 2 * c + hs;
+                    int32_t sc, mm;
+                    scale_min(cw.hdr.y, cw.hdr.z, cw.hdr.w, s2, sc, mm);
+                    mn[s2] = (uint32_t)mm;
+                    const uint32_t lo = (uint32_t)sc & 7u, hi = (uint32_t)sc >> 3;
+                    pb[s2][0] = v4i{(int)bmul(q[hs][0], lo), (int)bmul(q[hs][1], lo), (int)bmul(q[hs][2], lo),
+                                    (int)bmul(q[hs][3], lo)};
+                    pb[s2][1] = v4i{(int)bmul(q[hs][0], hi), (int)bmul(q[hs][1], hi), (int)bmul(q[hs][2], hi),
+                                    (int)bmul(q[hs][3], hi)};
+                }
+            }
+            const long mnv = (long)((uint64_t)mn[0] | (uint64_t)mn[1] << 8 | (uint64_t)mn[2] << 16 |
+                                    (uint64_t)mn[3] << 24 | (uint64_t)mn[4] << 32 | (uint64_t)mn[5] << 40 |
+                                    (uint64_t)mn[6] << 48 | (uint64_t)mn[7] << 56);
+            const float wd = h2f(cw.hdr.x & 0xffffu), wdm = h2f(cw.hdr.x >> 16);
+            stage();
+            v16i a0 = zero, a1 = zero;
+#pragma unroll
+            for (int s2 = 0; s2 < 8; s2++) {
+                const v4i av = *(const QK_LDS v4i *)(&sa[wave][col][32 * s2 + 16 * h]);
+                a0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, pb[s2][0], a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, pb[s2][1], a1, 0, 0, 0);
+            }
+            // isum_mins as two small MFMAs (bsum pair digits lo | hi
+            // against the mins: mins = lo_product + 128 * hi_product)
+            const long amv = *(const QK_LDS long *)&sa[wave][col][256 + 8 * h];
+            const v16i dl = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 0 ? mnv : 0L, zero, 0, 0, 0);
+            const v16i dh = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 1 ? mnv : 0L, zero, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int32_t is = a0[v] + 8 * a1[v];
+                const int32_t mins = dl[v] + dh[v] * 128;
+                const float yd = syd[wave][tok_of(v, h)];
+                const float d = __fmul_rn(yd, wd);
+                const float dmin = __fmul_rn(yd, wdm);
+                const float pm = __fmul_rn(dmin, (float)mins);
+                st[wave][v][lane] = FUSED ? __builtin_fmaf(d, (float)is, -pm) : __fsub_rn(__fmul_rn(d, (float)is), pm);
+            }
+        }
+        lds_barrier();
+        // the round's terms in super-block order, outputs 4 * wave .. + 3
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            if (r + q >= nb) break;                    // uniform
+#pragma unroll
+            for (int b = 0; b < 4; b++) sum[b] = __fadd_rn(sum[b], st[q][4 * wave + b][lane]);
+        }
+    }
+    if (row < n) {
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int v = 4 * wave + b;
+            const int64_t t = t0 + tok_of(v, h);
+            if (t < m) __builtin_nontemporal_store(FUSED ? bcast8(sum[b]) : sum[b], &y[t * n + row]);
+        }
+    }
+}
+
 // ---- Q8_0 x Q8_0 --------------------------------------------------------------
 // The token loop of tensor_matmul_q8_0_f32 (slm/tensor.c:952-981) over
 // q8_0_dot_q8_0 (simd/avx.c:65-158, simd/quants.h:244-256). Per 32-element
@@ -1156,6 +1293,16 @@ hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, const u
         // tiles below 1024 tokens, 64-token tiles from there (N = 3584,
         // K = 1024: M = 512 10.7 against 11.0 us, 1024 15.3 against 16.0,
         // 2048 27.9 against 30.0)
+        // Q4_K up to 512 tokens: the super-blocks of a 32 x 32 tile across
+        // the waves of one workgroup (k_gemm_ks). N = 3584, K = 1024: M = 64
+        // 4.2 against 7.5 us, 128 5.2 / 7.4, 256 6.8 / 9.7, 384 8.7 / 11.4,
+        // 512 10.1 / 10.4 (k_gemm_r); 768 14.2 / 13.8.
+        if (type == 12 && m <= 512) {
+            const dim3 grid((unsigned)((n + 31) / 32), (unsigned)((m + 31) / 32));
+            if (fused) hipLaunchKernelGGL((k_gemm_ks<true>), grid, dim3(256), 0, s, w, n, nb, xq, m, y);
+            else hipLaunchKernelGGL((k_gemm_ks<false>), grid, dim3(256), 0, s, w, n, nb, xq, m, y);
+            return hipGetLastError();
+        }
         if (tiles >= 192 && type == 12) {
             if (m < 1024) {
                 const dim3 grid((unsigned)((n + 127) / 128), (unsigned)((m + 31) / 32));
