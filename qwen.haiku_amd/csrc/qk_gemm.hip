@@ -51,6 +51,8 @@ namespace qk {
 
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
 typedef int32_t v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 #define GM_BM 64                      // tokens per workgroup tile
 #define GM_LD 272                     // LDS row stride of the int8 tiles (256 + 16)
@@ -1076,6 +1078,172 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const uint8_t *__restrict__ w, 
     }
 }
 
+// ---- super-blocks across waves (Q6_K) -------------------------------------------
+// k_gemm_ks for Q6_K (q6k_row_dot_q8k, simd/quants.h:355-402): a 256-thread
+// workgroup owns one 32-token x 32-row tile, wave w computes super-block
+// 4r + w in round r, and the waves' fp32 terms are added in super-block
+// order through LDS. Per super-block, the reference's integer sums:
+//
+//  * isum = sum_j scale_j * sum_{e in sub-block j} w_e * y_e over the
+//    unsigned 6-bit weights w: one v_mfma_i32_32x32x16_i8 per 16-element
+//    sub-block (lane half h takes elements 8h..8h+7 of it, in both
+//    operands), times the row's int8 scale, added in int32 (exact);
+//  * isum_mins = sum_j bsums_j * scale_j: one v_mfma_f32_32x32x16_f16,
+//    every operand exact in f16 (|bsums_j| <= 16 * 128 = 2048, the
+//    magnitude any Q8_K block's sixteen quants give) and every partial sum
+//    an integer below 2^24, so exact in f32;
+//
+// then term = rn(rn(fp16(d) * y.d) * (float)(isum - 32 * isum_mins)).
+// Element 16jj + l (l < 16) of a 128-element half hb is the low (jj < 4)
+// or high nibble of ql[64hb + 16(jj % 4) + l] with bits 2(jj / 2).. of
+// qh[32hb + 16(jj % 2) + l] on top, so lane half h reads 8-byte runs at
+// 64hb + 16c + 8h (c < 4) and 128 + 32hb + 16c + 8h (c < 2): twelve runs,
+// each through the three aligned dwords that contain it (blocks are
+// 2-byte aligned).
+template <bool FUSED>
+__global__ __launch_bounds__(256) void k_gemm_ks6(const uint8_t *__restrict__ w, int64_t n, int nb,
+                                                  const uint8_t *__restrict__ xq, int64_t m, float *__restrict__ y) {
+    __shared__ __attribute__((aligned(16))) int8_t sa[4][32][GM_LD];   // super-block 4r + q in sa[q]
+    __shared__ __attribute__((aligned(16))) _Float16 sbs[4][32][16];   // its bsums in f16
+    __shared__ float syd[4][32];
+    __shared__ __attribute__((aligned(16))) float st[4][16][64];       // the waves' terms, [wave][v][lane]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, h = lane >> 5;
+    const int64_t r0 = (int64_t)blockIdx.x * 32, t0 = (int64_t)blockIdx.y * 32;
+    const int mrows = (m - t0 < 32) ? (int)(m - t0) : 32;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(xq + t0 * nb * Q8K_BYTES), 0, mrows * nb * Q8K_BYTES, 0x00020000);
+    // the tile's weight rows as one buffer from the 4-byte aligned address
+    // at or below its first row; rows past n read zeros
+    const int nrows = (n - r0 < 32) ? (int)(n - r0) : 32;
+    const uint8_t *wt = w + r0 * nb * Q6K_BYTES;
+    const int off0 = (int)(reinterpret_cast<uintptr_t>(wt) & 3u);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(wt - off0), 0, off0 + nrows * nb * Q6K_BYTES, 0x00020000);
+    const int at = tid >> 3, ae = tid & 7;             // staging: eighth ae of token at
+    const int row = (int)(r0 + col);
+    float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};          // this lane's outputs v = 4 * wave + b
+    const v16i zero = {0};
+    for (int r = 0; r < nb; r += 4) {
+        const int sb = r + wave;
+        const bool act = sb < nb;                      // wave-uniform
+        // this wave's super-block: twelve 8-byte runs, the scales and d
+        const int b = off0 + (col * nb + (act ? sb : nb - 1)) * Q6K_BYTES;
+        const int sh = b & 3, ba = b - sh;
+        uint32_t raw[12][3], rs[5], rd;
+#pragma unroll
+        for (int hb = 0; hb < 2; hb++) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const auto v = __builtin_amdgcn_raw_buffer_load_b96(wr, ba + 64 * hb + 16 * c + 8 * h, 0, 0);
+                raw[6 * hb + c][0] = v[0], raw[6 * hb + c][1] = v[1], raw[6 * hb + c][2] = v[2];
+            }
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const auto v = __builtin_amdgcn_raw_buffer_load_b96(wr, ba + 128 + 32 * hb + 16 * c + 8 * h, 0, 0);
+                raw[6 * hb + 4 + c][0] = v[0], raw[6 * hb + 4 + c][1] = v[1], raw[6 * hb + 4 + c][2] = v[2];
+            }
+        }
+        {
+            const uint4 v = bl128(wr, ba + 192);
+            rs[0] = v.x, rs[1] = v.y, rs[2] = v.z, rs[3] = v.w;
+            rs[4] = bl32(wr, ba + 208);                // used only when sh > 0, then inside the block
+            rd = __builtin_amdgcn_raw_buffer_load_b16(wr, b + 208, 0, 0);
+        }
+        // the round's activations, in flight during the unpack
+        struct A8 { uint4 q0, q1; uint32_t bp, d; } ar[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int o = at * nb * Q8K_BYTES + (r + q < nb ? r + q : nb - 1) * Q8K_BYTES;
+            ar[q].q0 = bl128(xr, o + 4 + 32 * ae);
+            ar[q].q1 = bl128(xr, o + 20 + 32 * ae);
+            ar[q].bp = bl32(xr, o + 260 + 4 * ae);
+            ar[q].d = bl32(xr, o);
+        }
+        auto stage = [&]() {
+            if (r > 0) lds_barrier();                  // the previous round's reads of sa / st done
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                if (r + q >= nb) break;                // uniform
+                *(QK_LDS uint4 *)&sa[q][at][32 * ae] = ar[q].q0;
+                *(QK_LDS uint4 *)&sa[q][at][32 * ae + 16] = ar[q].q1;
+                sbs[q][at][2 * ae] = (_Float16)(int16_t)(ar[q].bp & 0xffffu);
+                sbs[q][at][2 * ae + 1] = (_Float16)(int16_t)(ar[q].bp >> 16);
+                if (ae == 0) syd[q][at] = __uint_as_float(ar[q].d);
+            }
+            lds_barrier();
+        };
+        if (!act) stage();                             // wave-uniform: the barriers match the active waves'
+        if (act) {
+            // runs realigned, then the sixteen B operands (unsigned 6-bit)
+            uint32_t run[12][2];
+#pragma unroll
+            for (int k = 0; k < 12; k++) {
+                run[k][0] = __builtin_amdgcn_alignbyte(raw[k][1], raw[k][0], sh);
+                run[k][1] = __builtin_amdgcn_alignbyte(raw[k][2], raw[k][1], sh);
+            }
+            long bq[16];
+#pragma unroll
+            for (int hb = 0; hb < 2; hb++)
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++) {
+                    uint32_t qd[2];
+#pragma unroll
+                    for (int k = 0; k < 2; k++) {
+                        const uint32_t lo = (run[6 * hb + (jj & 3)][k] >> (4 * (jj >> 2))) & 0x0F0F0F0Fu;
+                        const uint32_t hi = ((run[6 * hb + 4 + (jj & 1)][k] >> (2 * (jj >> 1))) & 0x03030303u) << 4;
+                        qd[k] = lo | hi;
+                    }
+                    bq[8 * hb + jj] = (long)((uint64_t)qd[0] | ((uint64_t)qd[1] << 32));
+                }
+            uint32_t scw[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) scw[k] = __builtin_amdgcn_alignbyte(rs[k + 1], rs[k], sh);
+            const float wd = h2f(rd);
+            // mins operand: scales 8h..8h+7 in f16
+            v8h mb;
+#pragma unroll
+            for (int k = 0; k < 8; k++) mb[k] = (_Float16)(int8_t)(scw[2 * h + (k >> 2)] >> (8 * (k & 3)));
+            stage();
+            int32_t isum[16];
+#pragma unroll
+            for (int v = 0; v < 16; v++) isum[v] = 0;
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const long av = *(const QK_LDS long *)&sa[wave][col][16 * j + 8 * h];
+                const v16i d = __builtin_amdgcn_mfma_i32_32x32x16_i8(av, bq[j], zero, 0, 0, 0);
+                const int32_t scv = (int32_t)(int8_t)(scw[j >> 2] >> (8 * (j & 3)));
+#pragma unroll
+                for (int v = 0; v < 16; v++) isum[v] += __mul24(scv, d[v]);
+            }
+            const v8h amv = *(const QK_LDS v8h *)&sbs[wave][col][8 * h];
+            const v16f mf = __builtin_amdgcn_mfma_f32_32x32x16_f16(amv, mb, v16f{0.0f}, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int32_t is = isum[v] - 32 * (int32_t)mf[v];
+                const float yd = syd[wave][tok_of(v, h)];
+                st[wave][v][lane] = __fmul_rn(__fmul_rn(wd, yd), (float)is);
+            }
+        }
+        lds_barrier();
+        // the round's terms in super-block order, outputs 4 * wave .. + 3
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            if (r + q >= nb) break;                    // uniform
+#pragma unroll
+            for (int bb = 0; bb < 4; bb++) sum[bb] = __fadd_rn(sum[bb], st[q][4 * wave + bb][lane]);
+        }
+    }
+    if (row < n) {
+#pragma unroll
+        for (int bb = 0; bb < 4; bb++) {
+            const int v = 4 * wave + bb;
+            const int64_t t = t0 + tok_of(v, h);
+            if (t < m) __builtin_nontemporal_store(FUSED ? bcast8(sum[bb]) : sum[bb], &y[t * n + row]);
+        }
+    }
+}
+
 // ---- Q8_0 x Q8_0 --------------------------------------------------------------
 // The token loop of tensor_matmul_q8_0_f32 (slm/tensor.c:952-981) over
 // q8_0_dot_q8_0 (simd/avx.c:65-158, simd/quants.h:244-256). Per 32-element
@@ -1321,6 +1489,15 @@ hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, const u
             else hipLaunchKernelGGL((k_gemm_w<13, false>), grid, dim3(512), 0, s, w, n, nb, xq, m, y);
             return hipGetLastError();
         }
+    }
+    // Q6_K up to 512 tokens: super-blocks across waves (k_gemm_ks6). N =
+    // 1024, K = 3584: M = 128 16.7 against 22.3 us, 256 16.6 / 22.3, 512
+    // 18.5 / 22.4; 1024 37.3 / 33.0.
+    if (type == 14 && m <= 512) {
+        const dim3 grid((unsigned)((n + 31) / 32), (unsigned)((m + 31) / 32));
+        if (fused) hipLaunchKernelGGL((k_gemm_ks6<true>), grid, dim3(256), 0, s, w, n, nb, xq, m, y);
+        else hipLaunchKernelGGL((k_gemm_ks6<false>), grid, dim3(256), 0, s, w, n, nb, xq, m, y);
+        return hipGetLastError();
     }
     const unsigned mt = (unsigned)((m + GM_BM - 1) / GM_BM);
     // 64-row tiles when they alone give every CU a workgroup, else 32-row
