@@ -1100,13 +1100,22 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const uint8_t *__restrict__ w, 
 // 64hb + 16c + 8h (c < 4) and 128 + 32hb + 16c + 8h (c < 2): twelve runs,
 // each through the three aligned dwords that contain it (blocks are
 // 2-byte aligned).
-template <bool FUSED>
-__global__ __launch_bounds__(256) void k_gemm_ks6(const uint8_t *__restrict__ w, int64_t n, int nb,
+// S waves per workgroup, S super-blocks per round (4 or 8). With 8, the
+// waves' terms reuse the activations' LDS once every wave has read them
+// (one more barrier), so two workgroups fit a CU.
+template <int S> struct Ks6Tiles { int8_t sa[S][32][GM_LD]; float st[S][16][64]; };
+template <int S> union Ks6Shared { int8_t sa[S][32][GM_LD]; float st[S][16][64]; };
+
+template <bool FUSED, int S>
+__global__ __launch_bounds__(64 * S) void k_gemm_ks6(const uint8_t *__restrict__ w, int64_t n, int nb,
                                                   const uint8_t *__restrict__ xq, int64_t m, float *__restrict__ y) {
-    __shared__ __attribute__((aligned(16))) int8_t sa[4][32][GM_LD];   // super-block 4r + q in sa[q]
-    __shared__ __attribute__((aligned(16))) _Float16 sbs[4][32][16];   // its bsums in f16
-    __shared__ float syd[4][32];
-    __shared__ __attribute__((aligned(16))) float st[4][16][64];       // the waves' terms, [wave][v][lane]
+    // super-block Sr + q in sa[q]; the waves' terms in st[wave][v][lane]
+    constexpr bool ALIAS = S == 8;
+    __shared__ __attribute__((aligned(16))) std::conditional_t<ALIAS, Ks6Shared<S>, Ks6Tiles<S>> u;
+    auto &sa = u.sa;
+    auto &st = u.st;
+    __shared__ __attribute__((aligned(16))) _Float16 sbs[S][32][16];   // its bsums in f16
+    __shared__ float syd[S][32];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, h = lane >> 5;
     const int64_t r0 = (int64_t)blockIdx.x * 32, t0 = (int64_t)blockIdx.y * 32;
@@ -1120,11 +1129,15 @@ __global__ __launch_bounds__(256) void k_gemm_ks6(const uint8_t *__restrict__ w,
     const int off0 = (int)(reinterpret_cast<uintptr_t>(wt) & 3u);
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(wt - off0), 0, off0 + nrows * nb * Q6K_BYTES, 0x00020000);
-    const int at = tid >> 3, ae = tid & 7;             // staging: eighth ae of token at
+    // staging: eighth ae of token at, of super-blocks Sr + 4g .. + 3
+    const int at = (tid >> 3) & 31, ae = tid & 7, ag = tid >> 8;
     const int row = (int)(r0 + col);
-    float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};          // this lane's outputs v = 4 * wave + b
+    constexpr int VW = 16 / S;                         // outputs per lane each wave adds up
+    float sum[VW];
+#pragma unroll
+    for (int bb = 0; bb < VW; bb++) sum[bb] = 0.0f;
     const v16i zero = {0};
-    for (int r = 0; r < nb; r += 4) {
+    for (int r = 0; r < nb; r += S) {
         const int sb = r + wave;
         const bool act = sb < nb;                      // wave-uniform
         // this wave's super-block: twelve 8-byte runs, the scales and d
@@ -1154,26 +1167,31 @@ __global__ __launch_bounds__(256) void k_gemm_ks6(const uint8_t *__restrict__ w,
         struct A8 { uint4 q0, q1; uint32_t bp, d; } ar[4];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const int o = at * nb * Q8K_BYTES + (r + q < nb ? r + q : nb - 1) * Q8K_BYTES;
+            const int sq = r + 4 * ag + q;
+            const int o = at * nb * Q8K_BYTES + (sq < nb ? sq : nb - 1) * Q8K_BYTES;
             ar[q].q0 = bl128(xr, o + 4 + 32 * ae);
             ar[q].q1 = bl128(xr, o + 20 + 32 * ae);
             ar[q].bp = bl32(xr, o + 260 + 4 * ae);
             ar[q].d = bl32(xr, o);
         }
         auto stage = [&]() {
-            if (r > 0) lds_barrier();                  // the previous round's reads of sa / st done
+            if (r > 0) lds_barrier();                  // the previous round's reads of st done
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                if (r + q >= nb) break;                // uniform
-                *(QK_LDS uint4 *)&sa[q][at][32 * ae] = ar[q].q0;
-                *(QK_LDS uint4 *)&sa[q][at][32 * ae + 16] = ar[q].q1;
-                sbs[q][at][2 * ae] = (_Float16)(int16_t)(ar[q].bp & 0xffffu);
-                sbs[q][at][2 * ae + 1] = (_Float16)(int16_t)(ar[q].bp >> 16);
-                if (ae == 0) syd[q][at] = __uint_as_float(ar[q].d);
+                const int qq = 4 * ag + q;
+                if (r + qq >= nb) break;               // wave-uniform
+                *(QK_LDS uint4 *)&sa[qq][at][32 * ae] = ar[q].q0;
+                *(QK_LDS uint4 *)&sa[qq][at][32 * ae + 16] = ar[q].q1;
+                sbs[qq][at][2 * ae] = (_Float16)(int16_t)(ar[q].bp & 0xffffu);
+                sbs[qq][at][2 * ae + 1] = (_Float16)(int16_t)(ar[q].bp >> 16);
+                if (ae == 0) syd[qq][at] = __uint_as_float(ar[q].d);
             }
             lds_barrier();
         };
-        if (!act) stage();                             // wave-uniform: the barriers match the active waves'
+        if (!act) {                                    // wave-uniform: the barriers match the active waves'
+            stage();
+            if constexpr (ALIAS) lds_barrier();
+        }
         if (act) {
             // runs realigned, then the sixteen B operands (unsigned 6-bit)
             uint32_t run[12][2];
@@ -1218,6 +1236,7 @@ __global__ __launch_bounds__(256) void k_gemm_ks6(const uint8_t *__restrict__ w,
             }
             const v8h amv = *(const QK_LDS v8h *)&sbs[wave][col][8 * h];
             const v16f mf = __builtin_amdgcn_mfma_f32_32x32x16_f16(amv, mb, v16f{0.0f}, 0, 0, 0);
+            if constexpr (ALIAS) lds_barrier();        // every wave's reads of sa done: st reuses it
 #pragma unroll
             for (int v = 0; v < 16; v++) {
                 const int32_t is = isum[v] - 32 * (int32_t)mf[v];
@@ -1226,18 +1245,18 @@ __global__ __launch_bounds__(256) void k_gemm_ks6(const uint8_t *__restrict__ w,
             }
         }
         lds_barrier();
-        // the round's terms in super-block order, outputs 4 * wave .. + 3
+        // the round's terms in super-block order, outputs VW * wave ..
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
+        for (int q = 0; q < S; q++) {
             if (r + q >= nb) break;                    // uniform
 #pragma unroll
-            for (int bb = 0; bb < 4; bb++) sum[bb] = __fadd_rn(sum[bb], st[q][4 * wave + bb][lane]);
+            for (int bb = 0; bb < VW; bb++) sum[bb] = __fadd_rn(sum[bb], st[q][VW * wave + bb][lane]);
         }
     }
     if (row < n) {
 #pragma unroll
-        for (int bb = 0; bb < 4; bb++) {
-            const int v = 4 * wave + bb;
+        for (int bb = 0; bb < VW; bb++) {
+            const int v = VW * wave + bb;
             const int64_t t = t0 + tok_of(v, h);
             if (t < m) __builtin_nontemporal_store(FUSED ? bcast8(sum[bb]) : sum[bb], &y[t * n + row]);
         }
@@ -1491,12 +1510,17 @@ hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, const u
         }
     }
     // Q6_K up to 512 tokens: super-blocks across waves (k_gemm_ks6). N =
-    // 1024, K = 3584: M = 128 16.7 against 22.3 us, 256 16.6 / 22.3, 512
-    // 18.5 / 22.4; 1024 37.3 / 33.0.
+    // 1024, K = 3584: M = 128 13.9 against 22.3 us, 256 13.9 / 22.3, 512
+    // 18.4 / 22.4; 1024 37.3 / 33.0.
     if (type == 14 && m <= 512) {
         const dim3 grid((unsigned)((n + 31) / 32), (unsigned)((m + 31) / 32));
-        if (fused) hipLaunchKernelGGL((k_gemm_ks6<true>), grid, dim3(256), 0, s, w, n, nb, xq, m, y);
-        else hipLaunchKernelGGL((k_gemm_ks6<false>), grid, dim3(256), 0, s, w, n, nb, xq, m, y);
+        if (m <= 256) {                                // 8 super-blocks a round: 128 / 256 tokens 13.9 us
+            if (fused) hipLaunchKernelGGL((k_gemm_ks6<true, 8>), grid, dim3(512), 0, s, w, n, nb, xq, m, y);
+            else hipLaunchKernelGGL((k_gemm_ks6<false, 8>), grid, dim3(512), 0, s, w, n, nb, xq, m, y);
+        } else {                                       // 4: 512 tokens 18.4 us (21.1 with 8)
+            if (fused) hipLaunchKernelGGL((k_gemm_ks6<true, 4>), grid, dim3(256), 0, s, w, n, nb, xq, m, y);
+            else hipLaunchKernelGGL((k_gemm_ks6<false, 4>), grid, dim3(256), 0, s, w, n, nb, xq, m, y);
+        }
         return hipGetLastError();
     }
     const unsigned mt = (unsigned)((m + GM_BM - 1) / GM_BM);
