@@ -279,20 +279,39 @@ def bench_config2(torch, qk, synth, lib, steps, warmup):
     return per, copies, R, secs
 
 
-def bench_config3(torch, qk, synth, lib, steps, warmup, wtype=12, n=3584, k=1024, m=512):
+def bench_config3(torch, qk, synth, lib, steps, warmup, wtype=12, n=3584, k=1024, m=512, planes=False):
     """Chunked-prefill GEMM (int8 MFMA): xq resident, y fp32. Weight and
     output buffers rotate through > 512 MB so each launch reads its weights
-    from HBM and writes its outputs to fresh lines. Returns (copies, R,
-    seconds for the GEMM alone, seconds for quantize + GEMM from fp32 x)."""
-    per = n * qk.row_bytes(wtype, k) + 4 * m * n
+    from HBM and writes its outputs to fresh lines. planes: the GEMM over
+    the weights repacked once into int8 MFMA planes (hip_matmul_planes;
+    the repacking is not timed). Returns (copies, R, seconds for the GEMM
+    alone, seconds for quantize + GEMM from fp32 x)."""
+    wbytes = lib.planes_bytes(wtype, n, k) if planes else n * qk.row_bytes(wtype, k)
+    per = wbytes + 4 * m * n
     copies = max(2, -(-MALL_DEFEAT_BYTES // per))
     w = torch.from_numpy(synth.blocks(wtype, n, k, seed=0)).cuda()
-    ws = [w] + [w.clone() for _ in range(copies - 1)]
+    pack_us = None
+    if planes:
+        p0 = lib.pack_planes(wtype, w, n, k)
+        ws = [p0] + [p0.clone() for _ in range(copies - 1)]
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        lib.pack_planes(wtype, w, n, k, planes=ws[-1])  # the one-time repacking, timed once
+        e1.record()
+        torch.cuda.synchronize()
+        pack_us = e0.elapsed_time(e1) * 1e3
+    else:
+        ws = [w] + [w.clone() for _ in range(copies - 1)]
     ys = [torch.empty((m, n), dtype=torch.float32, device="cuda") for _ in range(copies)]
     x = torch.from_numpy(synth.activations(m, k, seed=0)).cuda()
     xq = lib.quantize_q8_0(x) if wtype == qk.Q8_0 else lib.quantize_q8k(x)
-    fn = {8: lib.L.hip_matmul_q8_0, 12: lib.L.hip_matmul_q4k, 13: lib.L.hip_matmul_q5k,
-          14: lib.L.hip_matmul_q6k}[wtype]
+    if planes:
+        def fn(wp_, n_, k_, xq_, m_, y_, sp_):
+            return lib.L.hip_matmul_planes(wtype, wp_, n_, k_, xq_, m_, y_, sp_)
+    else:
+        fn = {8: lib.L.hip_matmul_q8_0, 12: lib.L.hip_matmul_q4k, 13: lib.L.hip_matmul_q5k,
+              14: lib.L.hip_matmul_q6k}[wtype]
     wp = [C.c_void_p(t.data_ptr()) for t in ws]
     yp = [C.c_void_p(t.data_ptr()) for t in ys]
     xp, xqp = C.c_void_p(x.data_ptr()), C.c_void_p(xq.data_ptr())
@@ -310,7 +329,7 @@ def bench_config3(torch, qk, synth, lib, steps, warmup, wtype=12, n=3584, k=1024
         gemm(i, sp)
 
     gt = GraphTimer(torch)
-    return copies, R, gt.time(gemm, R, steps, warmup), gt.time(both, R, steps, warmup)
+    return copies, R, gt.time(gemm, R, steps, warmup), gt.time(both, R, steps, warmup), pack_us
 
 
 # config 3 (Q4_K at three prompt lengths, the Q6_K down projection) and
@@ -323,8 +342,9 @@ def config3_extras(torch, qk, synth, lib, steps, warmup, peak_tops=None):
     """Config 3 at M = 512 / 128 / 2048 (Q4_K) and the Q6_K down projection.
     peak_tops: the measured int8 MFMA throughput, for a second fraction."""
     extra = {}
-    for (t, n3, k3, m3) in CONFIG3_CASES:
-        c3, R, sg, sb = bench_config3(torch, qk, synth, lib, steps, warmup, t, n3, k3, m3)
+    for (t, n3, k3, m3, pl) in [c + (False,) for c in CONFIG3_CASES] + \
+            [c + (True,) for c in CONFIG3_CASES if c[0] != qk.Q8_0]:
+        c3, R, sg, sb, pack_us = bench_config3(torch, qk, synth, lib, steps, warmup, t, n3, k3, m3, planes=pl)
         ops = 2.0 * m3 * n3 * k3
         launches = steps * R
         alg = 4 * m3 * k3 + n3 * qk.row_bytes(t, k3) + 4 * m3 * n3
@@ -338,7 +358,9 @@ def config3_extras(torch, qk, synth, lib, steps, warmup, peak_tops=None):
              "copies": c3, "launches_per_step": R}
         if peak_tops:
             e["frac_of_measured_mfma_peak_gemm"] = round(tg / (peak_tops * 1e12), 4)
-        extra[f"config3_gemm_{name}_m{m3}_n{n3}_k{k3}"] = e
+        if pl:
+            e["pack_once_us"] = round(pack_us, 2)
+        extra[f"config3_gemm_{name}_m{m3}_n{n3}_k{k3}" + ("_planes" if pl else "")] = e
     return extra
 
 

@@ -217,6 +217,27 @@ int hip_matmul_q6k(const void *w, int64_t n, int64_t k, const void *xq,
 int hip_matmul_q8_0(const void *w, int64_t n, int64_t k, const void *xq,
                     int64_t m, float *y, void *stream);
 
+/* ---- device layer: prefill GEMM over repacked weights --------------- */
+
+/* No counterpart in the reference, whose weights stay in GGUF blocks; for
+ * callers that run many prefill GEMMs on one weight matrix. Weights are
+ * immutable after load (slm/slm.h:12-13), so a Q4_K / Q5_K / Q6_K matrix
+ * can be repacked once into int8 MFMA planes (552 / 552 / 520 bytes per
+ * row and super-block, against 144 / 176 / 210 for the blocks; the host
+ * seam does this for every matrix it runs a prefill GEMM on).
+ * hip_matmul_planes then computes exactly what hip_matmul_q4k / _q5k /
+ * _q6k compute on the original blocks, bit for bit, without re-deriving
+ * the operands for every token tile.
+ * hip_gemm_planes_bytes: bytes of the planes of an n x k matrix, 0 for a
+ * type or shape without planes. hip_gemm_pack_planes: w (device, native
+ * blocks, 16-byte aligned) -> planes (device, that many bytes, 16-byte
+ * aligned, not overlapping w). */
+size_t hip_gemm_planes_bytes(int type, int64_t n, int64_t k);
+int hip_gemm_pack_planes(int type, const void *w, int64_t n, int64_t k,
+                         void *planes, void *stream);
+int hip_matmul_planes(int type, const void *planes, int64_t n, int64_t k,
+                      const void *xq, int64_t m, float *y, void *stream);
+
 /* ---- device layer: dequantization ----------------------------------- */
 
 /* nblocks blocks -> nblocks*256 floats. Bit-exact q{4,5,6}k_dequant_block

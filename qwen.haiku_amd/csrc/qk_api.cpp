@@ -36,7 +36,14 @@ struct Weight {
     int64_t k, n;
     size_t bytes;
     void *dev;
+    void *planes = nullptr;    // Q5_K / Q6_K: int8 MFMA planes, made at the first prefill GEMM
 };
+
+void free_weight(Weight &w) {
+    (void)hipFree(w.dev);
+    if (w.planes) (void)hipFree(w.planes);
+    w.dev = w.planes = nullptr;
+}
 
 // Host-seam working set of one host thread: its own stream (the
 // reference's contexts are single-threaded each, slm/slm.h:33-36, so a
@@ -391,7 +398,7 @@ void hip_qk_shutdown(void) {
     s.sel.clear();
     for (void *p : s.retired) (void)hipFree(p);
     s.retired.clear();
-    for (auto &kv : s.weights) (void)hipFree(kv.second.dev);
+    for (auto &kv : s.weights) free_weight(kv.second);
     s.weights.clear();
     s.gen.fetch_add(1);                    // every thread's lane and device choice are stale
     s.init = false;
@@ -523,6 +530,43 @@ int hip_matmul_q6k(const void *w, int64_t n, int64_t k, const void *xq, int64_t 
 }
 int hip_matmul_q8_0(const void *w, int64_t n, int64_t k, const void *xq, int64_t m, float *y, void *s) {
     return matmul(QK_TYPE_Q8_0, w, n, k, xq, m, y, s);
+}
+
+size_t hip_gemm_planes_bytes(int type, int64_t n, int64_t k) {
+    if (type != QK_TYPE_Q4_K && type != QK_TYPE_Q5_K && type != QK_TYPE_Q6_K) return 0;
+    if (n < 1 || k < 1 || k % QK_K || k > QK_MAX_K || n > 0x7fffffffLL) return 0;
+    return qk::gemm_planes_bytes(type, n, k);
+}
+
+int hip_gemm_pack_planes(int type, const void *w, int64_t n, int64_t k, void *planes, void *s) {
+    int rc = require_init();
+    if (rc) return rc;
+    if (hip_gemm_planes_bytes(type, n, k) == 0)
+        return fail(QK_ERR_UNSUPPORTED, "no planes for type %d, n=%lld, k=%lld", type, (long long)n, (long long)k);
+    if ((rc = check_mat(type, w, n, k, planes, planes))) return rc;
+    if (!aligned(planes, 16)) return fail(QK_ERR_ARG, "planes must be 16-byte aligned");
+    const uintptr_t a = reinterpret_cast<uintptr_t>(w), b = reinterpret_cast<uintptr_t>(planes);
+    const size_t wb = (size_t)n * (size_t)(k / QK_K) * block_bytes(type), pb = qk::gemm_planes_bytes(type, n, k);
+    if (a < b + pb && b < a + wb) return fail(QK_ERR_ARG, "planes overlap the weights");
+    HIP_OK(qk::launch_pack_planes(type, static_cast<const uint8_t *>(w), n, k, static_cast<uint8_t *>(planes),
+                                  stream_of(s)),
+           "pack launch");
+    return QK_OK;
+}
+
+int hip_matmul_planes(int type, const void *planes, int64_t n, int64_t k, const void *xq, int64_t m, float *y,
+                      void *s) {
+    int rc = require_init();
+    if (rc) return rc;
+    if (hip_gemm_planes_bytes(type, n, k) == 0)
+        return fail(QK_ERR_UNSUPPORTED, "no planes for type %d, n=%lld, k=%lld", type, (long long)n, (long long)k);
+    if ((rc = check_mat(type, planes, n, k, xq, y))) return rc;
+    if (m < 1 || m > gemm_max_m(type))
+        return fail(QK_ERR_ARG, "m=%lld tokens (1..%lld)", (long long)m, (long long)gemm_max_m(type));
+    HIP_OK(qk::launch_gemm_planes(type, static_cast<const uint8_t *>(planes), n, k, static_cast<const uint8_t *>(xq),
+                                  m, y, fused_of(st().tier.load()), stream_of(s)),
+           "gemm launch");
+    return QK_OK;
 }
 
 static int dequant(int type, const void *w, int64_t nblocks, float *y, void *s) {
@@ -830,7 +874,7 @@ int register_locked(const void *host_w, int type, int64_t k, int64_t n) {
             return fail(QK_ERR_ARG, "weight %p re-registered with a different shape/type", host_w);
         return QK_OK;
     }
-    Weight w{type, k, n, (size_t)(n * (k / block_elems(type)) * block_bytes(type)), nullptr};
+    Weight w{type, k, n, (size_t)(n * (k / block_elems(type)) * block_bytes(type)), nullptr, nullptr};
     HIP_OK(hipMalloc(&w.dev, w.bytes), "hipMalloc(weight)");
     hipError_t e = hipMemcpy(w.dev, host_w, w.bytes, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
@@ -872,6 +916,40 @@ int acquire_weight(const void *host_w, int type, int64_t k, int64_t n, std::shar
     }
     return fail(QK_ERR_UNREGISTERED, "weight %p was unregistered during the call", host_w);
 }
+
+// Prefill GEMMs on Q5_K / Q6_K weights run on int8 MFMA planes
+// (hip_matmul_planes), made once per weight on its first prefill: release
+// the shared lock, pack under the exclusive one (synchronously, so no
+// other stream sees half-written planes), and take the shared lock again.
+bool planes_pay(int type) { return type == QK_TYPE_Q5_K || type == QK_TYPE_Q6_K; }
+
+int acquire_planes(const void *host_w, int type, int64_t k, int64_t n, hipStream_t stream,
+                   std::shared_lock<std::shared_mutex> &rl, Weight *out) {
+    State &s = st();
+    int rc;
+    if (out->planes) return QK_OK;
+    rl.unlock();
+    {
+        std::unique_lock<std::shared_mutex> wl(s.wmu);
+        auto it = s.weights.find(host_w);
+        if (it != s.weights.end() && !it->second.planes) {
+            Weight &w = it->second;
+            void *p = nullptr;
+            HIP_OK(hipMalloc(&p, qk::gemm_planes_bytes(type, n, k)), "hipMalloc(planes)");
+            hipError_t e = qk::launch_pack_planes(type, static_cast<const uint8_t *>(w.dev), n, k,
+                                                  static_cast<uint8_t *>(p), stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(stream);
+            if (e != hipSuccess) {
+                (void)hipFree(p);
+                return hip_fail(e, "pack planes");
+            }
+            w.planes = p;
+        }
+    }
+    if ((rc = acquire_weight(host_w, type, k, n, rl, out))) return rc;
+    if (!out->planes) return fail(QK_ERR_UNREGISTERED, "weight %p was re-registered during the call", host_w);
+    return QK_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -893,7 +971,7 @@ int hip_qk_unregister_weight(const void *host_w) {
     std::unique_lock<std::shared_mutex> wl(s.wmu);
     auto it = s.weights.find(host_w);
     if (it == s.weights.end()) return fail(QK_ERR_UNREGISTERED, "weight %p is not registered", host_w);
-    (void)hipFree(it->second.dev);
+    free_weight(it->second);
     s.weights.erase(it);
     return QK_OK;
 }
@@ -908,7 +986,7 @@ int hip_qk_unregister_range(const void *base, size_t bytes) {
     for (auto it = s.weights.begin(); it != s.weights.end();) {
         const uintptr_t a = reinterpret_cast<uintptr_t>(it->first), b = a + it->second.bytes;
         if (a < hi && lo < b) {
-            (void)hipFree(it->second.dev);
+            free_weight(it->second);
             it = s.weights.erase(it);
             count++;
         } else {
@@ -938,6 +1016,7 @@ int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f, int64_t k, c
     std::shared_lock<std::shared_mutex> rl;
     Weight w;
     if ((rc = acquire_weight(host_w, type, k, out_f, rl, &w))) return rc;
+    if (n_tok > 1 && planes_pay(type) && (rc = acquire_planes(host_w, type, k, out_f, l->stream, rl, &w))) return rc;
     const size_t xb = (size_t)(n_tok * k) * sizeof(float);
     const size_t qb = (size_t)(n_tok * act_bytes(type, k));
     const size_t yb = (size_t)(n_tok * out_f) * sizeof(float);
@@ -982,6 +1061,10 @@ int hip_qk_matmul_host(const void *host_w, int type, int64_t out_f, int64_t k, c
         a.d[0].y = dy;
         qk::gemv_plan(a.d[0]);
         HIP_OK(qk::launch_gemv(a, matvec_grid(type), l->stream), "gemv launch");
+    } else if (planes_pay(type)) {
+        HIP_OK(qk::launch_gemm_planes(type, static_cast<const uint8_t *>(w.planes), out_f, k, dxq, n_tok, dy, fused,
+                                      l->stream),
+               "gemm launch");
     } else {
         HIP_OK(qk::launch_gemm(type, static_cast<const uint8_t *>(w.dev), out_f, k, dxq, n_tok, dy, fused, l->stream),
                "gemm launch");

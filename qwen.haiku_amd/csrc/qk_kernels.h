@@ -77,4 +77,12 @@ hipError_t launch_deltanet(const float *q, const float *k, const float *v, const
 hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, const uint8_t *xq,
                        int64_t m, float *y, int fused, hipStream_t s);
 
+// Prefill GEMM over weights repacked into int8 MFMA planes
+// (qk_gemm_planes.hip): bytes of the planes of an n x k K-quant matrix (0
+// for other types), the repacking, and the GEMM.
+size_t gemm_planes_bytes(int type, int64_t n, int64_t k);
+hipError_t launch_pack_planes(int type, const uint8_t *w, int64_t n, int64_t k, uint8_t *wp, hipStream_t s);
+hipError_t launch_gemm_planes(int type, const uint8_t *wp, int64_t n, int64_t k, const uint8_t *xq, int64_t m,
+                              float *y, int fused, hipStream_t s);
+
 }  // namespace qk

@@ -99,6 +99,10 @@ class QK:
         L.hip_matvec_group_f32.argtypes = [C.POINTER(GemvDesc), C.c_int, _vp]
         for f in ("hip_matmul_q4k", "hip_matmul_q5k", "hip_matmul_q6k", "hip_matmul_q8_0"):
             getattr(L, f).argtypes = [_vp, _i64, _i64, _vp, _i64, _vp, _vp]
+        L.hip_gemm_planes_bytes.argtypes = [C.c_int, _i64, _i64]
+        L.hip_gemm_planes_bytes.restype = C.c_size_t
+        L.hip_gemm_pack_planes.argtypes = [C.c_int, _vp, _i64, _i64, _vp, _vp]
+        L.hip_matmul_planes.argtypes = [C.c_int, _vp, _i64, _i64, _vp, _i64, _vp, _vp]
         for f in ("hip_dequant_q4k", "hip_dequant_q5k", "hip_dequant_q6k"):
             getattr(L, f).argtypes = [_vp, _i64, _vp, _vp]
         L.hip_lmhead_q6k_argmax_topk.argtypes = [_vp, _i64, _i64, _vp, C.c_int, _vp, _vp, _vp, _vp, _vp]
@@ -214,6 +218,30 @@ class QK:
         _need(xq, m * act_bytes(wtype, k), "xq")
         _need(y, 4 * m * n, "y")
         self._ck(f(_dp(w), n, k, _dp(xq), m, _dp(y), self._stream()))
+        return y
+
+    def planes_bytes(self, wtype, n, k):
+        return int(self.L.hip_gemm_planes_bytes(wtype, n, k))
+
+    def pack_planes(self, wtype, w, n, k, planes=None):
+        """Repack a device K-quant matrix into the GEMM's int8 MFMA planes."""
+        import torch
+        nb = self.planes_bytes(wtype, n, k)
+        if planes is None:
+            planes = torch.empty(nb, dtype=torch.uint8, device=w.device)
+        _need(w, n * row_bytes(wtype, k), "w")
+        _need(planes, nb, "planes")
+        self._ck(self.L.hip_gemm_pack_planes(wtype, _dp(w), n, k, _dp(planes), self._stream()))
+        return planes
+
+    def matmul_planes(self, wtype, planes, n, k, xq, m, y=None):
+        import torch
+        if y is None:
+            y = torch.empty((m, n), dtype=torch.float32, device=planes.device)
+        _need(planes, self.planes_bytes(wtype, n, k), "planes")
+        _need(xq, m * act_bytes(wtype, k), "xq")
+        _need(y, 4 * m * n, "y")
+        self._ck(self.L.hip_matmul_planes(wtype, _dp(planes), n, k, _dp(xq), m, _dp(y), self._stream()))
         return y
 
     def dequant(self, wtype, w, nblocks, y=None):

@@ -386,9 +386,12 @@ def test_lmhead_argmax_ties(lib, orc):
 
 # ---- host seam ---------------------------------------------------------------------------
 
+# Q5_K / Q6_K prefill GEMMs go through int8 MFMA planes packed at the
+# first one (both kernels: up to 1024 output tiles and beyond)
 @pytest.mark.parametrize("wtype,n,k,m", [(12, 3584, 1024, 1), (13, 512, 1024, 1), (14, 1024, 3584, 1),
                                           (8, 1024, 1024, 1), (8, 64, 1024, 21), (12, 3584, 1024, 64),
-                                          (13, 512, 1024, 21), (14, 1024, 3584, 9)])
+                                          (13, 512, 1024, 21), (14, 1024, 3584, 9), (14, 1024, 3584, 600),
+                                          (13, 2048, 1024, 700)])
 def test_matmul_host_seam(lib, orc, wtype, n, k, m):
     step(f"host seam type={wtype} n={n} k={k} m={m}")
     w = synth.blocks(wtype, n, k, seed=3, tag=wtype)
