@@ -336,20 +336,25 @@ def bench_config3(torch, qk, synth, lib, steps, warmup, wtype=12, n=3584, k=1024
 # the Q8_0 GEMM on config 1's Q8_0 matrix at a 512-token prompt
 CONFIG3_CASES = ((12, 3584, 1024, 512), (12, 3584, 1024, 128), (12, 3584, 1024, 2048), (14, 1024, 3584, 512),
                  (8, 1024, 1024, 512))
+# the GEMM on int8 MFMA planes (hip_matmul_planes): config 3's K-quant cases,
+# the Q6_K down projection at 128 / 2048 tokens and a Q5_K projection
+PLANES_CASES = tuple(c for c in CONFIG3_CASES if c[0] != 8) + \
+    ((14, 1024, 3584, 128), (14, 1024, 3584, 2048), (13, 2048, 1024, 512), (13, 2048, 1024, 2048))
 
 
-def config3_extras(torch, qk, synth, lib, steps, warmup, peak_tops=None):
-    """Config 3 at M = 512 / 128 / 2048 (Q4_K) and the Q6_K down projection.
-    peak_tops: the measured int8 MFMA throughput, for a second fraction."""
+def config3_extras(torch, qk, synth, lib, steps, warmup, peak_tops=None, native=True):
+    """Config 3 at M = 512 / 128 / 2048 (Q4_K) and the Q6_K down projection,
+    on the native blocks and on the planes. peak_tops: the measured int8
+    MFMA throughput, for a second fraction."""
     extra = {}
-    for (t, n3, k3, m3, pl) in [c + (False,) for c in CONFIG3_CASES] + \
-            [c + (True,) for c in CONFIG3_CASES if c[0] != qk.Q8_0]:
+    for (t, n3, k3, m3, pl) in ([c + (False,) for c in CONFIG3_CASES] if native else []) + \
+            [c + (True,) for c in PLANES_CASES]:
         c3, R, sg, sb, pack_us = bench_config3(torch, qk, synth, lib, steps, warmup, t, n3, k3, m3, planes=pl)
         ops = 2.0 * m3 * n3 * k3
         launches = steps * R
         alg = 4 * m3 * k3 + n3 * qk.row_bytes(t, k3) + 4 * m3 * n3
         tg, tb = ops * launches / sg, ops * launches / sb
-        name = {8: "q80", 12: "q4k", 14: "q6k"}[t]
+        name = {8: "q80", 12: "q4k", 13: "q5k", 14: "q6k"}[t]
         e = {"TOPS_gemm": round(tg / 1e12, 2), "us_gemm": round(sg / launches * 1e6, 3),
              "TOPS_with_quantize": round(tb / 1e12, 2), "us_with_quantize": round(sb / launches * 1e6, 3),
              "frac_of_5POPS_gemm": round(tg / (MFMA_I8_PEAK_TOPS * 1e12), 4),
@@ -670,8 +675,8 @@ def main():
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--warm-seconds", type=float, default=WARM_S,
                     help="minimum warm-up replay time per case (short values keep profiler traces small)")
-    ap.add_argument("--only", choices=["all", "config1", "config3", "lmhead", "q4k_stream", "chain", "sampler",
-                                       "deltanet"],
+    ap.add_argument("--only", choices=["all", "config1", "config3", "config3_planes", "lmhead", "q4k_stream",
+                                       "chain", "sampler", "deltanet"],
                     default="all",
                     help="time one case only (profiling aids)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -698,9 +703,10 @@ def main():
     def progress(msg):
         print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
-    if a.only == "config3":
+    if a.only in ("config3", "config3_planes"):
         print(json.dumps({"metric": "prefill int8 TOPS (config 3)", "unit": "TOPS", "dtype": "int8",
-                          "extra": config3_extras(torch, qk, synth, lib, a.steps, a.warmup)}))
+                          "extra": config3_extras(torch, qk, synth, lib, a.steps, a.warmup,
+                                                  native=a.only == "config3")}))
         return
     if a.only == "lmhead":
         p2, c2, R2, s2 = bench_config2(torch, qk, synth, lib, a.steps, a.warmup)
