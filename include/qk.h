@@ -288,13 +288,14 @@ int hip_swiglu_q8k(const float *gate, const float *up, int64_t m, int64_t k,
  *   logits (optional, may be NULL): n floats, as hip_matvec_q6k;
  *   *argmax: first index of the maximum logit (sample_argmax,
  *            slm/model.c:401-412: strict '>', NaN never wins);
- *   topk_idx/topk_val (optional when topk == 0): the topk largest
- *            logits, value-descending, ties broken by lower index; the
- *            set equals topk_collect's (slm/sampler.c:70-93) whenever
- *            the topk-th value is not tied and no logit is NaN. NaN
- *            logits rank below every number here; topk_collect instead
- *            keeps a NaN that lands in its first k slots and, once one
- *            holds its minimum slot, replaces nothing more.
+ *   topk_idx/topk_val (optional when topk == 0): the set
+ *            topk_collect (slm/sampler.c:70-93) keeps whenever the
+ *            topk-th largest number is not tied: the topk largest logits,
+ *            except that a NaN among the first topk rows keeps its slot
+ *            (the rest are the largest numbers) and a NaN at row 0 keeps
+ *            rows 0..topk-1; a later NaN never enters. Ranked numbers
+ *            first, value-descending (ties by lower index), then the NaN
+ *            rows by row.
  * 0 <= topk <= QK_TOPK_MAX. All outputs are device pointers.
  * Selection scratch is kept per stream: calls on different streams run
  * concurrently without sharing it. A stream's scratch is replaced (never

@@ -1327,6 +1327,14 @@ __global__ __launch_bounds__(1024) void k_topk_filter(const float *__restrict__ 
 // row-ascending, by the filter's last block (all 1024 threads). The
 // candidates and their count were written by atomics at agent scope, which
 // bypass the per-XCD L2, so plain agent-scope atomic loads see them.
+//
+// NaN follows topk_collect (slm/sampler.c:70-93): its first k rows fill the
+// slots, and a NaN slot never compares as the worst one, so it is never
+// replaced; a NaN after the fill never enters (NaN > x is false). With row
+// 0 NaN the worst slot stays 0 and nothing is ever replaced: the set is
+// rows 0..k-1. Otherwise the set is the c NaN rows among 1..k-1 plus the
+// k - c largest numbers. Ranked here: numbers value-descending, then the
+// NaN rows by row.
 __device__ __forceinline__ uint64_t agent_load(const uint64_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1336,34 +1344,52 @@ __device__ void topk_rank(const float *__restrict__ logits, int64_t n, const uin
     __shared__ uint32_t hist[258];
     __shared__ uint64_t win[1024];                     // candidates (ranking) or winners
     __shared__ uint64_t red[16];
-    __shared__ uint32_t nwin;
+    __shared__ uint32_t nwin, nnan, frozen;
+    __shared__ uint8_t nanrow[QK_TOPK_MAX_DEV];        // NaN among the first k rows
     const int t = threadIdx.x;
     const uint64_t mine = agent_load(&cand[t]);        // t < 1024 <= TOPK_CAND; used when t < c
-    if (t == 0) nwin = 0;
+    const float fill = t < topk && t < n ? logits[t] : 0.0f;
+    const bool fnan = t < topk && t < n && fill != fill;
+    if (t == 0) {
+        nwin = 0;
+        nnan = 0;
+        frozen = fnan;
+    }
+    if (t < topk) nanrow[t] = fnan;
+    __syncthreads();
+    if (fnan && t > 0) atomicAdd(&nnan, 1u);
+    __syncthreads();
+    // numbers to rank: all k when row 0 is NaN (the fill itself is ranked),
+    // else k minus the NaN rows of the fill
+    const int kk = frozen ? topk : topk - (int)nnan;
     int nw;                                            // keys in win[] to rank
-    if (c <= 1024) {
-        // Few candidates: rank every one of them directly.
-        if (t < (int)c) win[t] = mine;
-        nw = (int)c;
+    if (frozen) {
+        if (t < topk) win[t] = ((uint64_t)valkey(fill) << 32) | (0xffffffffu - (uint32_t)t);
+        nw = topk;
+    } else if (c <= 1024) {
+        // Few candidates: rank every number among them directly.
+        if (t < (int)c && (mine >> 32) != 0) win[atomicAdd(&nwin, 1u)] = mine;
+        __syncthreads();
+        nw = (int)nwin;
     } else if (c <= TOPK_CAND) {
         uint64_t key[4];
         bool have[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const uint32_t i = t + 1024 * r;
-            have[r] = i < c;
-            key[r] = r == 0 ? mine : have[r] ? agent_load(&cand[i]) : 0;
+            key[r] = r == 0 ? mine : i < c ? agent_load(&cand[i]) : 0;
+            have[r] = i < c && (key[r] >> 32) != 0;    // value key 0: NaN
         }
-        const uint64_t T = block_kth_largest<4, 64, uint64_t>(key, have, topk, hist);
+        const uint64_t T = block_kth_largest<4, 64, uint64_t>(key, have, kk, hist);
 #pragma unroll
         for (int r = 0; r < 4; r++)
             if (have[r] && key[r] >= T) win[atomicAdd(&nwin, 1u)] = key[r];
-        nw = topk;
+        nw = kk;
     } else {
         // Fallback: k exact passes, each taking the largest key below the
-        // previous winner.
+        // previous winner (NaN keys, 0, never win).
         uint64_t prev = ~(uint64_t)0;
-        for (int r = 0; r < topk; r++) {
+        for (int r = 0; r < kk; r++) {
             uint64_t b = 0;
             for (int64_t i = t; i < n; i += 1024) {
                 const uint64_t kk = ((uint64_t)valkey(logits[i]) << 32) | (0xffffffffu - (uint32_t)i);
@@ -1383,7 +1409,7 @@ __device__ void topk_rank(const float *__restrict__ logits, int64_t n, const uin
             if (t == 0) win[r] = bb;
             prev = bb;
         }
-        nw = topk;
+        nw = kk;
     }
     __syncthreads();
     // Rank the keys (all distinct): P lanes per key, lane j of a group
@@ -1400,9 +1426,16 @@ __device__ void topk_rank(const float *__restrict__ logits, int64_t n, const uin
     if (live)
         for (int q = j; q < nw; q += P) cnt += win[q] > me;
     cnt = group_sum(cnt, P);
-    if (live && j == 0 && cnt < topk) {
+    if (live && j == 0 && cnt < kk) {
         topk_idx[cnt] = idx;
         topk_val[cnt] = val;
+    }
+    // the fill's NaN rows after the numbers, by row
+    if (!frozen && fnan && t > 0) {
+        int below = 0;
+        for (int u = 1; u < t; u++) below += nanrow[u];
+        topk_idx[kk + below] = t;
+        topk_val[kk + below] = fill;
     }
 }
 
