@@ -404,13 +404,15 @@ def test_matmul_host_seam(lib, orc, wtype, n, k, m):
     lib.unregister_weight(w)
 
 
-def test_host_seam_reload_at_same_address(lib, orc):
+@pytest.mark.parametrize("t", [12, 13, 14])
+def test_host_seam_reload_at_same_address(lib, orc, t):
     # a model unloaded and another loaded at the same host addresses (the
     # GGUF mapping reused): hip_qk_unregister_range, which the seam calls
-    # before munmap, drops the old device copy, so the new bytes are used
+    # before munmap, drops the old device copy (and, for Q5_K / Q6_K, the
+    # MFMA planes the first prefill made), so the new bytes are used
     import ctypes as C
-    step("host seam reload at the same address")
-    t, n, k = 12, 512, 1024
+    step(f"host seam reload at the same address type={t}")
+    n, k = 512, 1024
     buf = synth.blocks(t, n, k, seed=40)
     x = synth.activations(2, k, seed=40)
     epi = oracle.TIER_EPI[lib.tier()]
