@@ -950,14 +950,23 @@ __global__ __launch_bounds__(256) void k_gemm_r(const uint8_t *__restrict__ w, i
 // writes its 16 terms per lane to LDS, and wave w adds, for outputs
 // 4w..4w+3 of every lane, the round's terms in order to the running sums
 // (sum starts at +0.0, so the first term enters exactly), which is the
-// reference's sequential `sum += term`.
-template <bool FUSED>
+// reference's sequential `sum += term`. SHARE: the terms reuse the
+// activations' LDS once every wave has read them (one more barrier a
+// round), so four workgroups fit a CU instead of three. Lane l's outputs
+// 4w..4w+3 are tokens 8w + 4(l / 32) + b, b < 4, of row l % 32: one output
+// pointer, stepped by n.
+template <bool SHARE> struct KsShared {
+    int8_t sa[4][32][GM_LD];          // super-block 4r + q in sa[q]: a token's 256 quants, then its bsum pairs as two int8 digits
+    float st[4][16][64];              // st[q][v][lane]: wave q's term for output v of a lane
+};
+template <> struct KsShared<true> {
+    union { int8_t sa[4][32][GM_LD]; float st[4][16][64]; };
+};
+
+template <bool FUSED, bool SHARE>
 __global__ __launch_bounds__(256) void k_gemm_ks(const uint8_t *__restrict__ w, int64_t n, int nb,
                                                  const uint8_t *__restrict__ xq, int64_t m, float *__restrict__ y) {
-    // super-block 4r + q in sa[q]: a token's 256 quants, then in the row's
-    // last 16 bytes its bsum pairs as two int8 digits
-    __shared__ __attribute__((aligned(16))) int8_t sa[4][32][GM_LD];
-    __shared__ __attribute__((aligned(16))) float st[4][16][64];       // the waves' terms, [wave][v][lane]
+    __shared__ __attribute__((aligned(16))) KsShared<SHARE> sh;
     __shared__ float syd[4][32];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, h = lane >> 5;
@@ -966,10 +975,13 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const uint8_t *__restrict__ w, 
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(xq + t0 * nb * Q8K_BYTES), 0, mrows * nb * Q8K_BYTES, 0x00020000);
     // staging: thread t stages eighth e = t % 8 of token t / 8 for each of
-    // the round's four super-blocks (super-block 4r + q in sa[q])
+    // the round's four super-blocks; the token's byte offset in the tile
+    // (below 2^24: nb <= 256)
     const int at = tid >> 3, ae = tid & 7;
+    const int abase = (int)__umul24((uint32_t)at, (uint32_t)(nb * Q8K_BYTES)) + 32 * ae;
     const int64_t row = r0 + col;
-    const uint8_t *wp = w + (row < n ? row : n - 1) * nb * Q4K_BYTES;
+    const uint32_t rowc = (uint32_t)(row < n ? row : n - 1);
+    const uint8_t *wp = w + (uint64_t)rowc * (uint32_t)(nb * Q4K_BYTES) + 16 * h;
     const v16i zero = {0};
     float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};          // this lane's outputs v = 4 * wave + b
     for (int r = 0; r < nb; r += 4) {
@@ -978,20 +990,20 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const uint8_t *__restrict__ w, 
         // weights of this wave's super-block, in flight during staging
         struct W5 { uint4 hdr, p[4]; } cw;
         {
-            const uint8_t *p = wp + (int64_t)(act ? sb : nb - 1) * Q4K_BYTES;
-            cw.hdr = ld16(p);
+            const uint8_t *p = wp + (act ? sb : nb - 1) * Q4K_BYTES;
+            cw.hdr = ld16(p - 16 * h);
 #pragma unroll
-            for (int c = 0; c < 4; c++) cw.p[c] = ld16(p + 16 + 32 * c + 16 * h);
+            for (int c = 0; c < 4; c++) cw.p[c] = ld16(p + 16 + 32 * c);
         }
         // the round's activations, in flight during the unpack
         struct A8 { uint4 q0, q1; uint32_t bp, d; } ar[4];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const int o = at * nb * Q8K_BYTES + (r + q < nb ? r + q : nb - 1) * Q8K_BYTES;
-            ar[q].q0 = bl128(xr, o + 4 + 32 * ae);
-            ar[q].q1 = bl128(xr, o + 20 + 32 * ae);
-            ar[q].bp = bl32(xr, o + 260 + 4 * ae);
-            ar[q].d = bl32(xr, o);
+            const int o = abase + (r + q < nb ? r + q : nb - 1) * Q8K_BYTES;
+            ar[q].q0 = bl128(xr, o + 4);
+            ar[q].q1 = bl128(xr, o + 20);
+            ar[q].bp = bl32(xr, o + 260 - 28 * ae);
+            ar[q].d = bl32(xr, o - 32 * ae);
         }
         // previous round's reads done, then this round's activations
         auto stage = [&]() {
@@ -999,15 +1011,16 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const uint8_t *__restrict__ w, 
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 if (r + q >= nb) break;                // uniform
-                *(QK_LDS uint4 *)&sa[q][at][32 * ae] = ar[q].q0;
-                *(QK_LDS uint4 *)&sa[q][at][32 * ae + 16] = ar[q].q1;
+                *(QK_LDS uint4 *)&sh.sa[q][at][32 * ae] = ar[q].q0;
+                *(QK_LDS uint4 *)&sh.sa[q][at][32 * ae + 16] = ar[q].q1;
                 const int32_t pr = (int32_t)(int16_t)(ar[q].bp & 0xffffu) + (int32_t)(int16_t)(ar[q].bp >> 16);
-                sa[q][at][256 + ae] = (int8_t)(pr & 127);
-                sa[q][at][264 + ae] = (int8_t)(pr >> 7);
+                sh.sa[q][at][256 + ae] = (int8_t)(pr & 127);
+                sh.sa[q][at][264 + ae] = (int8_t)(pr >> 7);
                 if (ae == 0) syd[q][at] = __uint_as_float(ar[q].d);
             }
             lds_barrier();
         };
+        float tm[16];                                  // this wave's terms
         if (!act) stage();                             // wave-uniform: the barriers match the active waves'
         if (act) {
             v4i pb[8][2];
@@ -1039,13 +1052,13 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const uint8_t *__restrict__ w, 
             v16i a0 = zero, a1 = zero;
 #pragma unroll
             for (int s2 = 0; s2 < 8; s2++) {
-                const v4i av = *(const QK_LDS v4i *)(&sa[wave][col][32 * s2 + 16 * h]);
+                const v4i av = *(const QK_LDS v4i *)(&sh.sa[wave][col][32 * s2 + 16 * h]);
                 a0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, pb[s2][0], a0, 0, 0, 0);
                 a1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, pb[s2][1], a1, 0, 0, 0);
             }
             // isum_mins as two small MFMAs (bsum pair digits lo | hi
             // against the mins: mins = lo_product + 128 * hi_product)
-            const long amv = *(const QK_LDS long *)&sa[wave][col][256 + 8 * h];
+            const long amv = *(const QK_LDS long *)&sh.sa[wave][col][256 + 8 * h];
             const v16i dl = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 0 ? mnv : 0L, zero, 0, 0, 0);
             const v16i dh = __builtin_amdgcn_mfma_i32_32x32x16_i8(amv, h == 1 ? mnv : 0L, zero, 0, 0, 0);
 #pragma unroll
@@ -1056,8 +1069,13 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const uint8_t *__restrict__ w, 
                 const float d = __fmul_rn(yd, wd);
                 const float dmin = __fmul_rn(yd, wdm);
                 const float pm = __fmul_rn(dmin, (float)mins);
-                st[wave][v][lane] = FUSED ? __builtin_fmaf(d, (float)is, -pm) : __fsub_rn(__fmul_rn(d, (float)is), pm);
+                tm[v] = FUSED ? __builtin_fmaf(d, (float)is, -pm) : __fsub_rn(__fmul_rn(d, (float)is), pm);
             }
+        }
+        if constexpr (SHARE) lds_barrier();            // every wave's reads of sa done
+        if (act) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) sh.st[wave][v][lane] = tm[v];
         }
         lds_barrier();
         // the round's terms in super-block order, outputs 4 * wave .. + 3
@@ -1065,19 +1083,19 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const uint8_t *__restrict__ w, 
         for (int q = 0; q < 4; q++) {
             if (r + q >= nb) break;                    // uniform
 #pragma unroll
-            for (int b = 0; b < 4; b++) sum[b] = __fadd_rn(sum[b], st[q][4 * wave + b][lane]);
+            for (int b = 0; b < 4; b++) sum[b] = __fadd_rn(sum[b], sh.st[q][4 * wave + b][lane]);
         }
     }
     if (row < n) {
+        const int tt = 8 * wave + 4 * h;               // token of output 4 * wave in the tile
+        float *yp = y + (uint64_t)(uint32_t)(t0 + tt) * (uint64_t)n + row;
 #pragma unroll
         for (int b = 0; b < 4; b++) {
-            const int v = 4 * wave + b;
-            const int64_t t = t0 + tok_of(v, h);
-            if (t < m) __builtin_nontemporal_store(FUSED ? bcast8(sum[b]) : sum[b], &y[t * n + row]);
+            if (tt + b < mrows) __builtin_nontemporal_store(FUSED ? bcast8(sum[b]) : sum[b], yp);
+            yp += n;
         }
     }
 }
-
 // ---- super-blocks across waves (Q6_K) -------------------------------------------
 // k_gemm_ks for Q6_K (q6k_row_dot_q8k, simd/quants.h:355-402): a 256-thread
 // workgroup owns one 32-token x 32-row tile, wave w computes super-block
@@ -1485,9 +1503,16 @@ hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, const u
         // 4.2 against 7.5 us, 128 5.2 / 7.4, 256 6.8 / 9.7, 384 8.7 / 11.4,
         // 512 10.1 / 10.4 (k_gemm_r); 768 14.2 / 13.8.
         if (type == 12 && m <= 512) {
+            // terms in the activations' LDS once the tiles outnumber three
+            // workgroups per CU (N = 3584, K = 1024: M = 512 10.1 -> 9.6 us,
+            // 256 6.77 -> 6.67; M = 128 keeps the separate arrays, 5.17
+            // against 5.24)
             const dim3 grid((unsigned)((n + 31) / 32), (unsigned)((m + 31) / 32));
-            if (fused) hipLaunchKernelGGL((k_gemm_ks<true>), grid, dim3(256), 0, s, w, n, nb, xq, m, y);
-            else hipLaunchKernelGGL((k_gemm_ks<false>), grid, dim3(256), 0, s, w, n, nb, xq, m, y);
+            const bool share = (uint64_t)grid.x * grid.y > 3 * 256;
+#define QK_KS_LAUNCH(F, S) hipLaunchKernelGGL((k_gemm_ks<F, S>), grid, dim3(256), 0, s, w, n, nb, xq, m, y)
+            if (fused) { if (share) QK_KS_LAUNCH(true, true); else QK_KS_LAUNCH(true, false); }
+            else { if (share) QK_KS_LAUNCH(false, true); else QK_KS_LAUNCH(false, false); }
+#undef QK_KS_LAUNCH
             return hipGetLastError();
         }
         if (tiles >= 192 && type == 12) {
