@@ -275,6 +275,27 @@ __device__ __forceinline__ float bcast8(float s) {
     return __fmul_rn(__fmul_rn(s, 8.0f), 0.125f);   // x / 8 and x * 2^-3 round the same exact value
 }
 
+// Stores outputs v0 .. v0 + NV - 1 of one lane of a 32x32 MFMA tile
+// (v_mfma_i32_32x32x*: output v of lane l is token 8(v / 4) + 4(l / 32) +
+// v % 4 of the tile and weight row l % 32) as y[t * n + row], where the
+// tile's tokens start at t0 + tm; outputs whose tile token is mrows or
+// more (past the tokens this tile holds) are not stored. One lane pointer, stepped by n to the
+// next token or by 5n past the fourth of a group of four, so no 64-bit
+// product per output.
+template <bool FUSED, int NV>
+__device__ __forceinline__ void store_mfma32(float *__restrict__ y, int64_t n, int64_t row, int64_t t0, int tm,
+                                             int mrows, int v0, int h, const float *s) {
+    const int tb = tm + 8 * (v0 >> 2) + 4 * h + (v0 & 3);
+    float *yp = y + (uint64_t)(uint32_t)(t0 + tb) * (uint64_t)n + row;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int v = v0 + i;
+        if (tm + 8 * (v >> 2) + 4 * h + (v & 3) < mrows)
+            __builtin_nontemporal_store(FUSED ? bcast8(s[i]) : s[i], yp);
+        yp += (v & 3) == 3 ? 5 * n : n;
+    }
+}
+
 // Q6_K term (all tiers, simd/quants.h:399): rn(rn(fp16(x.d)*y.d) * (float)v).
 __device__ __forceinline__ float q6term(float yd, uint32_t xd, int32_t v) {
     return __fmul_rn(__fmul_rn(h2f(xd), yd), (float)v);

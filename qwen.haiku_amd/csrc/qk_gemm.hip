@@ -617,13 +617,7 @@ void k_gemm(const uint8_t *__restrict__ w, int64_t n, int nb, const uint8_t *__r
         // non-temporal stores: the outputs are not read again by this
         // kernel, and every workgroup's stores leave at about the same time
         const int64_t row = r0 + tn + col;
-        if (row < n) {
-#pragma unroll
-            for (int v = 0; v < VPW; v++) {
-                const int64_t t = t0 + tm + tok_of(VPW * g + v, h);
-                if (t < m) __builtin_nontemporal_store(FUSED ? bcast8(sum[v]) : sum[v], &y[t * n + row]);
-            }
-        }
+        if (row < n) store_mfma32<FUSED, VPW>(y, n, row, t0, tm, mrows, VPW * g, h, sum);
     };
     if (role == 1) {
         typename WRawOf<TYPE>::T wr;
@@ -772,13 +766,7 @@ void k_gemm_w(const uint8_t *__restrict__ w, int64_t n, int nb, const uint8_t *_
         }
     }
     const int64_t row = r0 + tn + col;
-    if (row < n) {
-#pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const int64_t t = t0 + tm + tok_of(v, h);
-            if (t < m) __builtin_nontemporal_store(FUSED ? bcast8(sum[v]) : sum[v], &y[t * n + row]);
-        }
-    }
+    if (row < n) store_mfma32<FUSED, 16>(y, n, row, t0, tm, mrows, 0, h, sum);
 }
 
 // ---- weight rows in registers (Q4_K) -----------------------------------------------
@@ -809,10 +797,12 @@ __global__ __launch_bounds__(256) void k_gemm_r(const uint8_t *__restrict__ w, i
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(xq + t0 * nb * Q8K_BYTES), 0, mrows * nb * Q8K_BYTES, 0x00020000);
     struct A8 { uint4 q0, q1; uint32_t bp, d; } ar[NT];
+    // token at's byte offset in the tile (below 2^24: nb <= 256)
+    const int abase = (int)__umul24((uint32_t)at, (uint32_t)(nb * Q8K_BYTES));
     auto load_a = [&](int i) {
 #pragma unroll
         for (int j = 0; j < NT; j++) {
-            const int o = (at + 32 * j) * nb * Q8K_BYTES + i * Q8K_BYTES;
+            const int o = abase + (32 * j * nb + i) * Q8K_BYTES;
             ar[j].q0 = bl128(xr, o + 4 + 32 * ae);
             ar[j].q1 = bl128(xr, o + 20 + 32 * ae);
             ar[j].bp = bl32(xr, o + 260 + 4 * ae);
@@ -833,7 +823,7 @@ __global__ __launch_bounds__(256) void k_gemm_r(const uint8_t *__restrict__ w, i
     };
     // weights: this lane's row and k-half
     const int64_t row = r0 + 32 * wave + col;
-    const uint8_t *wp = row < n ? w + row * nb * Q4K_BYTES : nullptr;
+    const uint8_t *wp = row < n ? w + (uint64_t)(uint32_t)row * (uint32_t)(nb * Q4K_BYTES) : nullptr;
     struct W5 { uint4 hdr, p[4]; } wr;
     auto load_w = [&](int i) {
         if (!wp) {
@@ -932,12 +922,7 @@ __global__ __launch_bounds__(256) void k_gemm_r(const uint8_t *__restrict__ w, i
     }
     if (row < n) {
 #pragma unroll
-        for (int j = 0; j < NT; j++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int64_t t = t0 + 32 * j + tok_of(v, h);
-                if (t < m) __builtin_nontemporal_store(FUSED ? bcast8(sum[j][v]) : sum[j][v], &y[t * n + row]);
-            }
+        for (int j = 0; j < NT; j++) store_mfma32<FUSED, 16>(y, n, row, t0, 32 * j, mrows, 0, h, sum[j]);
     }
 }
 
@@ -952,9 +937,7 @@ __global__ __launch_bounds__(256) void k_gemm_r(const uint8_t *__restrict__ w, i
 // (sum starts at +0.0, so the first term enters exactly), which is the
 // reference's sequential `sum += term`. SHARE: the terms reuse the
 // activations' LDS once every wave has read them (one more barrier a
-// round), so four workgroups fit a CU instead of three. Lane l's outputs
-// 4w..4w+3 are tokens 8w + 4(l / 32) + b, b < 4, of row l % 32: one output
-// pointer, stepped by n.
+// round), so four workgroups fit a CU instead of three.
 template <bool SHARE> struct KsShared {
     int8_t sa[4][32][GM_LD];          // super-block 4r + q in sa[q]: a token's 256 quants, then its bsum pairs as two int8 digits
     float st[4][16][64];              // st[q][v][lane]: wave q's term for output v of a lane
@@ -1086,15 +1069,7 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const uint8_t *__restrict__ w, 
             for (int b = 0; b < 4; b++) sum[b] = __fadd_rn(sum[b], sh.st[q][4 * wave + b][lane]);
         }
     }
-    if (row < n) {
-        const int tt = 8 * wave + 4 * h;               // token of output 4 * wave in the tile
-        float *yp = y + (uint64_t)(uint32_t)(t0 + tt) * (uint64_t)n + row;
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            if (tt + b < mrows) __builtin_nontemporal_store(FUSED ? bcast8(sum[b]) : sum[b], yp);
-            yp += n;
-        }
-    }
+    if (row < n) store_mfma32<FUSED, 4>(y, n, row, t0, 0, mrows, 4 * wave, h, sum);
 }
 // ---- super-blocks across waves (Q6_K) -------------------------------------------
 // k_gemm_ks for Q6_K (q6k_row_dot_q8k, simd/quants.h:355-402): a 256-thread
@@ -1149,6 +1124,7 @@ __global__ __launch_bounds__(64 * S) void k_gemm_ks6(const uint8_t *__restrict__
         const_cast<uint8_t *>(wt - off0), 0, off0 + nrows * nb * Q6K_BYTES, 0x00020000);
     // staging: eighth ae of token at, of super-blocks Sr + 4g .. + 3
     const int at = (tid >> 3) & 31, ae = tid & 7, ag = tid >> 8;
+    const int abase = (int)__umul24((uint32_t)at, (uint32_t)(nb * Q8K_BYTES));   // below 2^24: nb <= 256
     const int row = (int)(r0 + col);
     constexpr int VW = 16 / S;                         // outputs per lane each wave adds up
     float sum[VW];
@@ -1186,7 +1162,7 @@ __global__ __launch_bounds__(64 * S) void k_gemm_ks6(const uint8_t *__restrict__
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int sq = r + 4 * ag + q;
-            const int o = at * nb * Q8K_BYTES + (sq < nb ? sq : nb - 1) * Q8K_BYTES;
+            const int o = abase + (sq < nb ? sq : nb - 1) * Q8K_BYTES;
             ar[q].q0 = bl128(xr, o + 4 + 32 * ae);
             ar[q].q1 = bl128(xr, o + 20 + 32 * ae);
             ar[q].bp = bl32(xr, o + 260 + 4 * ae);
@@ -1271,14 +1247,7 @@ __global__ __launch_bounds__(64 * S) void k_gemm_ks6(const uint8_t *__restrict__
             for (int bb = 0; bb < VW; bb++) sum[bb] = __fadd_rn(sum[bb], st[q][VW * wave + bb][lane]);
         }
     }
-    if (row < n) {
-#pragma unroll
-        for (int bb = 0; bb < VW; bb++) {
-            const int v = VW * wave + bb;
-            const int64_t t = t0 + tok_of(v, h);
-            if (t < m) __builtin_nontemporal_store(FUSED ? bcast8(sum[bb]) : sum[bb], &y[t * n + row]);
-        }
-    }
+    if (row < n) store_mfma32<FUSED, VW>(y, n, row, t0, 0, mrows, VW * wave, h, sum);
 }
 
 // ---- Q8_0 x Q8_0 --------------------------------------------------------------
