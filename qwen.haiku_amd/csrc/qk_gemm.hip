@@ -1467,11 +1467,12 @@ hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, const u
         // tiles below 1024 tokens, 64-token tiles from there (N = 3584,
         // K = 1024: M = 512 10.7 against 11.0 us, 1024 15.3 against 16.0,
         // 2048 27.9 against 30.0)
-        // Q4_K up to 512 tokens: the super-blocks of a 32 x 32 tile across
+        // Q4_K up to 704 tokens: the super-blocks of a 32 x 32 tile across
         // the waves of one workgroup (k_gemm_ks). N = 3584, K = 1024: M = 64
         // 4.2 against 7.5 us, 128 5.2 / 7.4, 256 6.8 / 9.7, 384 8.7 / 11.4,
-        // 512 10.1 / 10.4 (k_gemm_r); 768 14.2 / 13.8.
-        if (type == 12 && m <= 512) {
+        // 512 10.1 / 10.4 (k_gemm_r), 640 12.4 / 13.7; 768 14.7 / 14.1,
+        // 1024 18.4 / 15.5, 2048 34 / 29.
+        if (type == 12 && m <= 704) {
             // terms in the activations' LDS once the tiles outnumber three
             // workgroups per CU (N = 3584, K = 1024: M = 512 10.1 -> 9.6 us,
             // 256 6.77 -> 6.67; M = 128 keeps the separate arrays, 5.17

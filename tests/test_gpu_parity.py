@@ -182,7 +182,8 @@ GEMM_SHAPES = [
     (12, 3584, 1024, 512), (12, 3584, 1024, 128), (14, 1024, 3584, 512),    # config 3
     (13, 2048, 1024, 96), (13, 1024, 2048, 33),
     (12, 100, 768, 37), (13, 65, 256, 1), (14, 63, 512, 65), (14, 129, 1280, 7),
-    (12, 64, 256, 64), (12, 1, 512, 3),
+    (12, 64, 256, 64), (12, 1, 512, 3), (12, 1000, 512, 650),   # super-blocks across waves up to 704 tokens
+    (12, 2050, 512, 777),                                        # weight rows in registers, 32-token tiles
     # 64-row tiles for every type: 64-token tiles (at least 256 of them,
     # fewer than 192 128-token tiles, or more than 256 for Q5_K), else
     # 128-token tiles (Q4_K / Q5_K); the others run 32-row tiles with a
