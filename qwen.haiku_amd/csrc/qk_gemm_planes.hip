@@ -335,7 +335,7 @@ void k_gemm_planes(const uint8_t *__restrict__ wp, int64_t n, int nb, const uint
 // the running sums (which start at +0.0, so the first term enters
 // exactly): the reference's sequential `sum += term`. The round's
 // activations are staged by all threads.
-template <int TYPE, bool FUSED, int S>
+template <int TYPE, bool FUSED, int S, bool PF>
 __global__ __launch_bounds__(64 * S) void k_gemm_planes_ks(const uint8_t *__restrict__ wp, int64_t n, int nb,
                                                         const uint8_t *__restrict__ xq, int64_t m,
                                                         float *__restrict__ y) {
@@ -363,44 +363,56 @@ __global__ __launch_bounds__(64 * S) void k_gemm_planes_ks(const uint8_t *__rest
     for (int b = 0; b < VW; b++) sum[b] = 0.0f;
     const p16i zero = {0};
     const p16f zerof = {0.0f};
-    for (int r = 0; r < nb; r += S) {
+    // PF (one workgroup per CU, the rounds latency-bound): a round's
+    // operands are loaded during the round before, the activations once the
+    // previous ones are staged, this wave's planes once the previous MFMAs
+    // have read theirs (172 VGPRs for Q6_K). Else at the start of their
+    // round. Past the last super-block the planes read zeros and the
+    // activations repeat the last block.
+    struct A8 { uint4 q0, q1; uint32_t bp, d; };
+    struct Ops { p4i bq[16]; p8h bmn; uint32_t scw[2]; A8 ar[4]; };
+    auto load_w = [&](Ops &o, int r) {
         const int sb = r + wave;
-        const bool act = sb < nb;                      // wave-uniform
-        // this wave's operands (past the last super-block: zeros)
-        p4i bq[16];
-        p8h bmn;
 #pragma unroll
         for (int q = 0; q < 16; q++) {
             const auto v = __builtin_amdgcn_raw_buffer_load_b128(wr, 16 * lane, sb * CH + 1024 * q, 0);
-            bq[q] = p4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+            o.bq[q] = p4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
         }
-        if (KQ) bmn = __builtin_bit_cast(p8h, __builtin_amdgcn_raw_buffer_load_b128(wr, 16 * lane, sb * CH + PL_PLANES, 0));
+        if (KQ) o.bmn = __builtin_bit_cast(p8h, __builtin_amdgcn_raw_buffer_load_b128(wr, 16 * lane, sb * CH + PL_PLANES, 0));
         const auto sc = __builtin_amdgcn_raw_buffer_load_b64(wr, 8 * col, sb * CH + pl_scal_off(TYPE), 0);
-        const float wd = __uint_as_float(sc[0]), wdm = __uint_as_float(sc[1]);
-        // the round's activations
-        struct A8 { uint4 q0, q1; uint32_t bp, d; } ar[4];
+        o.scw[0] = sc[0], o.scw[1] = sc[1];
+    };
+    auto load_a = [&](Ops &o, int r) {
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int sq = r + q;
-            const int o = at * nb * Q8K_BYTES + (sq < nb ? sq : nb - 1) * Q8K_BYTES;
-            ar[q].q0 = bl128(xr, o + 4 + 32 * ae);
-            ar[q].q1 = bl128(xr, o + 20 + 32 * ae);
-            if (KQ) ar[q].bp = bl32(xr, o + 260 + 4 * ae);
-            ar[q].d = bl32(xr, o);
+            const int of = at * nb * Q8K_BYTES + (sq < nb ? sq : nb - 1) * Q8K_BYTES;
+            o.ar[q].q0 = bl128(xr, of + 4 + 32 * ae);
+            o.ar[q].q1 = bl128(xr, of + 20 + 32 * ae);
+            if (KQ) o.ar[q].bp = bl32(xr, of + 260 + 4 * ae);
+            o.ar[q].d = bl32(xr, of);
         }
+    };
+    // round r from the operands in o, which it reloads for round r + S
+    auto round = [&](Ops &o, int r) __attribute__((always_inline)) {
+        const int sb = r + wave;
+        const bool act = sb < nb;                      // wave-uniform
+        const float wd = __uint_as_float(o.scw[0]), wdm = __uint_as_float(o.scw[1]);
         if (r > 0) pl_barrier();                       // the previous round's reads of st done
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int qq = q;
-            *(QK_LDS uint4 *)&sa[qq][at][32 * ae] = ar[q].q0;
-            *(QK_LDS uint4 *)&sa[qq][at][32 * ae + 16] = ar[q].q1;
+            *(QK_LDS uint4 *)&sa[qq][at][32 * ae] = o.ar[q].q0;
+            *(QK_LDS uint4 *)&sa[qq][at][32 * ae + 16] = o.ar[q].q1;
             if (KQ) {
                 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-                const h2 v = {(_Float16)(int16_t)(ar[q].bp & 0xffffu), (_Float16)(int16_t)(ar[q].bp >> 16)};
+                const h2 v = {(_Float16)(int16_t)(o.ar[q].bp & 0xffffu), (_Float16)(int16_t)(o.ar[q].bp >> 16)};
                 *(QK_LDS h2 *)&sbs[qq][at][2 * ae] = v;
             }
-            syd[qq][at] = __uint_as_float(ar[q].d);   // the token's eight threads store the same d
+            syd[qq][at] = __uint_as_float(o.ar[q].d); // the token's eight threads store the same d
         }
+        const bool more = r + S < nb;                  // uniform
+        if (more) load_a(o, r + S);
         pl_barrier();
         p16i a0 = zero, a1 = zero;
         p16f mf = zerof;
@@ -408,13 +420,13 @@ __global__ __launch_bounds__(64 * S) void k_gemm_planes_ks(const uint8_t *__rest
         if (act) {
             if (KQ) {
                 const p8h amv = *(const QK_LDS p8h *)&sbs[wave][col][8 * h];
-                mf = __builtin_amdgcn_mfma_f32_32x32x16_f16(amv, bmn, zerof, 0, 0, 0);
+                mf = __builtin_amdgcn_mfma_f32_32x32x16_f16(amv, o.bmn, zerof, 0, 0, 0);
             }
 #pragma unroll
             for (int s = 0; s < 8; s++) {
                 const p4i av = *(const QK_LDS p4i *)&sa[wave][col][32 * s + 16 * h];
-                a0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bq[2 * s], a0, 0, 0, 0);
-                a1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bq[2 * s + 1], a1, 0, 0, 0);
+                a0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, o.bq[2 * s], a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, o.bq[2 * s + 1], a1, 0, 0, 0);
             }
 #pragma unroll
             for (int q = 0; q < 4; q++) {
@@ -422,6 +434,7 @@ __global__ __launch_bounds__(64 * S) void k_gemm_planes_ks(const uint8_t *__rest
                 yv[4 * q] = y4.x, yv[4 * q + 1] = y4.y, yv[4 * q + 2] = y4.z, yv[4 * q + 3] = y4.w;
             }
         }
+        if (more) load_w(o, r + S);
         if (act) {
 #pragma unroll
             for (int v = 0; v < 16; v++) {
@@ -446,6 +459,97 @@ __global__ __launch_bounds__(64 * S) void k_gemm_planes_ks(const uint8_t *__rest
 #pragma unroll
             for (int b = 0; b < VW; b++) sum[b] = __fadd_rn(sum[b], st[q][VW * wave + b][lane]);
         }
+    };
+    if constexpr (PF) {
+        Ops o;
+        load_w(o, 0);
+        load_a(o, 0);
+        for (int r = 0; r < nb; r += S) round(o, r);
+    } else {
+        for (int r = 0; r < nb; r += S) {
+            const int sb = r + wave;
+            const bool act = sb < nb;                      // wave-uniform
+            // this wave's operands (past the last super-block: zeros)
+            p4i bq[16];
+            p8h bmn;
+    #pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const auto v = __builtin_amdgcn_raw_buffer_load_b128(wr, 16 * lane, sb * CH + 1024 * q, 0);
+                bq[q] = p4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+            }
+            if (KQ) bmn = __builtin_bit_cast(p8h, __builtin_amdgcn_raw_buffer_load_b128(wr, 16 * lane, sb * CH + PL_PLANES, 0));
+            const auto sc = __builtin_amdgcn_raw_buffer_load_b64(wr, 8 * col, sb * CH + pl_scal_off(TYPE), 0);
+            const float wd = __uint_as_float(sc[0]), wdm = __uint_as_float(sc[1]);
+            // the round's activations
+            struct A8 { uint4 q0, q1; uint32_t bp, d; } ar[4];
+    #pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int sq = r + q;
+                const int o = at * nb * Q8K_BYTES + (sq < nb ? sq : nb - 1) * Q8K_BYTES;
+                ar[q].q0 = bl128(xr, o + 4 + 32 * ae);
+                ar[q].q1 = bl128(xr, o + 20 + 32 * ae);
+                if (KQ) ar[q].bp = bl32(xr, o + 260 + 4 * ae);
+                ar[q].d = bl32(xr, o);
+            }
+            if (r > 0) pl_barrier();                       // the previous round's reads of st done
+    #pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int qq = q;
+                *(QK_LDS uint4 *)&sa[qq][at][32 * ae] = ar[q].q0;
+                *(QK_LDS uint4 *)&sa[qq][at][32 * ae + 16] = ar[q].q1;
+                if (KQ) {
+                    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                    const h2 v = {(_Float16)(int16_t)(ar[q].bp & 0xffffu), (_Float16)(int16_t)(ar[q].bp >> 16)};
+                    *(QK_LDS h2 *)&sbs[qq][at][2 * ae] = v;
+                }
+                syd[qq][at] = __uint_as_float(ar[q].d);   // the token's eight threads store the same d
+            }
+            pl_barrier();
+            p16i a0 = zero, a1 = zero;
+            p16f mf = zerof;
+            float yv[16];
+            if (act) {
+                if (KQ) {
+                    const p8h amv = *(const QK_LDS p8h *)&sbs[wave][col][8 * h];
+                    mf = __builtin_amdgcn_mfma_f32_32x32x16_f16(amv, bmn, zerof, 0, 0, 0);
+                }
+    #pragma unroll
+                for (int s = 0; s < 8; s++) {
+                    const p4i av = *(const QK_LDS p4i *)&sa[wave][col][32 * s + 16 * h];
+                    a0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bq[2 * s], a0, 0, 0, 0);
+                    a1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bq[2 * s + 1], a1, 0, 0, 0);
+                }
+    #pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 y4 = *(const QK_LDS float4 *)&syd[wave][8 * q + 4 * h];
+                    yv[4 * q] = y4.x, yv[4 * q + 1] = y4.y, yv[4 * q + 2] = y4.z, yv[4 * q + 3] = y4.w;
+                }
+            }
+            if (act) {
+    #pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const float yd = yv[v];
+                    const int32_t is = a0[v] + 128 * a1[v];
+                    float term;
+                    if (KQ) {
+                        const float d = __fmul_rn(yd, wd);
+                        const float dmin = __fmul_rn(yd, wdm);
+                        const float pm = __fmul_rn(dmin, mf[v]);
+                        term = FUSED ? __builtin_fmaf(d, (float)is, -pm) : __fsub_rn(__fmul_rn(d, (float)is), pm);
+                    } else {
+                        term = __fmul_rn(__fmul_rn(wd, yd), (float)is);
+                    }
+                    st[wave][v][lane] = term;
+                }
+            }
+            pl_barrier();
+    #pragma unroll
+            for (int q = 0; q < S; q++) {
+                if (r + q >= nb) break;                    // uniform
+    #pragma unroll
+                for (int b = 0; b < VW; b++) sum[b] = __fadd_rn(sum[b], st[q][VW * wave + b][lane]);
+            }
+        }
     }
     const int64_t row = g * 32 + col;
     if (row < n) {
@@ -457,21 +561,26 @@ __global__ __launch_bounds__(64 * S) void k_gemm_planes_ks(const uint8_t *__rest
     }
 }
 
-template <int TYPE, int S>
-static void launch_planes_ks(const uint8_t *wp, int64_t n, int nb, const uint8_t *xq, int64_t m, float *y, int fused,
-                             hipStream_t s) {
-    const dim3 grid((unsigned)((n + 31) / 32), (unsigned)((m + 31) / 32));
-    if (fused) hipLaunchKernelGGL((k_gemm_planes_ks<TYPE, true, S>), grid, dim3(64 * S), 0, s, wp, n, nb, xq, m, y);
-    else hipLaunchKernelGGL((k_gemm_planes_ks<TYPE, false, S>), grid, dim3(64 * S), 0, s, wp, n, nb, xq, m, y);
-}
-
 template <int TYPE>
 static void launch_planes(const uint8_t *wp, int64_t n, int nb, const uint8_t *xq, int64_t m, float *y, int fused,
                           bool ks, hipStream_t s) {
     if (ks) {
+        // Q6_K: operands a round ahead when the tiles fit one workgroup per
+        // CU (1024 x 3584: M = 128 11.3 -> 10.4 us; Q5_K and more tiles
+        // were slower with it)
         const dim3 grid((unsigned)((n + 31) / 32), (unsigned)((m + 31) / 32));
-        if (fused) hipLaunchKernelGGL((k_gemm_planes_ks<TYPE, true, 4>), grid, dim3(256), 0, s, wp, n, nb, xq, m, y);
-        else hipLaunchKernelGGL((k_gemm_planes_ks<TYPE, false, 4>), grid, dim3(256), 0, s, wp, n, nb, xq, m, y);
+        const bool pf = (uint64_t)grid.x * grid.y <= 256;
+#define QK_PLKS(F, P) hipLaunchKernelGGL((k_gemm_planes_ks<TYPE, F, 4, P>), grid, dim3(256), 0, s, wp, n, nb, xq, m, y)
+        if constexpr (TYPE == 14) {
+            if (pf) {
+                if (fused) QK_PLKS(true, true);
+                else QK_PLKS(false, true);
+                return;
+            }
+        }
+        if (fused) QK_PLKS(true, false);
+        else QK_PLKS(false, false);
+#undef QK_PLKS
     } else {
         const dim3 grid((unsigned)(((n + 31) / 32 + 3) / 4), (unsigned)((m + 63) / 64));
         if (fused) hipLaunchKernelGGL((k_gemm_planes<TYPE, true, 2>), grid, dim3(256), 0, s, wp, n, nb, xq, m, y);
